@@ -1,0 +1,184 @@
+"""Full-sequence chunked causal FLARE forward on MI355X.
+
+Drop-in for ``flare_autoregressive_triton`` / ``AutoRegressiveFLARE``
+(``causal_flare/autoregressive/training.py:731-905, 4921-4932``): same
+signature, defaults, assertions and return arity.  The three phases run as
+HIP kernels from ``libflare_mi355x.so``:
+
+    flare_chunk_prepare -> flare_chunk_prefix -> flare_chunk_output
+
+(reference kernels flare_chunk_prepare :914, flare_chunk_prefix :1021,
+flare_chunk_decoder_lse :1106 + flare_chunk_fwd :1189).
+
+The backward pass is not part of this build; calling ``.backward()`` through
+the output raises ``NotImplementedError``.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.autograd as autograd
+
+from .. import _lib
+from .._common import (
+    _PhaseTimer,
+    _compute_dtype,
+    _normalize_input_precision,
+    _refresh_profile_totals,
+    _require_gpu,
+    _resolve_attn_scale,
+)
+from .._reference_utils import resolve_flare_causal_decode_inputs
+
+
+def _resolve_chunk_size(chunk_size, B, N, H, M, Dv, validate_only=False) -> tuple[int, int]:
+    """(validated chunk_size, kernel chunk length).
+
+    The reference's default chunk is 64 (training.py:328-337) and must be a
+    multiple of 16 (:344).  Chunk length only changes fp32 rounding, so when
+    neither ``chunk_size`` nor FLARE_CHUNK_SIZE is given the library's own
+    policy (long chunks, ~2048 workgroups) is used.
+    """
+    explicit = chunk_size
+    if explicit is None:
+        env = os.environ.get("FLARE_CHUNK_SIZE", "")
+        explicit = int(env) if env else None
+    requested = 64 if explicit is None else int(explicit)
+    assert requested % 16 == 0, f"CHUNK_SIZE must be divisible by 16. Got CHUNK_SIZE={requested}."
+    if validate_only:
+        return requested, requested
+    if explicit is None:
+        return requested, int(_lib.lib().flare_ar_default_chunk(B, N, H, M, Dv))
+    return requested, requested
+
+
+def _decoder_args(Q, K, Q_dec, K_dec, separate_q, separate_k):
+    """C-ABI decoder pointers: None selects the encoder tensor (K for Q_dec, Q for K_dec)."""
+    qd = Q_dec if (separate_q and Q_dec is not K) else None
+    kd = K_dec if (separate_k and K_dec is not Q) else None
+    return qd, kd
+
+
+def _prep(t, dtype):
+    return None if t is None else t.to(dtype).contiguous()
+
+
+def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
+                        want_state=False, timings=None):
+    """Launch phases 1-3; returns (Y, final_state or None).  Inputs are validated by the caller."""
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    device = K.device
+    cdt = _compute_dtype(Q, K, V, qd, kd)
+    code = _lib.dtype_code(cdt)
+    q, k, v, qd, kd = (_prep(t, cdt) for t in (Q, K, V, qd, kd))
+    lib = _lib.lib()
+    stream = _lib.stream_of(device)
+    Y = torch.empty((B, N, H, Dv), device=device, dtype=out_dtype)
+    out_code = _lib.dtype_code(out_dtype)
+    m0 = d0 = u0 = None
+    if state is not None:
+        m0, d0, u0 = state["m"], state["d"], state["u"]
+    fin = None
+    if want_state:
+        fin = {
+            "m": torch.empty((B, H, M), device=device, dtype=torch.float32),
+            "d": torch.empty((B, H, M), device=device, dtype=torch.float32),
+            "u": torch.empty((B, H, M, Dv), device=device, dtype=torch.float32),
+        }
+    P = _lib.ptr
+    fin_ptrs = (P(fin["m"]), P(fin["d"]), P(fin["u"])) if fin else (None, None, None)
+    NC = (N + chunk - 1) // chunk
+    if timings is None:
+        nbytes = lib.flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk)
+        ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+        rc = lib.flare_ar_forward(P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv,
+                                  float(scale), chunk, P(m0), P(d0), P(u0), *fin_ptrs, P(Y),
+                                  out_code, P(ws), nbytes, stream)
+        _lib.check(rc, "flare_ar_forward")
+        return Y, fin
+    timer = _PhaseTimer(device, timings)
+    cmax = torch.empty((B * H, NC, M), device=device, dtype=torch.float32)
+    cden = torch.empty_like(cmax)
+    cnum = torch.empty((B * H, NC, M, Dv), device=device, dtype=torch.float32)
+    _lib.check(timer("flare_chunk_prepare", lambda: lib.flare_chunk_prepare(
+        P(q), P(k), P(v), code, B, N, H, M, Dk, Dv, float(scale), chunk, P(cmax), P(cden),
+        P(cnum), stream)), "flare_chunk_prepare")
+    _lib.check(timer("flare_chunk_prefix", lambda: lib.flare_chunk_prefix(
+        P(cmax), P(cden), P(cnum), B * H, NC, M, Dv, P(m0), P(d0), P(u0), *fin_ptrs, stream)),
+        "flare_chunk_prefix")
+    _lib.check(timer("flare_chunk_fwd", lambda: lib.flare_chunk_output(
+        P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv, float(scale), chunk, P(cmax),
+        P(cden), P(cnum), P(Y), out_code, None, stream)), "flare_chunk_fwd")
+    return Y, fin
+
+
+class AutoRegressiveFLARE(autograd.Function):
+    """Forward of causal FLARE (reference ``training.py:731-905``)."""
+
+    @staticmethod
+    def forward(ctx, Q, K, V, scale=None, chunk_size=None, input_precision=None, profile=False,
+                Q_dec=None, K_dec=None):
+        assert Q.dim() == 3 and K.dim() == 4 and V.dim() == 4, (
+            "Q, K, V must be 3D and 4D tensors respectively "
+            f"got Q.dim()={Q.dim()}, K.dim()={K.dim()}, V.dim()={V.dim()}"
+        )
+        assert K.shape[:3] == V.shape[:3], (
+            f"Expected K/V to agree on [B, N, H]. Got K.shape={K.shape} and V.shape={V.shape}"
+        )
+        assert Q.size(0) == K.size(2) and Q.size(2) == K.size(3), (
+            f"Expected Q [H, M, D_k] and K [B, N, H, D_k]. Got Q.shape={Q.shape} and K.shape={K.shape}"
+        )
+        H, M, D_score = Q.shape
+        B, N, _, D_value = V.shape
+        Q_dec_r, K_dec_r, sep_q, sep_k, shared = resolve_flare_causal_decode_inputs(Q, K, Q_dec, K_dec)
+        scale = _resolve_attn_scale(scale, D_score)
+        _normalize_input_precision(input_precision)
+        assert M % 16 == 0, f"M must be divisible by 16. Got M={M}."
+        assert D_score % 16 == 0, f"score_head_dim must be divisible by 16. Got score_head_dim={D_score}."
+        assert D_value % 16 == 0, f"value_head_dim must be divisible by 16. Got value_head_dim={D_value}."
+        _resolve_chunk_size(chunk_size, B, N, H, M, D_value, validate_only=True)
+        _require_gpu("flare_autoregressive_triton", Q, K, V, Q_dec, K_dec)
+        # Output in the compute dtype of K (training.py:322-324, 724-727).
+        out_dtype = K.dtype if K.dtype in (torch.bfloat16, torch.float16) else torch.float32
+        profile_data = {"forward": {}, "backward": {}} if profile else None
+        if N == 0:
+            Y = torch.empty((B, 0, H, D_value), device=K.device, dtype=out_dtype)
+        else:
+            _, chunk = _resolve_chunk_size(chunk_size, B, N, H, M, D_value)
+            qd, kd = (None, None) if shared else _decoder_args(Q, K, Q_dec_r, K_dec_r, sep_q, sep_k)
+            Y, _ = run_chunked_forward(
+                Q, K, V, qd, kd, scale=scale, chunk=chunk, out_dtype=out_dtype,
+                timings=profile_data["forward"] if profile else None,
+            )
+        if profile:
+            _refresh_profile_totals(profile_data)
+            return Y, profile_data
+        return Y
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(
+            "The MI355X causal FLARE build implements the forward pass only; backward is not available."
+        )
+
+
+def flare_autoregressive_triton(
+    Q: torch.Tensor,
+    K: torch.Tensor,
+    V: torch.Tensor,
+    scale: float | None = None,
+    chunk_size: int | None = None,
+    input_precision: str | None = None,
+    profile: bool = False,
+    Q_dec: torch.Tensor | None = None,
+    K_dec: torch.Tensor | None = None,
+):
+    """Causal FLARE forward. Q [H,M,D], K/V [B,N,H,D] -> Y [B,N,H,D] (reference training.py:4921)."""
+    return AutoRegressiveFLARE.apply(Q, K, V, scale, chunk_size, input_precision, profile, Q_dec, K_dec)
+
+
+# Names the reference keeps for downstream callers (training.py:4935-4937).
+ChunkedFLARE = AutoRegressiveFLARE
+flare_chunk_triton = flare_autoregressive_triton

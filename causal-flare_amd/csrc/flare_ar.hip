@@ -1,0 +1,513 @@
+// flare_ar.hip -- chunked causal FLARE forward / prefill (scalar-fp32 kernels).
+//
+// Three phases, the structure of causal_flare/autoregressive/training.py:
+//   1. chunk_prepare_kernel  per-chunk (max, den, num) summaries   (:914-1018)
+//   2. chunk_prefix_kernel   exclusive scan over chunks + initial / final
+//                            state merges                          (:1021-1103,
+//                            inference.py:753-814)
+//   3. chunk_output_kernel   tokenwise replay from the chunk prefix and the
+//                            latent softmax readout                 (:1106-1392)
+// All arithmetic is fp32 on CUDA-core-equivalent VALU lanes; inputs may be
+// fp32, bf16 or fp16.  These kernels serve every dtype and shape; the bf16/fp16
+// MFMA kernels in flare_ar_mfma.hip take over the shapes they support.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "flare_common.h"
+#include "flare_internal.h"
+
+namespace flare {
+
+constexpr int kNT = 256;        // threads per workgroup (4 wavefronts)
+constexpr int kPrepTT = 16;     // tokens per LDS tile in the prepare kernel
+constexpr int kPrepMT = 64;     // latents per prepare workgroup
+constexpr int kPrepCols = 64;   // max value columns per prepare thread (Dv <= 256)
+
+__device__ __forceinline__ void store_out(void* Y, size_t idx, float v, int out_dtype) {
+    if (out_dtype == FLARE_BF16) reinterpret_cast<__hip_bfloat16*>(Y)[idx] = __float2bfloat16(v);
+    else if (out_dtype == FLARE_F16) reinterpret_cast<__half*>(Y)[idx] = __float2half(v);
+    else reinterpret_cast<float*>(Y)[idx] = v;
+}
+
+// ---------------------------------------------------------------------------
+// Phase 1.  grid = (NC, B*H, ceil(M/64)), 256 threads.  Thread (ml, g) owns
+// latent m0+ml and value columns g, g+4, g+8, ...
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, int N, int H,
+    int M, int Dk, int Dv, float scale, int chunk, float* __restrict__ cmax,
+    float* __restrict__ cden, float* __restrict__ cnum) {
+    extern __shared__ float smem[];
+    float* k_tile = smem;                       // [TT][Dk]
+    float* v_tile = k_tile + kPrepTT * Dk;      // [TT][Dv]
+    float* s_tile = v_tile + kPrepTT * Dv;      // [TT][64]
+
+    const int c = blockIdx.x, bh = blockIdx.y, mbase = blockIdx.z * kPrepMT;
+    const int NC = gridDim.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, ml = tid & 63, g = tid >> 6;
+    const int m = mbase + ml;
+    const T* q_h = Q + (size_t)h * M * Dk;
+
+    float mx = kNegInf, den = 0.0f;
+    float num[kPrepCols];
+#pragma unroll
+    for (int i = 0; i < kPrepCols; ++i) num[i] = 0.0f;
+
+    const int t_begin = c * chunk;
+    const int t_end = min(N, t_begin + chunk);
+    for (int t0 = t_begin; t0 < t_end; t0 += kPrepTT) {
+        const int nt = min(kPrepTT, t_end - t0);
+        for (int e = tid; e < kPrepTT * Dk; e += kNT) {
+            const int i = e / Dk, d = e % Dk;
+            k_tile[e] = i < nt ? to_f32(K[(((size_t)b * N + t0 + i) * H + h) * Dk + d]) : 0.0f;
+        }
+        for (int e = tid; e < kPrepTT * Dv; e += kNT) {
+            const int i = e / Dv, d = e % Dv;
+            v_tile[e] = i < nt ? to_f32(V[(((size_t)b * N + t0 + i) * H + h) * Dv + d]) : 0.0f;
+        }
+        __syncthreads();
+        for (int p = tid; p < kPrepTT * kPrepMT; p += kNT) {
+            const int i = p / kPrepMT, mm = mbase + p % kPrepMT;
+            float s = kNegInf;
+            if (i < nt && mm < M) {
+                const T* qrow = q_h + (size_t)mm * Dk;
+                const float* kr = k_tile + i * Dk;
+                float acc = 0.0f;
+                for (int d = 0; d < Dk; ++d) acc += kr[d] * to_f32(qrow[d]);
+                s = acc * scale;
+            }
+            s_tile[p] = s;
+        }
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+            const float s = s_tile[i * kPrepMT + ml];
+            const float m_new = fmaxf(mx, s);
+            const float r = __expf(mx - m_new);     // mx = -inf on the first token -> 0
+            const float e = __expf(s - m_new);
+            den = den * r + e;
+            const float* vr = v_tile + i * Dv;
+#pragma unroll
+            for (int k = 0; k < kPrepCols; ++k) {
+                const int col = g + 4 * k;
+                if (col < Dv) num[k] = num[k] * r + e * vr[col];
+            }
+            mx = m_new;
+        }
+        __syncthreads();
+    }
+    if (m < M) {
+        const size_t sidx = ((size_t)bh * NC + c) * M + m;
+        if (g == 0) {
+            cmax[sidx] = mx;
+            cden[sidx] = den;
+        }
+        float* nrow = cnum + sidx * Dv;
+#pragma unroll
+        for (int k = 0; k < kPrepCols; ++k) {
+            const int col = g + 4 * k;
+            if (col < Dv) nrow[col] = num[k];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Phase 2.  grid = B*H*M workgroups of one wavefront; lane owns value columns
+// lane, lane+64, ... (Dv <= 256).  Summaries are overwritten in place by the
+// exclusive prefix; the next chunk's summary is loaded before the current
+// merge so the serial chain does not wait on memory.
+// ---------------------------------------------------------------------------
+constexpr int kScanCols = 4;
+
+__global__ __launch_bounds__(64) void chunk_prefix_kernel(
+    float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum, int NC, int M,
+    int Dv, const float* __restrict__ m0, const float* __restrict__ d0,
+    const float* __restrict__ u0, float* __restrict__ m_fin, float* __restrict__ d_fin,
+    float* __restrict__ u_fin) {
+    const int row = blockIdx.x;  // bh * M + m
+    const int bh = row / M, m = row % M;
+    const int lane = threadIdx.x;
+    float mc = m0 ? m0[row] : kNegInf;
+    float dc = d0 ? d0[row] : 0.0f;
+    float uc[kScanCols];
+#pragma unroll
+    for (int k = 0; k < kScanCols; ++k) {
+        const int col = lane + 64 * k;
+        uc[k] = (u0 && col < Dv) ? u0[(size_t)row * Dv + col] : 0.0f;
+    }
+    auto sidx = [&](int c) { return ((size_t)bh * NC + c) * M + m; };
+    float nm = cmax[sidx(0)], nd = cden[sidx(0)];
+    float nu[kScanCols];
+#pragma unroll
+    for (int k = 0; k < kScanCols; ++k) {
+        const int col = lane + 64 * k;
+        nu[k] = col < Dv ? cnum[sidx(0) * Dv + col] : 0.0f;
+    }
+    for (int c = 0; c < NC; ++c) {
+        const float cm = nm, cd = nd;
+        float cu[kScanCols];
+#pragma unroll
+        for (int k = 0; k < kScanCols; ++k) cu[k] = nu[k];
+        if (c + 1 < NC) {
+            nm = cmax[sidx(c + 1)];
+            nd = cden[sidx(c + 1)];
+#pragma unroll
+            for (int k = 0; k < kScanCols; ++k) {
+                const int col = lane + 64 * k;
+                nu[k] = col < Dv ? cnum[sidx(c + 1) * Dv + col] : 0.0f;
+            }
+        }
+        if (lane == 0) {
+            cmax[sidx(c)] = mc;
+            cden[sidx(c)] = dc;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanCols; ++k) {
+            const int col = lane + 64 * k;
+            if (col < Dv) cnum[sidx(c) * Dv + col] = uc[k];
+        }
+        const MergeScales ms = merge_scales(mc, cm);
+        dc = dc * ms.sa + cd * ms.sb;
+#pragma unroll
+        for (int k = 0; k < kScanCols; ++k) uc[k] = uc[k] * ms.sa + cu[k] * ms.sb;
+        mc = ms.m_new;
+    }
+    if (m_fin) {
+        if (lane == 0) {
+            m_fin[row] = mc;
+            d_fin[row] = dc;
+        }
+#pragma unroll
+        for (int k = 0; k < kScanCols; ++k) {
+            const int col = lane + 64 * k;
+            if (col < Dv) u_fin[(size_t)row * Dv + col] = uc[k];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Phase 3.  grid = (NC, B*H, Dv/DT), 256 threads.  Thread (col, rg) owns the
+// numerator entries u[m][dt0+col] for m = rg, rg+R, ... (R = 256/DT) in
+// registers; per-latent max/den live in LDS.  Tokens are processed in tiles
+// of TT: scores and decoder log-sum-exps for the tile first, then the
+// tokenwise recurrence and the readout, two barriers per token.
+// ---------------------------------------------------------------------------
+struct OutSmem {
+    int TT, Dk, DT, M, R;
+    bool shared;
+    __host__ __device__ size_t floats() const {
+        return (size_t)TT * Dk * (shared ? 1 : 2) + (size_t)TT * DT + (size_t)TT * M * (shared ? 1 : 2) +
+               (size_t)5 * M + (size_t)R * DT + TT + 8;
+    }
+};
+
+template <typename T, int ROWS>
+__global__ __launch_bounds__(kNT) void chunk_output_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    const T* __restrict__ Qdec, const T* __restrict__ Kdec, int N, int H, int M, int Dk, int Dv,
+    int DT, int TT, float scale, int chunk, bool shared, const float* __restrict__ pmax,
+    const float* __restrict__ pden, const float* __restrict__ pnum, void* __restrict__ Y,
+    int out_dtype, float* __restrict__ lse_dec) {
+    extern __shared__ float smem[];
+    const int R = kNT / DT;
+    float* k_tile = smem;                                   // [TT][Dk]
+    float* qd_tile = k_tile + TT * Dk;                      // [TT][Dk] (separate decoder only)
+    float* v_tile = qd_tile + (shared ? 0 : TT * Dk);       // [TT][DT]
+    float* s_tile = v_tile + TT * DT;                       // [TT][M]
+    float* a_tile = s_tile + TT * M;                        // [TT][M] (separate decoder only)
+    float* mstate = a_tile + (shared ? 0 : TT * M);         // [M]
+    float* dstate = mstate + M;
+    float* gam = dstate + M;
+    float* eta = gam + M;
+    float* wts = eta + M;
+    float* ypart = wts + M;                                 // [R][DT]
+    float* lse = ypart + R * DT;                            // [TT]
+
+    const int c = blockIdx.x, bh = blockIdx.y, dt0 = blockIdx.z * DT;
+    const int NC = gridDim.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, col = tid % DT, rg = tid / DT;
+    const T* q_h = Q + (size_t)h * M * Dk;
+    const T* kd_h = shared ? q_h : Kdec + (size_t)h * M * Dk;
+
+    const size_t pbase = ((size_t)bh * NC + c) * M;
+    for (int m = tid; m < M; m += kNT) {
+        mstate[m] = pmax[pbase + m];
+        dstate[m] = pden[pbase + m];
+    }
+    float U[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int m = rg + R * r;
+        U[r] = m < M ? pnum[(pbase + m) * Dv + dt0 + col] : 0.0f;
+    }
+
+    const int t_begin = c * chunk;
+    const int t_end = min(N, t_begin + chunk);
+    for (int t0 = t_begin; t0 < t_end; t0 += TT) {
+        const int nt = min(TT, t_end - t0);
+        __syncthreads();
+        for (int e = tid; e < TT * Dk; e += kNT) {
+            const int i = e / Dk, d = e % Dk;
+            const size_t gi = (((size_t)b * N + t0 + i) * H + h) * Dk + d;
+            k_tile[e] = i < nt ? to_f32(K[gi]) : 0.0f;
+            if (!shared) qd_tile[e] = i < nt ? to_f32(Qdec[gi]) : 0.0f;
+        }
+        for (int e = tid; e < TT * DT; e += kNT) {
+            const int i = e / DT, d = e % DT;
+            v_tile[e] = i < nt ? to_f32(V[(((size_t)b * N + t0 + i) * H + h) * Dv + dt0 + d]) : 0.0f;
+        }
+        __syncthreads();
+        for (int p = tid; p < nt * M; p += kNT) {
+            const int i = p / M, m = p % M;
+            const T* qrow = q_h + (size_t)m * Dk;
+            const float* kr = k_tile + i * Dk;
+            float acc = 0.0f;
+            for (int d = 0; d < Dk; ++d) acc += kr[d] * to_f32(qrow[d]);
+            s_tile[p] = acc * scale;
+            if (!shared) {
+                const T* krow = kd_h + (size_t)m * Dk;
+                const float* qr = qd_tile + i * Dk;
+                float acc2 = 0.0f;
+                for (int d = 0; d < Dk; ++d) acc2 += qr[d] * to_f32(krow[d]);
+                a_tile[p] = acc2 * scale;
+            }
+        }
+        __syncthreads();
+        {   // decoder log-sum-exp per token: wavefront w handles tokens w, w+4, ...
+            const int w = tid >> 6, lane = tid & 63;
+            const float* asrc = shared ? s_tile : a_tile;
+            for (int i = w; i < nt; i += kNT / 64) {
+                float mxv = kNegInf;
+                for (int m = lane; m < M; m += 64) mxv = fmaxf(mxv, asrc[i * M + m]);
+                mxv = wave_max(mxv);
+                float sm = 0.0f;
+                for (int m = lane; m < M; m += 64) sm += __expf(asrc[i * M + m] - mxv);
+                sm = wave_sum(sm);
+                if (lane == 0) lse[i] = mxv + __logf(sm);
+            }
+        }
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+            const float li = lse[i];
+            for (int m = tid; m < M; m += kNT) {
+                const float s = s_tile[i * M + m];
+                const MergeScales ts = token_scales(mstate[m], s);
+                const float dn = dstate[m] * ts.sa + ts.sb;
+                mstate[m] = ts.m_new;
+                dstate[m] = dn;
+                gam[m] = ts.sa;
+                eta[m] = ts.sb;
+                const float a = shared ? s : a_tile[i * M + m];
+                wts[m] = __expf(a - li) / (dn > 0.0f ? dn : 1.0f);
+            }
+            __syncthreads();
+            const float vc = v_tile[i * DT + col];
+            float yp = 0.0f;
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                const int m = rg + R * r;
+                if (m < M) {
+                    U[r] = U[r] * gam[m] + eta[m] * vc;
+                    yp += wts[m] * U[r];
+                }
+            }
+            ypart[rg * DT + col] = yp;
+            __syncthreads();
+            if (tid < DT) {
+                float y = 0.0f;
+                for (int g2 = 0; g2 < R; ++g2) y += ypart[g2 * DT + tid];
+                const int t = t0 + i;
+                store_out(Y, (((size_t)b * N + t) * H + h) * Dv + dt0 + tid, y, out_dtype);
+                if (lse_dec && dt0 == 0 && tid == 0) lse_dec[(size_t)bh * N + t] = li;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+static int launch_prepare(const void* Q, const void* K, const void* V, int dtype, int64_t B,
+                          int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                          int64_t chunk, float* cmax, float* cden, float* cnum,
+                          hipStream_t stream) {
+    FLARE_REQUIRE(Dv <= 4 * kPrepCols, "chunk_prepare: Dv=%lld exceeds %d", (long long)Dv, 4 * kPrepCols);
+    const int64_t NC = (N + chunk - 1) / chunk;
+    dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)((M + kPrepMT - 1) / kPrepMT));
+    const size_t sm = sizeof(float) * (kPrepTT * (Dk + Dv) + kPrepTT * kPrepMT);
+    FLARE_REQUIRE(sm <= 64 * 1024, "chunk_prepare: Dk+Dv too large for LDS");
+#define FLARE_PREP(TY)                                                                          \
+    hipLaunchKernelGGL(chunk_prepare_kernel<TY>, grid, dim3(kNT), sm, stream,                   \
+                       (const TY*)Q, (const TY*)K, (const TY*)V, (int)N, (int)H, (int)M,         \
+                       (int)Dk, (int)Dv, scale, (int)chunk, cmax, cden, cnum)
+    if (dtype == FLARE_BF16) FLARE_PREP(__hip_bfloat16);
+    else if (dtype == FLARE_F16) FLARE_PREP(__half);
+    else FLARE_PREP(float);
+#undef FLARE_PREP
+    return check_launch("chunk_prepare_kernel");
+}
+
+static int launch_prefix(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M,
+                         int64_t Dv, const float* m0, const float* d0, const float* u0,
+                         float* m_fin, float* d_fin, float* u_fin, hipStream_t stream) {
+    FLARE_REQUIRE(Dv <= 64 * kScanCols, "chunk_prefix: Dv=%lld exceeds %d", (long long)Dv, 64 * kScanCols);
+    FLARE_REQUIRE((m0 && d0 && u0) || (!m0 && !d0 && !u0), "chunk_prefix: give all of m0/d0/u0 or none");
+    FLARE_REQUIRE((m_fin && d_fin && u_fin) || (!m_fin && !d_fin && !u_fin),
+                  "chunk_prefix: give all of m_fin/d_fin/u_fin or none");
+    hipLaunchKernelGGL(chunk_prefix_kernel, dim3((unsigned)(BH * M)), dim3(64), 0, stream, cmax, cden,
+                       cnum, (int)NC, (int)M, (int)Dv, m0, d0, u0, m_fin, d_fin, u_fin);
+    return check_launch("chunk_prefix_kernel");
+}
+
+// Value-column tile: the largest power of two <= 128 dividing Dv with at most
+// 64 numerator registers per thread.
+static int pick_dt(int64_t M, int64_t Dv) {
+    for (int dt = 128; dt >= 16; dt >>= 1) {
+        if (Dv % dt) continue;
+        const int64_t rows = (M + (kNT / dt) - 1) / (kNT / dt);
+        if (rows <= 64) return dt;
+    }
+    return 0;
+}
+
+static int launch_output(const void* Q, const void* K, const void* V, const void* Qdec,
+                         const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                         int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
+                         const float* pden, const float* pnum, void* Y, int out_dtype,
+                         float* lse_dec, hipStream_t stream) {
+    const bool shared = Qdec == nullptr && Kdec == nullptr;
+    const int DT = pick_dt(M, Dv);
+    FLARE_REQUIRE(DT > 0, "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
+                  (long long)M, (long long)Dv);
+    const int R = kNT / DT;
+    const int64_t rows = (M + R - 1) / R;
+    int TT = 16;
+    OutSmem lay{TT, (int)Dk, DT, (int)M, R, shared};
+    while (lay.floats() * sizeof(float) > 64 * 1024 && lay.TT > 1) lay.TT /= 2;
+    FLARE_REQUIRE(lay.floats() * sizeof(float) <= 64 * 1024, "chunk_output: shape too large for LDS");
+    TT = lay.TT;
+    const int64_t NC = (N + chunk - 1) / chunk;
+    dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)(Dv / DT));
+    const size_t sm = lay.floats() * sizeof(float);
+    // Missing decoder tensors default to the encoder ones (K as Qdec, Q as Kdec).
+    const void* qd = Qdec ? Qdec : K;
+    const void* kd = Kdec ? Kdec : Q;
+#define FLARE_OUT(TY, RW)                                                                       \
+    hipLaunchKernelGGL((chunk_output_kernel<TY, RW>), grid, dim3(kNT), sm, stream, (const TY*)Q, \
+                       (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd, (int)N, (int)H,  \
+                       (int)M, (int)Dk, (int)Dv, DT, TT, scale, (int)chunk, shared, pmax, pden,   \
+                       pnum, Y, out_dtype, lse_dec)
+#define FLARE_OUT_ROWS(TY)                   \
+    if (rows <= 8) FLARE_OUT(TY, 8);         \
+    else if (rows <= 16) FLARE_OUT(TY, 16);  \
+    else if (rows <= 32) FLARE_OUT(TY, 32);  \
+    else FLARE_OUT(TY, 64);
+    if (dtype == FLARE_BF16) { FLARE_OUT_ROWS(__hip_bfloat16) }
+    else if (dtype == FLARE_F16) { FLARE_OUT_ROWS(__half) }
+    else { FLARE_OUT_ROWS(float) }
+#undef FLARE_OUT_ROWS
+#undef FLARE_OUT
+    return check_launch("chunk_output_kernel");
+}
+
+int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
+                          int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream) {
+    return launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, stream);
+}
+
+int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
+    // Enough chunks to give every CU several workgroups, each chunk a multiple
+    // of 64 tokens and at most 2048 long.
+    const int64_t BH = B * H;
+    int64_t target_chunks = (2048 + BH - 1) / BH;  // ~2048 workgroups in phases 1 and 3
+    int64_t c = (N + target_chunks - 1) / target_chunks;
+    c = ((c + 63) / 64) * 64;
+    if (c < 64) c = 64;
+    if (c > 2048) c = 2048;
+    return c;
+}
+
+}  // namespace flare
+
+using namespace flare;
+
+extern "C" {
+
+int flare_chunk_prepare(const void* Q, const void* K, const void* V, int dtype, int64_t B,
+                        int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                        int64_t chunk, float* chunk_max, float* chunk_den, float* chunk_num,
+                        void* stream) {
+    FLARE_REQUIRE(Q && K && V && chunk_max && chunk_den && chunk_num, "chunk_prepare: null pointer");
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0 && chunk > 0,
+                  "chunk_prepare: sizes must be positive");
+    return launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, chunk_max, chunk_den,
+                          chunk_num, (hipStream_t)stream);
+}
+
+int flare_chunk_prefix(float* chunk_max, float* chunk_den, float* chunk_num, int64_t BH,
+                       int64_t NC, int64_t M, int64_t Dv, const float* m0, const float* d0,
+                       const float* u0, float* m_fin, float* d_fin, float* u_fin, void* stream) {
+    FLARE_REQUIRE(chunk_max && chunk_den && chunk_num, "chunk_prefix: null pointer");
+    FLARE_REQUIRE(BH > 0 && NC > 0 && M > 0 && Dv > 0, "chunk_prefix: sizes must be positive");
+    return launch_prefix(chunk_max, chunk_den, chunk_num, BH, NC, M, Dv, m0, d0, u0, m_fin, d_fin,
+                         u_fin, (hipStream_t)stream);
+}
+
+int flare_chunk_output(const void* Q, const void* K, const void* V, const void* Qdec,
+                       const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                       int64_t Dk, int64_t Dv, float scale, int64_t chunk,
+                       const float* prefix_max, const float* prefix_den, const float* prefix_num,
+                       void* Y, int out_dtype, float* lse_dec, void* stream) {
+    FLARE_REQUIRE(Q && K && V && Y && prefix_max && prefix_den && prefix_num, "chunk_output: null pointer");
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0 && chunk > 0,
+                  "chunk_output: sizes must be positive");
+    return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, prefix_max,
+                         prefix_den, prefix_num, Y, out_dtype, lse_dec, (hipStream_t)stream);
+}
+
+int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
+    return default_chunk(B, N, H, M, Dv);
+}
+
+size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                       int64_t chunk) {
+    if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
+    const int64_t NC = (N + chunk - 1) / chunk;
+    const size_t per = (size_t)B * H * NC * M;
+    return sizeof(float) * (per * 2 + per * Dv) + 3 * 256;
+}
+
+int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
+                     const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                     const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                     void* Y, int out_dtype, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    FLARE_REQUIRE(Q && K && V && Y, "ar_forward: null pointer");
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0, "ar_forward: sizes must be positive");
+    if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
+    const size_t need = flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk);
+    if (!workspace || workspace_bytes < need) {
+        set_error("ar_forward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        return FLARE_ERR_WORKSPACE;
+    }
+    const int64_t NC = (N + chunk - 1) / chunk;
+    const size_t per = (size_t)B * H * NC * M;
+    char* ws = (char*)workspace;
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    float* cmax = (float*)ws;
+    float* cden = (float*)(ws + align(per * sizeof(float)));
+    float* cnum = (float*)(ws + 2 * align(per * sizeof(float)));
+    hipStream_t s = (hipStream_t)stream;
+    int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s);
+    if (rc) return rc;
+    rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
+    if (rc) return rc;
+    return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
+                         cnum, Y, out_dtype, nullptr, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,189 @@
+// flare_decode.hip -- one recurrent decode step of causal FLARE for every (b,h).
+//
+// Follows flare_recurrent_step_kernel (causal_flare/autoregressive/inference.py:358-489):
+//   s = scale * Q k                         (encoder scores, [M])
+//   (m, d, u) <- inf-safe update with (s, v) (in place, fp32)
+//   z = u / d_safe;  alpha = softmax_M(a);  y = sum_m alpha_m z_m
+// with a = s when the decoder shares the encoder weights.
+//
+// The step is HBM-bound: per (b,h) it reads and writes the fp32 state
+// (8M + 4*M*Dv bytes each way).  One 256-thread workgroup owns one (b,h), so
+// the per-latent scalars never leave the workgroup (no cross-workgroup race on
+// m/d); the numerator u is streamed with 16-byte loads/stores, consecutive
+// threads covering consecutive addresses of a row.
+#include "flare_common.h"
+
+namespace flare {
+
+constexpr int kDecNT = 256;
+constexpr int kDecBatchRows = 8;   // float4 rows loaded before any is stored
+
+__device__ __forceinline__ void store_out_dec(void* Y, size_t idx, float v, int out_dtype) {
+    if (out_dtype == FLARE_BF16) reinterpret_cast<__hip_bfloat16*>(Y)[idx] = __float2bfloat16(v);
+    else if (out_dtype == FLARE_F16) reinterpret_cast<__half*>(Y)[idx] = __float2half(v);
+    else reinterpret_cast<float*>(Y)[idx] = v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kDecNT) void decode_step_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    const T* __restrict__ Qdec, const T* __restrict__ Kdec, const int32_t* __restrict__ mask,
+    int H, int M, int Dk, int Dv, float scale, bool shared, float* __restrict__ mst,
+    float* __restrict__ dst, float* __restrict__ ust, void* __restrict__ Y, int out_dtype) {
+    extern __shared__ float smem[];
+    float* kv = smem;                 // [Dk]
+    float* qd = kv + Dk;              // [Dk]
+    float* vv = qd + Dk;              // [Dv]
+    float* av = vv + Dv;              // [M] decoder scores
+    float* gam = av + M;              // [M]
+    float* eta = gam + M;             // [M]
+    float* wts = eta + M;             // [M]
+    float* red = wts + M;             // [8]
+    float4* ypart = reinterpret_cast<float4*>(smem + ((2 * Dk + Dv + 4 * M + 8 + 3) & ~3));  // [RG][NT4]
+
+    const int bh = blockIdx.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x;
+    const bool valid = mask == nullptr || mask[b] != 0;
+    const size_t kvoff = (size_t)bh * Dk;
+
+    if (!valid) {
+        // s = -inf for every latent: gamma = 1, eta = 0, so the state is unchanged
+        // and y = 0 (inference.py:395-397, 476-478).
+        for (int j = tid; j < Dv; j += kDecNT) store_out_dec(Y, (size_t)bh * Dv + j, 0.0f, out_dtype);
+        return;
+    }
+    for (int j = tid; j < Dk; j += kDecNT) {
+        kv[j] = to_f32(K[kvoff + j]);
+        if (!shared) qd[j] = to_f32(Qdec[kvoff + j]);
+    }
+    for (int j = tid; j < Dv; j += kDecNT) vv[j] = to_f32(V[(size_t)bh * Dv + j]);
+    __syncthreads();
+
+    // Scores and the per-latent scalar update; thread-per-latent dot products
+    // (Q[h] is shared by every batch row and stays in L2).
+    const T* qh = Q + (size_t)h * M * Dk;
+    const T* kdh = shared ? qh : Kdec + (size_t)h * M * Dk;
+    float amax = kNegInf;
+    for (int m = tid; m < M; m += kDecNT) {
+        const T* qrow = qh + (size_t)m * Dk;
+        float acc = 0.0f;
+        for (int d = 0; d < Dk; ++d) acc += to_f32(qrow[d]) * kv[d];
+        const float s = acc * scale;
+        float a = s;
+        if (!shared) {
+            const T* krow = kdh + (size_t)m * Dk;
+            float acc2 = 0.0f;
+            for (int d = 0; d < Dk; ++d) acc2 += to_f32(krow[d]) * qd[d];
+            a = acc2 * scale;
+        }
+        const size_t si = (size_t)bh * M + m;
+        const MergeScales ts = token_scales(mst[si], s);
+        const float dn = dst[si] * ts.sa + ts.sb;
+        mst[si] = ts.m_new;
+        dst[si] = dn;
+        gam[m] = ts.sa;
+        eta[m] = ts.sb;
+        wts[m] = dn > 0.0f ? dn : 1.0f;   // d_safe, turned into weights below
+        av[m] = a;
+        amax = fmaxf(amax, a);
+    }
+    amax = block_max<kDecNT>(amax, red);
+    float asum = 0.0f;
+    for (int m = tid; m < M; m += kDecNT) asum += __expf(av[m] - amax);
+    asum = block_sum<kDecNT>(asum, red);
+    const float inv = 1.0f / asum;
+    for (int m = tid; m < M; m += kDecNT) wts[m] = __expf(av[m] - amax) * inv / wts[m];
+    __syncthreads();
+
+    // Numerator update and readout, 16 bytes per access.
+    const int D4 = Dv >> 2;
+    int NT4 = 1;
+    while (NT4 * 2 <= D4 && NT4 * 2 <= kDecNT) NT4 *= 2;
+    const int RG = kDecNT / NT4;
+    const int jt = tid % NT4, rg = tid / NT4;
+    float4* u4 = reinterpret_cast<float4*>(ust + (size_t)bh * M * Dv);
+    const float4* v4 = reinterpret_cast<const float4*>(vv);
+    for (int j0 = 0; j0 < D4; j0 += NT4) {
+        const int j4 = j0 + jt;
+        const bool act = j4 < D4;
+        float4 y4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (act) {
+            const float4 vj = v4[j4];
+            for (int mb = rg; mb < M; mb += RG * kDecBatchRows) {
+                float4 buf[kDecBatchRows];
+#pragma unroll
+                for (int r = 0; r < kDecBatchRows; ++r) {
+                    const int m = mb + r * RG;
+                    if (m < M) buf[r] = u4[(size_t)m * D4 + j4];
+                }
+#pragma unroll
+                for (int r = 0; r < kDecBatchRows; ++r) {
+                    const int m = mb + r * RG;
+                    if (m < M) {
+                        const float g = gam[m], e = eta[m], w = wts[m];
+                        float4 x = buf[r];
+                        x.x = x.x * g + e * vj.x;
+                        x.y = x.y * g + e * vj.y;
+                        x.z = x.z * g + e * vj.z;
+                        x.w = x.w * g + e * vj.w;
+                        u4[(size_t)m * D4 + j4] = x;
+                        y4.x += w * x.x;
+                        y4.y += w * x.y;
+                        y4.z += w * x.z;
+                        y4.w += w * x.w;
+                    }
+                }
+            }
+        }
+        ypart[rg * NT4 + jt] = y4;
+        __syncthreads();
+        if (tid < NT4 && j0 + tid < D4) {
+            float4 acc = ypart[tid];
+            for (int g2 = 1; g2 < RG; ++g2) {
+                const float4 p = ypart[g2 * NT4 + tid];
+                acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+            }
+            const size_t yo = (size_t)bh * Dv + 4 * (j0 + tid);
+            store_out_dec(Y, yo + 0, acc.x, out_dtype);
+            store_out_dec(Y, yo + 1, acc.y, out_dtype);
+            store_out_dec(Y, yo + 2, acc.z, out_dtype);
+            store_out_dec(Y, yo + 3, acc.w, out_dtype);
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace flare
+
+using namespace flare;
+
+extern "C" int flare_decode_step(const void* Q, const void* K, const void* V, const void* Qdec,
+                                 const void* Kdec, const int32_t* mask, int dtype, int64_t B,
+                                 int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                                 float* m, float* d, float* u, void* y, int out_dtype,
+                                 void* stream) {
+    FLARE_REQUIRE(Q && K && V && m && d && u && y, "decode_step: null pointer");
+    FLARE_REQUIRE(B > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0, "decode_step: sizes must be positive");
+    FLARE_REQUIRE(Dv % 4 == 0, "decode_step: Dv=%lld must be a multiple of 4", (long long)Dv);
+    FLARE_REQUIRE(((uintptr_t)u & 15) == 0, "decode_step: u must be 16-byte aligned");
+    const bool shared = Qdec == nullptr && Kdec == nullptr;
+    const void* qd = Qdec ? Qdec : K;
+    const void* kd = Kdec ? Kdec : Q;
+    int NT4 = 1;
+    while (NT4 * 2 <= Dv / 4 && NT4 * 2 <= kDecNT) NT4 *= 2;
+    const size_t sm = sizeof(float) * (2 * Dk + Dv + 4 * M + 8 + 3) + sizeof(float4) * kDecNT;
+    FLARE_REQUIRE(sm <= 64 * 1024, "decode_step: shape too large for LDS");
+    (void)NT4;
+    hipStream_t s = (hipStream_t)stream;
+#define FLARE_DEC(TY)                                                                          \
+    hipLaunchKernelGGL(decode_step_kernel<TY>, dim3((unsigned)(B * H)), dim3(kDecNT), sm, s,     \
+                       (const TY*)Q, (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd,   \
+                       mask, (int)H, (int)M, (int)Dk, (int)Dv, scale, shared, m, d, u, y,        \
+                       out_dtype)
+    if (dtype == FLARE_BF16) FLARE_DEC(__hip_bfloat16);
+    else if (dtype == FLARE_F16) FLARE_DEC(__half);
+    else FLARE_DEC(float);
+#undef FLARE_DEC
+    return check_launch("decode_step_kernel");
+}

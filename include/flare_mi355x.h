@@ -1,0 +1,139 @@
+/*
+ * flare_mi355x.h -- C ABI of the MI355X (gfx950) causal FLARE forward library.
+ *
+ * Every entry point takes plain device pointers, sizes, a scale and a HIP
+ * stream (passed as void*; NULL = the legacy default stream), enqueues its
+ * kernels on that stream and returns without synchronising.  The return value
+ * is FLARE_OK or a negative FLARE_ERR_* code; flare_last_error() then gives a
+ * human-readable message (thread-local).
+ *
+ * Tensor layouts are the reference's (vpuri3/causal-flare), contiguous:
+ *   Q     [H, M, Dk]      latent queries (encoder)
+ *   K     [B, N, H, Dk]   keys        V [B, N, H, Dv] values
+ *   Qdec  [B, N, H, Dk]   decoder queries (NULL -> K, the reference default)
+ *   Kdec  [H, M, Dk]      decoder keys    (NULL -> Q, the reference default)
+ *   Y     [B, N, H, Dv]   output, element type `out_dtype`
+ *   state m, d [B, H, M] and u [B, H, M, Dv], always fp32
+ * `dtype` is the element type of Q, K, V, Qdec and Kdec (one type for all).
+ * Chunk summaries (chunk_max/den [B*H, NC, M], chunk_num [B*H, NC, M, Dv])
+ * are fp32 and are owned by the caller.
+ *
+ * Each declaration names the reference interface it replaces (path:line in
+ * vpuri3/causal-flare).
+ */
+#ifndef FLARE_MI355X_H
+#define FLARE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum flare_dtype { FLARE_F32 = 0, FLARE_BF16 = 1, FLARE_F16 = 2 };
+
+enum flare_status {
+    FLARE_OK = 0,
+    FLARE_ERR_INVALID = -1,     /* bad argument / unsupported shape */
+    FLARE_ERR_LAUNCH = -2,      /* HIP launch or runtime error */
+    FLARE_ERR_WORKSPACE = -3    /* workspace too small */
+};
+
+/* Library identification and the message of the last failed call. */
+int flare_abi_version(void);
+const char* flare_last_error(void);
+
+/*
+ * Phase 1 of the chunked forward: per chunk of `chunk` tokens and per latent,
+ * the max score, softmax denominator and softmax-weighted value sum.
+ * Replaces the Triton kernel flare_chunk_prepare
+ * (causal_flare/autoregressive/training.py:914-1018) and its launcher
+ * _run_chunked_prepare_phase (training.py:489-557).  NC = ceil(N / chunk).
+ */
+int flare_chunk_prepare(const void* Q, const void* K, const void* V, int dtype, int64_t B,
+                        int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                        int64_t chunk, float* chunk_max, float* chunk_den, float* chunk_num,
+                        void* stream);
+
+/*
+ * Phase 2: in-place exclusive online-softmax scan over the NC chunk summaries
+ * of each (b,h), optionally starting from an initial cached state (m0/d0/u0,
+ * any may be NULL only if all are NULL) and optionally writing the inclusive
+ * final state (m_fin/d_fin/u_fin, all or none).
+ * Replaces flare_chunk_prefix (training.py:1021-1103) and, for prefill, the
+ * torch merges of the initial and final states
+ * (causal_flare/autoregressive/inference.py:753-814, _merge_flare_stats :194-228).
+ */
+int flare_chunk_prefix(float* chunk_max, float* chunk_den, float* chunk_num, int64_t BH,
+                       int64_t NC, int64_t M, int64_t Dv, const float* m0, const float* d0,
+                       const float* u0, float* m_fin, float* d_fin, float* u_fin, void* stream);
+
+/*
+ * Phase 3: per chunk, replay the token recurrence from the chunk's prefix
+ * state and emit y_t = sum_m softmax_m(a_t)[m] * z_t[m].  Optionally writes
+ * LSE_dec [B*H, N] (logsumexp_m of the decoder scores; may be NULL).
+ * Replaces flare_chunk_decoder_lse + flare_chunk_fwd
+ * (training.py:1106-1392) and _run_chunked_output_phase (training.py:615-728).
+ */
+int flare_chunk_output(const void* Q, const void* K, const void* V, const void* Qdec,
+                       const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                       int64_t Dk, int64_t Dv, float scale, int64_t chunk,
+                       const float* prefix_max, const float* prefix_den, const float* prefix_num,
+                       void* Y, int out_dtype, float* lse_dec, void* stream);
+
+/* Bytes of fp32 workspace flare_ar_forward needs (chunk summaries). */
+size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                       int64_t chunk);
+
+/*
+ * Whole chunked forward / prefill: phases 1-3 on one stream.  `chunk` <= 0
+ * selects the library's own chunk length.  m0/d0/u0 (initial state) and
+ * m_fin/d_fin/u_fin (final state) are optional as in flare_chunk_prefix.
+ * Replaces AutoRegressiveFLARE.forward (training.py:731-905) and
+ * flare_autoregressive_prefill_triton's unmasked path (inference.py:697-820).
+ */
+int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
+                     const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                     const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                     void* Y, int out_dtype, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* The chunk length flare_ar_forward uses when called with chunk <= 0. */
+int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
+
+/*
+ * One recurrent decode step for every (b,h): K, V (and Qdec) are [B, H, D];
+ * the fp32 state m/d/u is updated in place; y [B, H, Dv] is written in
+ * `out_dtype`.  mask [B] (int32, nonzero = valid) may be NULL; an invalid
+ * batch row leaves its state unchanged and gets y = 0.
+ * Replaces flare_recurrent_step_kernel + flare_autoregressive_decode_triton
+ * (inference.py:358-621).
+ */
+int flare_decode_step(const void* Q, const void* K, const void* V, const void* Qdec,
+                      const void* Kdec, const int32_t* mask, int dtype, int64_t B, int64_t H,
+                      int64_t M, int64_t Dk, int64_t Dv, float scale, float* m, float* d,
+                      float* u, void* y, int out_dtype, void* stream);
+
+/*
+ * Block-causal (semi-autoregressive) forward: token t of block g attends to
+ * every token of blocks <= g.  Writes Y, and optionally LSE_dec [B*H, N] and
+ * LSE_enc [B*H, NB, M] (NB = N / block).  Requires N % block == 0 and
+ * block % 16 == 0 (validated on the host side as in the reference).
+ * Replaces _semi_autoregressive_forward_triton and its kernels
+ * (causal_flare/semi_autoregressive/training.py:540-1399, 1836-1961).
+ */
+size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                    int64_t block);
+int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
+                          const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H,
+                          int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,
+                          void* Y, int out_dtype, float* lse_dec, float* lse_enc,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLARE_MI355X_H */

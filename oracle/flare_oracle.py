@@ -1,0 +1,303 @@
+"""CPU oracle for the causal FLARE forward paths -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
+may import this module, and only as the checker or as the timed CPU baseline.
+The product package never imports it; there is no CPU fallback in the product.
+
+Two layers:
+
+* ``ar_chunked`` / ``ar_recurrent`` / ``semi_ar`` call the fp32 C restatement in
+  ``flare_oracle.c`` (built by ``oracle/Makefile`` into ``oracle/_build``).
+  They follow, in order:
+    - ``causal_flare/autoregressive/reference.py:203-512`` (chunked forward)
+    - ``causal_flare/autoregressive/inference.py:231-351`` (prefill / decode)
+    - ``causal_flare/semi_autoregressive/reference.py:308-536`` (block-causal)
+* ``brute_*`` are fp64 numpy restatements of the definitions the reference
+  uses as its own ground truth:
+    - ``brute_ar``: the per-token two-SDPA oracle, ``reference.py:15-47``
+    - ``brute_semi_ar``: the per-block two-SDPA oracle, ``semi_autoregressive/reference.py:560-597``
+    - ``brute_ar_state``: the same definition continued from a cached state
+      ``{m, d, u}`` (``inference.py:66-120``), with an optional token mask.
+  They are the pins for the C restatement (see tests/test_oracle.py).
+
+Parity status: every C entry point is pinned by fp64 brute force, by
+invariants (chunk-size independence, prefill/decode continuation, state
+continuation, semi-AR/AR agreement at block ends) and by closed forms
+(N=1, constant V, M=1 via torch SDPA).  No function here is "parity unpinned".
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libflare_oracle.so")
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+def build(force: bool = False) -> str:
+    """Compile the C oracle with its Makefile (gcc, OpenMP)."""
+    if force or not os.path.exists(_LIB_PATH):
+        subprocess.run(["make", "-s", "-C", _HERE, "-B" if force else "_build/libflare_oracle.so"],
+                       check=True)
+    return _LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        i = ctypes.c_int
+        f = ctypes.c_float
+        lib.oracle_ar_chunked.argtypes = [_f32p] * 5 + [_u8p] + [_f32p] * 3 + [i] * 6 + [f, i, i] + [_f32p] * 4 + [i]
+        lib.oracle_ar_recurrent.argtypes = [_f32p] * 5 + [_u8p] + [_f32p] * 3 + [i] * 6 + [f, i] + [_f32p] * 4 + [i]
+        lib.oracle_semi_ar.argtypes = [_f32p] * 5 + [i] * 6 + [f, i, i] + [_f32p] * 3 + [i]
+        for fn in (lib.oracle_ar_chunked, lib.oracle_ar_recurrent, lib.oracle_semi_ar):
+            fn.restype = ctypes.c_int
+        _lib = lib
+    return _lib
+
+
+def _f32(x):
+    if x is None:
+        return None
+    if hasattr(x, "detach"):  # torch tensor
+        x = x.detach().float().cpu().numpy()
+    return np.ascontiguousarray(x, dtype=np.float32)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_f32p)
+
+
+def _u8(mask):
+    if mask is None:
+        return None, None
+    if hasattr(mask, "detach"):
+        mask = mask.detach().cpu().numpy()
+    m = np.ascontiguousarray(mask != 0, dtype=np.uint8)
+    return m, m.ctypes.data_as(_u8p)
+
+
+def resolve_scale(scale, head_dim: int) -> float:
+    """``_common.py:201-204``: 1.0 when D <= 8, else D**-0.5."""
+    if scale is not None:
+        return float(scale)
+    return 1.0 if head_dim <= 8 else head_dim ** -0.5
+
+
+def resolve_reference_chunk_size(N: int, M: int, D_score: int, chunk_size=None) -> int:
+    """``reference.py:190-200`` (the PyTorch path's own chunk policy)."""
+    if chunk_size is not None:
+        return int(chunk_size)
+    if D_score <= 32 and M <= 64 and N >= 1024:
+        return 64
+    if D_score <= 64 and M <= 128 and N >= 1024:
+        return 128
+    return max(64, min(2048, max(1, N // 2)))
+
+
+def _shared(Q_dec, K_dec):
+    return Q_dec is None and K_dec is None
+
+
+def _state_arrays(state):
+    if state is None:
+        return None, None, None
+    return _f32(state["m"]), _f32(state["d"]), _f32(state["u"])
+
+
+def ar_chunked(Q, K, V, scale=None, chunk_size=None, Q_dec=None, K_dec=None, state=None,
+               attention_mask=None, return_state=False, nthreads=0):
+    """fp32 chunked causal FLARE forward (reference.py:203-512). Returns fp32 numpy."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    Qd, Kd = _f32(Q_dec), _f32(K_dec)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    C = resolve_reference_chunk_size(N, M, Dk, chunk_size)
+    mask, maskp = _u8(attention_mask)
+    m0, d0, u0 = _state_arrays(state)
+    Y = np.zeros((B, N, H, Dv), np.float32)
+    mo = np.empty((B, H, M), np.float32)
+    do = np.empty((B, H, M), np.float32)
+    uo = np.empty((B, H, M, Dv), np.float32)
+    rc = _load().oracle_ar_chunked(_ptr(Q), _ptr(K), _ptr(V), _ptr(Qd), _ptr(Kd), maskp,
+                                   _ptr(m0), _ptr(d0), _ptr(u0), B, N, H, M, Dk, Dv, scale, C,
+                                   int(_shared(Q_dec, K_dec)), _ptr(Y), _ptr(mo), _ptr(do), _ptr(uo),
+                                   int(nthreads))
+    assert rc == 0, rc
+    if return_state:
+        return Y, {"m": mo, "d": do, "u": uo}
+    return Y
+
+
+def ar_recurrent(Q, K, V, state=None, scale=1.0, attention_mask=None, Q_dec=None, K_dec=None,
+                 nthreads=0):
+    """fp32 tokenwise prefill (inference.py:231-315); decode is T=1 (:318-351)."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    Qd, Kd = _f32(Q_dec), _f32(K_dec)
+    H, M, Dk = Q.shape
+    B, T, _, Dv = V.shape
+    mask, maskp = _u8(attention_mask)
+    m0, d0, u0 = _state_arrays(state)
+    Y = np.zeros((B, T, H, Dv), np.float32)
+    mo = np.empty((B, H, M), np.float32)
+    do = np.empty((B, H, M), np.float32)
+    uo = np.empty((B, H, M, Dv), np.float32)
+    rc = _load().oracle_ar_recurrent(_ptr(Q), _ptr(K), _ptr(V), _ptr(Qd), _ptr(Kd), maskp,
+                                     _ptr(m0), _ptr(d0), _ptr(u0), B, T, H, M, Dk, Dv,
+                                     float(scale), int(_shared(Q_dec, K_dec)), _ptr(Y), _ptr(mo),
+                                     _ptr(do), _ptr(uo), int(nthreads))
+    assert rc == 0, rc
+    return Y, {"m": mo, "d": do, "u": uo}
+
+
+def semi_ar(Q, K, V, block_size, chunk_size, scale=None, Q_dec=None, K_dec=None, nthreads=0):
+    """fp32 block-causal forward (semi reference.py:308-536). Returns (Y, LSE_dec, LSE_enc)."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    Qd, Kd = _f32(Q_dec), _f32(K_dec)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    NB = N // block_size
+    Y = np.zeros((B, N, H, Dv), np.float32)
+    lse_dec = np.empty((B, H, N), np.float32)
+    lse_enc = np.empty((B, H, NB, M), np.float32)
+    rc = _load().oracle_semi_ar(_ptr(Q), _ptr(K), _ptr(V), _ptr(Qd), _ptr(Kd), B, N, H, M, Dk, Dv,
+                                scale, int(block_size), int(chunk_size), _ptr(Y), _ptr(lse_dec),
+                                _ptr(lse_enc), int(nthreads))
+    assert rc == 0, rc
+    return Y, lse_dec, lse_enc
+
+
+# --------------------------------------------------------------------------
+# fp64 brute-force definitions (the pins)
+# --------------------------------------------------------------------------
+
+def _f64(x):
+    if x is None:
+        return None
+    if hasattr(x, "detach"):
+        x = x.detach().double().cpu().numpy()
+    return np.asarray(x, dtype=np.float64)
+
+
+def _softmax(x, axis=-1):
+    x = x - x.max(axis=axis, keepdims=True)
+    e = np.exp(x)
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+def brute_ar(Q, K, V, scale=None, Q_dec=None, K_dec=None):
+    """reference.py:15-47: z_t = SDPA(Q, K[:t+1], V[:t+1]); y_t = SDPA(Qdec_t, Kdec, z_t). fp64."""
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    S = scale * np.einsum("bnhd,hmd->bhnm", K, Q)             # encoder scores
+    A = scale * np.einsum("bnhd,hmd->bhnm", Qd, Kd)           # decoder scores
+    Vt = V.transpose(0, 2, 1, 3)                               # [B,H,N,Dv]
+    Y = np.empty((B, H, N, Dv))
+    for t in range(N):
+        P = _softmax(S[:, :, : t + 1, :], axis=2)              # over tau <= t
+        Z = np.einsum("bhtm,bhtd->bhmd", P, Vt[:, :, : t + 1])
+        alpha = _softmax(A[:, :, t, :], axis=-1)
+        Y[:, :, t] = np.einsum("bhm,bhmd->bhd", alpha, Z)
+    return Y.transpose(0, 2, 1, 3)
+
+
+def brute_ar_state(Q, K, V, state=None, scale=1.0, attention_mask=None, Q_dec=None, K_dec=None):
+    """Prefill continuing a cached state {m,d,u} (inference.py:66-120 semantics), fp64.
+
+    The cached state stands for earlier tokens with weights exp(m) * d (denominator)
+    and exp(m) * u (numerator).  Masked tokens contribute nothing and output y = 0
+    (inference.py:279-311).  Returns (Y, state) with the state in the convention
+    m = running max of all seen scores.
+    """
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, T, _, Dv = V.shape
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    valid = np.ones((B, T), bool) if attention_mask is None else (np.asarray(
+        attention_mask.cpu() if hasattr(attention_mask, "cpu") else attention_mask) != 0)
+    S = scale * np.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * np.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    Vt = V.transpose(0, 2, 1, 3)
+    if state is None:
+        m0 = np.full((B, H, M), -np.inf)
+        d0 = np.zeros((B, H, M))
+        u0 = np.zeros((B, H, M, Dv))
+    else:
+        m0, d0, u0 = _f64(state["m"]), _f64(state["d"]), _f64(state["u"])
+    Y = np.zeros((B, H, T, Dv))
+    mfin, dfin, ufin = m0.copy(), d0.copy(), u0.copy()
+    for b in range(B):
+        for h in range(H):
+            for t in range(T):
+                sel = np.nonzero(valid[b, : t + 1])[0]
+                s = S[b, h, sel, :]                              # [n_valid, M]
+                mx = np.maximum(m0[b, h], s.max(axis=0) if len(sel) else -np.inf)
+                mx_safe = np.where(np.isneginf(mx), 0.0, mx)
+                w_state = np.where(np.isneginf(m0[b, h]), 0.0, np.exp(m0[b, h] - mx_safe))
+                w_tok = np.exp(s - mx_safe)                      # [n, M]
+                den = d0[b, h] * w_state + w_tok.sum(axis=0)
+                num = u0[b, h] * w_state[:, None] + w_tok.T @ Vt[b, h, sel]
+                if t == T - 1:
+                    mfin[b, h], dfin[b, h], ufin[b, h] = mx, den, num
+                if not valid[b, t]:
+                    continue
+                z = num / np.where(den > 0, den, 1.0)[:, None]
+                alpha = _softmax(A[b, h, t])
+                Y[b, h, t] = alpha @ z
+    return Y.transpose(0, 2, 1, 3), {"m": mfin, "d": dfin, "u": ufin}
+
+
+def brute_semi_ar(Q, K, V, block_size, scale=None, Q_dec=None, K_dec=None):
+    """semi_autoregressive/reference.py:560-597: per block, two SDPAs over all tokens < block end. fp64."""
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    S = scale * np.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * np.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    Vt = V.transpose(0, 2, 1, 3)
+    Y = np.empty((B, H, N, Dv))
+    for g in range(math.ceil(N / block_size)):
+        t0, t1 = g * block_size, min(N, (g + 1) * block_size)
+        P = _softmax(S[:, :, :t1, :], axis=2)
+        Z = np.einsum("bhtm,bhtd->bhmd", P, Vt[:, :, :t1])
+        alpha = _softmax(A[:, :, t0:t1, :], axis=-1)
+        Y[:, :, t0:t1] = np.einsum("bhtm,bhmd->bhtd", alpha, Z)
+    return Y.transpose(0, 2, 1, 3)
+
+
+def allclose_rel(a, b, dtype_name: str):
+    """Tolerance used by every parity test.
+
+    ``_common.py:132-137`` gives (rtol, atol) = (1e-5, 1e-5) for fp32 and
+    (1e-2, 1e-2) for bf16/fp16; ``_common.py:144-146`` defines
+    max_rel_err = max |a-b| / (|b| + atol).
+    Returns (max_rel_err, max_abs_err).
+    """
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    atol = 1e-5 if dtype_name == "float32" else 1e-2
+    if a.size == 0:
+        return 0.0, 0.0
+    d = np.abs(a - b)
+    return float((d / (np.abs(b) + atol)).max()), float(d.max())

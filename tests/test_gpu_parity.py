@@ -1,0 +1,292 @@
+"""GPU parity: the HIP kernels (through the drop-in Python entry points and the
+C ABI) against the fp32 CPU oracle on identical seeded inputs.
+
+Mirrors the reference's GPU suites: testing/autoregressive/test_flare.py:342-490
+(chunked / prefill / decode parity, 3x3 decoder-aliasing modes),
+testing/autoregressive/test_cached_suites.py:24-104 (masked prefill, decode
+continuation) and testing/semi_autoregressive/test_block_causal.py:178-255.
+Tolerances are stated in tests/_util.py (assert_parity).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import flare_oracle as O
+from _util import assert_parity, seeded, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _print_case(*args):
+    print("CASE", *args, flush=True)
+    sys.stdout.flush()
+
+
+def _dec_variants(q, k, g):
+    qd_rand = torch.randn(k.shape, generator=g).to(k.dtype).to(k.device)
+    kd_rand = torch.randn(q.shape, generator=g).to(q.dtype).to(q.device)
+    return {"none": None, "k_enc": k, "rand": qd_rand}, {"none": None, "q_enc": q, "rand": kd_rand}
+
+
+def _oracle_dec(x, enc):
+    """The oracle takes None for the default decoder tensor."""
+    return None if (x is None or x is enc) else x
+
+
+# --------------------------------------------------------------------------
+# Full-sequence chunked forward
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("d_score,d_value", [(16, 16), (64, 128)])
+def test_chunked_forward_decoder_variants_fp32(d_score, d_value):
+    from causal_flare import flare_autoregressive_triton
+    B, N, H, M = 1, 16, 2, 16
+    _print_case("chunked_fp32_variants", d_score, d_value)
+    q, k, v = seeded(2028, B, N, H, M, d_score, d_value, torch.float32, device=DEV)
+    g = torch.Generator().manual_seed(7)
+    qds, kds = _dec_variants(q, k, g)
+    scale = 1.0 / math.sqrt(d_score)
+    for qn, qd in qds.items():
+        for kn, kd in kds.items():
+            y = flare_autoregressive_triton(q, k, v, scale=scale, chunk_size=16, Q_dec=qd, K_dec=kd)
+            ref = O.ar_chunked(q, k, v, scale=scale, chunk_size=16, Q_dec=_oracle_dec(qd, k),
+                               K_dec=_oracle_dec(kd, q))
+            assert y.dtype == torch.float32
+            assert_parity(y, ref, torch.float32, f"chunked q_dec={qn} k_dec={kn}")
+
+
+@pytest.mark.parametrize("chunk", [None, 16, 48, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chunked_forward_ragged_lengths(chunk, dtype):
+    from causal_flare import flare_autoregressive_triton
+    B, N, H, M, D = 2, 203, 3, 32, 64
+    _print_case("chunked_ragged", chunk, dtype)
+    q, k, v = seeded(11, B, N, H, M, D, D, dtype, q_std=D ** -0.5, device=DEV)
+    y = flare_autoregressive_triton(q, k, v, chunk_size=chunk)
+    assert y.dtype == dtype
+    ref = O.ar_chunked(q, k, v)
+    assert_parity(y, ref, dtype, f"ragged chunk={chunk}")
+
+
+def test_cfg1_cpu_reference_shape_fp32():
+    """B=1, N=256, H=8, M=64, D=32, fp32, q ~ N(0,1), seed 0."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("cfg1")
+    torch.manual_seed(0)
+    q = torch.randn(8, 64, 32)
+    k = torch.randn(1, 256, 8, 32)
+    v = torch.randn(1, 256, 8, 32)
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert_parity(y, O.ar_chunked(q, k, v), torch.float32, "cfg1")
+    # and against the fp64 two-SDPA definition itself
+    assert_parity(y, O.brute_ar(q, k, v), torch.float32, "cfg1 brute")
+
+
+def _cfg_inputs(seed, B, N, H, M, D, dtype):
+    torch.manual_seed(seed)
+    q = torch.randn(H, M, D) / math.sqrt(D)
+    k = torch.randn(B, N, H, D)
+    v = torch.randn(B, N, H, D)
+    return q.to(dtype), k.to(dtype), v.to(dtype)
+
+
+def test_cfg2_chunked_prefill_bf16():
+    """B=4, N=4096, H=16, M=128, D=64, bf16, seed 1."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("cfg2")
+    q, k, v = _cfg_inputs(1, 4, 4096, 16, 128, 64, torch.bfloat16)
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert y.dtype == torch.bfloat16
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    assert_parity(y, ref, torch.bfloat16, "cfg2")
+
+
+def test_cfg3_long_context_bf16_two_heads():
+    """BASELINE config 3 (B=1, N=65536, H=16, M=256, D=128, bf16, seed 2) on the
+    GPU for all heads; the oracle checks heads 0 and 9 at full length."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("cfg3")
+    q, k, v = _cfg_inputs(2, 1, 65536, 16, 256, 128, torch.bfloat16)
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
+    assert torch.isfinite(y.float()).all()
+    for h in (0, 9):
+        ref = O.ar_chunked(q[h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1], scale=128 ** -0.5, nthreads=16)
+        assert_parity(y[:, :, h:h + 1], ref, torch.bfloat16, f"cfg3 head {h}")
+
+
+# --------------------------------------------------------------------------
+# Prefill / decode
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("q_dec_mode", ["none", "k_enc", "rand"])
+@pytest.mark.parametrize("k_dec_mode", ["none", "q_enc", "rand"])
+@pytest.mark.parametrize("d_score,d_value", [(16, 16), (64, 128)])
+def test_prefill_decode_variants_fp32(q_dec_mode, k_dec_mode, d_score, d_value):
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("prefill_decode", q_dec_mode, k_dec_mode, d_score, d_value)
+    B, N, H, M = 1, 16, 2, 16
+    q, k, v = seeded(1337, B, N, H, M, d_score, d_value, torch.float32, device=DEV)
+    g = torch.Generator().manual_seed(3)
+    qds, kds = _dec_variants(q, k, g)
+    qd, kd = qds[q_dec_mode], kds[{"none": "none", "q_enc": "q_enc", "rand": "rand"}[k_dec_mode]]
+    scale = 1.0 / math.sqrt(d_score)
+    y, st = flare_autoregressive_prefill_triton(Q=q, K=k, V=v, Q_dec=qd, K_dec=kd, scale=scale)
+    y_ref, st_ref = O.ar_recurrent(q, k, v, scale=scale, Q_dec=_oracle_dec(qd, k), K_dec=_oracle_dec(kd, q))
+    assert_parity(y, y_ref, torch.float32, "prefill y")
+    for key in ("m", "d", "u"):
+        assert_parity(st[key], st_ref[key], torch.float32, f"prefill state {key}")
+
+    k_next = torch.randn((B, 1, H, d_score), generator=g).to(DEV)
+    v_next = torch.randn((B, 1, H, d_value), generator=g).to(DEV)
+    qd_next = {"none": None, "k_enc": k_next, "rand": torch.randn((B, 1, H, d_score), generator=g).to(DEV)}[q_dec_mode]
+    y1, st1 = flare_autoregressive_decode_triton(Q=q, K=k_next, V=v_next, state=st, Q_dec=qd_next, K_dec=kd,
+                                                 scale=scale)
+    assert st1["u"] is st["u"], "decode must update the fp32 state in place"
+    y1_ref, st1_ref = O.ar_recurrent(q, k_next, v_next, state=st_ref, scale=scale,
+                                     Q_dec=_oracle_dec(qd_next, k_next), K_dec=_oracle_dec(kd, q))
+    assert y1.shape == (B, 1, H, d_value)
+    assert_parity(y1, y1_ref, torch.float32, "decode y")
+    for key in ("m", "d", "u"):
+        assert_parity(st1[key], st1_ref[key], torch.float32, f"decode state {key}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_continuation_equals_prefill_of_concatenation(dtype):
+    """test_cached_suites.py:55-63: prefill(T) + decode steps == prefill(T + steps)."""
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("continuation", dtype)
+    B, T, S, H, M, D = 3, 150, 5, 2, 32, 64
+    q, k, v = seeded(5, B, T + S, H, M, D, D, dtype, q_std=D ** -0.5, device=DEV)
+    y_all, st_all = flare_autoregressive_prefill_triton(q, k, v)
+    y_pre, st = flare_autoregressive_prefill_triton(q, k[:, :T], v[:, :T])
+    ys = [y_pre]
+    for t in range(T, T + S):
+        y_t, st = flare_autoregressive_decode_triton(q, k[:, t:t + 1], v[:, t:t + 1], state=st)
+        ys.append(y_t)
+    y_cat = torch.cat(ys, dim=1)
+    assert_parity(y_cat.float(), y_all.float(), dtype, "continuation y")
+    ref, st_ref = O.ar_recurrent(q, k, v)
+    assert_parity(y_all, ref, dtype, "prefill vs oracle")
+    assert_parity(st["u"], st_ref["u"], torch.float32 if dtype == torch.float32 else dtype, "continued state u")
+
+
+def test_prefill_with_initial_state_and_mask():
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("prefill_state_mask")
+    B, T, H, M, D = 2, 40, 2, 16, 32
+    q, k, v = seeded(9, B, 2 * T, H, M, D, D, torch.float32, device=DEV)
+    _, st = flare_autoregressive_prefill_triton(q, k[:, :T], v[:, :T])
+    st_keep = {kk: vv.clone() for kk, vv in st.items()}
+    y, st2 = flare_autoregressive_prefill_triton(q, k[:, T:], v[:, T:], state=st)
+    for kk in st_keep:
+        assert torch.equal(st_keep[kk], st[kk]), "prefill must not modify its input state"
+    _, st_o = O.ar_recurrent(q, k[:, :T], v[:, :T])
+    y_ref, st2_ref = O.ar_recurrent(q, k[:, T:], v[:, T:], state=st_o)
+    assert_parity(y, y_ref, torch.float32, "prefill with state")
+    assert_parity(st2["u"], st2_ref["u"], torch.float32, "state u")
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[0, 3] = 0
+    mask[1, 10:20] = 0
+    ym, stm = flare_autoregressive_prefill_triton(q, k[:, T:], v[:, T:], state=st, attention_mask=mask.to(DEV))
+    ym_ref, stm_ref = O.ar_recurrent(q, k[:, T:], v[:, T:], state=st_o, attention_mask=mask)
+    assert_parity(ym, ym_ref, torch.float32, "masked prefill")
+    assert float(ym[0, 3].abs().max()) == 0.0 and float(ym[1, 10:20].abs().max()) == 0.0
+    assert_parity(stm["m"], stm_ref["m"], torch.float32, "masked state m")
+    assert_parity(stm["u"], stm_ref["u"], torch.float32, "masked state u")
+
+
+def test_cfg4_decode_bf16():
+    """BASELINE config 4 (reduced steps): B=64, H=16, M=128, D=64, 2048-token prefill then decode."""
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("cfg4")
+    B, T, H, M, D, steps = 64, 2048, 16, 128, 64, 4
+    torch.manual_seed(3)
+    q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16)
+    k = torch.randn(B, T + steps, H, D).to(torch.bfloat16)
+    v = torch.randn(B, T + steps, H, D).to(torch.bfloat16)
+    qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
+    y, st = flare_autoregressive_prefill_triton(qg, kg[:, :T], vg[:, :T])
+    ys = []
+    for t in range(T, T + steps):
+        y_t, st = flare_autoregressive_decode_triton(qg, kg[:, t], vg[:, t], state=st)
+        ys.append(y_t)
+    y_dec = torch.cat(ys, dim=1)
+    ref, st_ref = O.ar_recurrent(q, k, v, nthreads=16)
+    assert_parity(y, ref[:, :T], torch.bfloat16, "cfg4 prefill")
+    assert_parity(y_dec, ref[:, T:], torch.bfloat16, "cfg4 decode")
+    assert_parity(st["u"], st_ref["u"], torch.bfloat16, "cfg4 state u")
+
+
+def test_decode_masked_rows_keep_state():
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("decode_mask")
+    B, T, H, M, D = 4, 20, 2, 16, 16
+    q, k, v = seeded(21, B, T + 1, H, M, D, D, torch.float32, device=DEV)
+    _, st = flare_autoregressive_prefill_triton(q, k[:, :T], v[:, :T])
+    before = {kk: vv.clone() for kk, vv in st.items()}
+    mask = torch.tensor([1, 0, 1, 0], device=DEV)
+    y, st = flare_autoregressive_decode_triton(q, k[:, T], v[:, T], state=st, attention_mask=mask)
+    assert float(y[1].abs().max()) == 0.0 and float(y[3].abs().max()) == 0.0
+    for kk in ("m", "d", "u"):
+        assert torch.equal(st[kk][1], before[kk][1]) and torch.equal(st[kk][3], before[kk][3])
+    _, st_o = O.ar_recurrent(q, k[:, :T], v[:, :T])
+    y_ref, _ = O.ar_recurrent(q, k[:, T:], v[:, T:], state=st_o, attention_mask=mask.cpu()[:, None])
+    assert_parity(y, y_ref, torch.float32, "masked decode")
+
+
+# --------------------------------------------------------------------------
+# Semi-autoregressive (block-causal)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("block_size,chunk_size,seq_len", [(16, 16, 48), (32, 16, 64), (64, 16, 128)])
+def test_semi_ar_small_fp32(block_size, chunk_size, seq_len):
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_small", block_size, seq_len)
+    B, H, M, D = 2, 3, 5, 16
+    q, k, v = seeded(0, B, seq_len, H, M, D, D, torch.float32, device=DEV)
+    y, aux = flare_semi_autoregressive_trition(q, k, v, block_size=block_size, chunk_size=chunk_size)
+    y_ref, lse_dec, lse_enc = O.semi_ar(q, k, v, block_size, chunk_size)
+    assert y.dtype == v.dtype
+    assert aux["LSE_dec"].shape == (B, H, seq_len)
+    assert aux["LSE_enc"].shape == (B, H, seq_len // block_size, M)
+    assert_parity(y, y_ref, torch.float32, "semi y")
+    assert_parity(aux["LSE_dec"], lse_dec, torch.float32, "semi LSE_dec")
+    assert_parity(aux["LSE_enc"], lse_enc, torch.float32, "semi LSE_enc")
+
+
+def test_semi_ar_decoder_variants_bf16():
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_variants")
+    B, N, H, M, D = 1, 128, 2, 16, 16
+    q, k, v = seeded(2, B, N, H, M, D, D, torch.bfloat16, device=DEV)
+    g = torch.Generator().manual_seed(4)
+    qds, kds = _dec_variants(q, k, g)
+    for qn, qd in qds.items():
+        for kn, kd in kds.items():
+            y, aux = flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=16, Q_dec=qd, K_dec=kd)
+            y_ref, _, lse_enc = O.semi_ar(q, k, v, 64, 16, Q_dec=_oracle_dec(qd, k), K_dec=_oracle_dec(kd, q))
+            assert_parity(y, y_ref, torch.bfloat16, f"semi q_dec={qn} k_dec={kn}")
+            assert_parity(aux["LSE_enc"], lse_enc, torch.bfloat16, "semi LSE_enc")
+
+
+def test_cfg5_semi_ar_bf16():
+    """B=2, N=8192, H=16, M=128, D=64, block 64, bf16, seed 4."""
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("cfg5")
+    q, k, v = _cfg_inputs(4, 2, 8192, 16, 128, 64, torch.bfloat16)
+    y, aux = flare_semi_autoregressive_trition(q.to(DEV), k.to(DEV), v.to(DEV), block_size=64, chunk_size=64)
+    y_ref, lse_dec, _ = O.semi_ar(q, k, v, 64, 64, nthreads=16)
+    assert_parity(y, y_ref, torch.bfloat16, "cfg5 y")
+    assert_parity(aux["LSE_dec"], lse_dec, torch.bfloat16, "cfg5 LSE_dec")
+
+
+def test_semi_ar_full_block_equals_noncausal_flare():
+    """block_size = N: every token sees every token (semi reference.py:575-596)."""
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_full_block")
+    B, N, H, M, D = 2, 64, 2, 16, 32
+    q, k, v = seeded(8, B, N, H, M, D, D, torch.float32, device=DEV)
+    y, _ = flare_semi_autoregressive_trition(q, k, v, block_size=N, chunk_size=64)
+    ref = O.brute_semi_ar(q, k, v, N)
+    assert_parity(y, ref, torch.float32, "semi block=N")

@@ -1,0 +1,190 @@
+"""Pins for the CPU oracle (oracle/flare_oracle.c and oracle/flare_oracle.py).
+
+The reference holds no golden vectors (all of its tests draw torch.randn at run
+time), so the C restatement is pinned by
+  * the fp64 brute-force definitions the reference itself treats as ground
+    truth (reference.py:15-47, semi_autoregressive/reference.py:560-597),
+  * torch's scaled_dot_product_attention for the special cases that reduce to
+    textbook attention (M = 1; semi-AR with block = N),
+  * invariants (chunk-size independence, prefill/decode continuation, state
+    continuation, masked tokens, semi-AR vs AR at block ends) and closed
+    forms (N = 1, constant V),
+  * the committed fixtures in tests/golden/ (written by
+    tests/golden/make_golden.py from the fp64 definitions).
+Each check is chosen so that a plausible slip in the oracle -- a dropped
+prefix term, a wrong max in a rescale, a transposed operand, a missing scale
+-- fails at least one of them.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import flare_oracle as O
+from _util import seeded
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _close(a, b, tol=2e-5):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    assert a.shape == b.shape
+    np.testing.assert_allclose(a, b, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("B,N,H,M,Dk,Dv", [(1, 7, 2, 16, 16, 16), (2, 37, 3, 8, 8, 24), (1, 70, 1, 32, 64, 32)])
+@pytest.mark.parametrize("chunk", [1, 5, 16, 64, None])
+def test_chunked_matches_brute_force(B, N, H, M, Dk, Dv, chunk):
+    q, k, v = seeded(1, B, N, H, M, Dk, Dv, torch.float32)
+    y = O.ar_chunked(q, k, v, chunk_size=chunk)
+    _close(y, O.brute_ar(q, k, v))
+
+
+@pytest.mark.parametrize("sep_q,sep_k", [(False, True), (True, False), (True, True)])
+def test_chunked_separate_decoder_matches_brute_force(sep_q, sep_k):
+    B, N, H, M, D = 2, 29, 2, 16, 16
+    q, k, v = seeded(2, B, N, H, M, D, D, torch.float32)
+    g = torch.Generator().manual_seed(5)
+    qd = torch.randn(k.shape, generator=g) if sep_q else None
+    kd = torch.randn(q.shape, generator=g) if sep_k else None
+    y = O.ar_chunked(q, k, v, chunk_size=8, Q_dec=qd, K_dec=kd)
+    _close(y, O.brute_ar(q, k, v, Q_dec=qd, K_dec=kd))
+    # the decoder really is used: the result differs from the shared-weight one
+    assert np.abs(y - O.ar_chunked(q, k, v, chunk_size=8)).max() > 1e-3
+
+
+def test_scale_default_and_explicit():
+    q, k, v = seeded(3, 1, 20, 2, 16, 32, 32, torch.float32)
+    _close(O.ar_chunked(q, k, v), O.ar_chunked(q, k, v, scale=32 ** -0.5))
+    assert np.abs(O.ar_chunked(q, k, v, scale=1.0) - O.ar_chunked(q, k, v)).max() > 1e-3
+    _close(O.ar_chunked(q, k, v, scale=0.7), O.brute_ar(q, k, v, scale=0.7))
+    assert O.resolve_scale(None, 8) == 1.0 and O.resolve_scale(None, 16) == 0.25
+
+
+def test_recurrent_matches_brute_force_and_chunked():
+    B, T, H, M, D = 2, 33, 2, 16, 24
+    q, k, v = seeded(4, B, T, H, M, D, D, torch.float32)
+    y, st = O.ar_recurrent(q, k, v, scale=0.3)
+    yb, stb = O.brute_ar_state(q, k, v, scale=0.3)
+    _close(y, yb)
+    for key in ("m", "d", "u"):
+        _close(st[key], stb[key], 1e-4)
+    yc, stc = O.ar_chunked(q, k, v, scale=0.3, chunk_size=7, return_state=True)
+    _close(yc, y)
+    for key in ("m", "d", "u"):
+        _close(stc[key], st[key], 1e-4)
+
+
+def test_prefill_then_decode_equals_longer_prefill():
+    B, T, H, M, D = 2, 20, 2, 16, 16
+    q, k, v = seeded(6, B, T + 3, H, M, D, D, torch.float32)
+    y_all, st_all = O.ar_recurrent(q, k, v)
+    y, st = O.ar_recurrent(q, k[:, :T], v[:, :T])
+    ys = [y]
+    for t in range(T, T + 3):
+        y_t, st = O.ar_recurrent(q, k[:, t:t + 1], v[:, t:t + 1], state=st)
+        ys.append(y_t)
+    _close(np.concatenate(ys, axis=1), y_all)
+    for key in ("m", "d", "u"):
+        _close(st[key], st_all[key], 1e-4)
+
+
+def test_chunked_with_initial_state_equals_concatenation():
+    B, T, H, M, D = 1, 24, 2, 16, 16
+    q, k, v = seeded(7, B, 2 * T, H, M, D, D, torch.float32)
+    _, st = O.ar_chunked(q, k[:, :T], v[:, :T], chunk_size=16, return_state=True)
+    y2 = O.ar_chunked(q, k[:, T:], v[:, T:], chunk_size=16, state=st)
+    _close(y2, O.brute_ar(q, k, v, scale=0.25)[:, T:])
+
+
+def test_masked_tokens_output_zero_and_leave_state():
+    B, T, H, M, D = 2, 12, 2, 16, 16
+    q, k, v = seeded(8, B, T, H, M, D, D, torch.float32)
+    mask = np.ones((B, T), np.uint8)
+    mask[0, 4] = 0
+    mask[1, 0:3] = 0
+    y, st = O.ar_recurrent(q, k, v, attention_mask=mask)
+    assert np.all(y[0, 4] == 0) and np.all(y[1, 0:3] == 0)
+    yb, stb = O.brute_ar_state(q, k, v, attention_mask=mask)
+    _close(y, yb)
+    _close(st["u"], stb["u"], 1e-4)
+    # dropping the masked token entirely gives the same later outputs
+    keep = [t for t in range(T) if t != 4]
+    y_drop, _ = O.ar_recurrent(q, k[:1, keep], v[:1, keep])
+    _close(y[0, 5:], y_drop[0, 4:])
+    # the chunked path with a mask agrees with the recurrent one (reference.py:262-282)
+    yc = O.ar_chunked(q, k, v, scale=1.0, attention_mask=mask, chunk_size=5)
+    _close(yc, y)
+
+
+def test_closed_form_single_token_and_constant_values():
+    q, k, v = seeded(9, 2, 1, 3, 16, 16, 16, torch.float32)
+    _close(O.ar_chunked(q, k, v), v.numpy())                 # N = 1: z = v_0 for every latent
+    q, k, _ = seeded(10, 1, 40, 2, 16, 16, 8, torch.float32)
+    c = torch.randn(1, 1, 2, 8).expand(1, 40, 2, 8).contiguous()
+    _close(O.ar_chunked(q, k, c, chunk_size=16), c.numpy())  # constant V -> y = that constant
+
+
+def test_single_latent_is_causal_softmax_attention():
+    """M = 1: alpha = 1 and y_t = softmax_{tau<=t}(q.k_tau) V  (torch SDPA, is_causal)."""
+    B, N, H, D = 2, 50, 3, 16
+    q, k, v = seeded(11, B, N, H, 1, D, D, torch.float32)
+    y = O.ar_chunked(q, k, v, chunk_size=16)
+    qq = q[:, 0][None, :, None, :].expand(B, H, N, D)           # same query at every position
+    ref = F.scaled_dot_product_attention(qq, k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), is_causal=True,
+                                         scale=D ** -0.5)
+    _close(y, ref.permute(0, 2, 1, 3).numpy())
+
+
+@pytest.mark.parametrize("block,chunk,N", [(16, 16, 48), (32, 16, 64), (64, 32, 128)])
+def test_semi_ar_matches_block_sdpa(block, chunk, N):
+    B, H, M, D = 2, 3, 5, 16
+    q, k, v = seeded(12, B, N, H, M, D, D, torch.float32)
+    y, lse_dec, lse_enc = O.semi_ar(q, k, v, block, chunk)
+    _close(y, O.brute_semi_ar(q, k, v, block))
+    assert lse_dec.shape == (B, H, N) and lse_enc.shape == (B, H, N // block, M)
+    # LSE_dec = logsumexp_m of the decoder scores; LSE_enc = logsumexp over tokens < block end
+    S = (0.25 * np.einsum("bnhd,hmd->bhnm", k.double().numpy(), q.double().numpy()))
+    _close(lse_dec, np.log(np.exp(S).sum(-1)), 1e-5)
+    for g in range(N // block):
+        _close(lse_enc[:, :, g], np.log(np.exp(S[:, :, : (g + 1) * block]).sum(2)), 1e-5)
+
+
+def test_semi_ar_full_block_is_noncausal_flare():
+    B, N, H, M, D = 1, 32, 2, 8, 16
+    q, k, v = seeded(13, B, N, H, M, D, D, torch.float32)
+    y, _, _ = O.semi_ar(q, k, v, N, 16)
+    z = F.scaled_dot_product_attention(q[None].expand(B, H, M, D), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
+                                       scale=0.25)
+    ref = F.scaled_dot_product_attention(k.permute(0, 2, 1, 3), q[None].expand(B, H, M, D), z, scale=0.25)
+    _close(y, ref.permute(0, 2, 1, 3).numpy())
+
+
+def test_semi_ar_block_ends_equal_ar():
+    """The last token of each block sees exactly the causal prefix: semi-AR == AR there."""
+    B, N, H, M, D, blk = 2, 64, 2, 16, 16, 16
+    q, k, v = seeded(14, B, N, H, M, D, D, torch.float32)
+    ys, _, _ = O.semi_ar(q, k, v, blk, 16)
+    ya = O.ar_chunked(q, k, v, chunk_size=16)
+    _close(ys[:, blk - 1::blk], ya[:, blk - 1::blk])
+    assert np.abs(ys[:, 0] - ya[:, 0]).max() > 1e-3   # and not elsewhere
+
+
+def test_golden_fixtures():
+    files = sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))
+    assert files, "no golden fixtures"
+    for f in files:
+        with np.load(os.path.join(GOLDEN, f), allow_pickle=False) as z:
+            kind = str(z["kind"])
+            q, k, v = z["q"], z["k"], z["v"]
+            if kind == "ar":
+                y = O.ar_chunked(q, k, v, scale=float(z["scale"]), chunk_size=int(z["chunk"]))
+            elif kind == "semi":
+                y, _, _ = O.semi_ar(q, k, v, int(z["block"]), 16, scale=float(z["scale"]))
+            else:
+                y, _ = O.ar_recurrent(q, k, v, scale=float(z["scale"]))
+            _close(y, z["y"], 3e-5)
