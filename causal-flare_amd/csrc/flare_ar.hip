@@ -333,6 +333,8 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum,
                           hipStream_t stream) {
+    if ((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv))
+        return launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, stream);
     FLARE_REQUIRE(Dv <= 4 * kPrepCols, "chunk_prepare: Dv=%lld exceeds %d", (long long)Dv, 4 * kPrepCols);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)((M + kPrepMT - 1) / kPrepMT));
@@ -378,6 +380,9 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          const float* pden, const float* pnum, void* Y, int out_dtype,
                          float* lse_dec, hipStream_t stream) {
     const bool shared = Qdec == nullptr && Kdec == nullptr;
+    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr &&
+        mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv))
+        return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, stream);
     const int DT = pick_dt(M, Dv);
     FLARE_REQUIRE(DT > 0, "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
                   (long long)M, (long long)Dv);

@@ -5,3 +5,31 @@
 namespace flare {
 int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 }
+
+#include <hip/hip_runtime.h>
+#include <stdlib.h>
+
+namespace flare {
+bool mfma_prepare_supported(int dtype, int64_t M, int64_t Dk, int64_t Dv);
+bool mfma_output_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv);
+int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
+                        int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
+                        float* cnum, hipStream_t stream);
+int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
+                       int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
+                       const float* pden, const float* pnum, void* Y, int out_dtype, hipStream_t stream);
+
+// FLARE_DISABLE_MFMA=1 routes every shape to the scalar-fp32 kernels (A/B checks);
+// FLARE_MFMA_PHASES=<bits> keeps the MFMA kernel only for phase 1 (bit 0) and/or
+// phase 3 (bit 1).  Both are read once per process.
+inline int mfma_phase_mask() {
+    static const int mask = [] {
+        const char* e = getenv("FLARE_DISABLE_MFMA");
+        if (e && e[0] == '1') return 0;
+        const char* p = getenv("FLARE_MFMA_PHASES");
+        return p ? atoi(p) : 3;
+    }();
+    return mask;
+}
+inline bool mfma_enabled() { return mfma_phase_mask() != 0; }
+}  // namespace flare

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import flare_oracle as O
-from _util import assert_parity, seeded, to_np
+from _util import assert_noise_model, assert_parity, assert_state_parity, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -169,7 +169,7 @@ def test_decode_continuation_equals_prefill_of_concatenation(dtype):
     assert_parity(y_cat.float(), y_all.float(), dtype, "continuation y")
     ref, st_ref = O.ar_recurrent(q, k, v)
     assert_parity(y_all, ref, dtype, "prefill vs oracle")
-    assert_parity(st["u"], st_ref["u"], torch.float32 if dtype == torch.float32 else dtype, "continued state u")
+    assert_state_parity(st, st_ref, dtype, "continued")
 
 
 def test_prefill_with_initial_state_and_mask():
@@ -216,7 +216,7 @@ def test_cfg4_decode_bf16():
     ref, st_ref = O.ar_recurrent(q, k, v, nthreads=16)
     assert_parity(y, ref[:, :T], torch.bfloat16, "cfg4 prefill")
     assert_parity(y_dec, ref[:, T:], torch.bfloat16, "cfg4 decode")
-    assert_parity(st["u"], st_ref["u"], torch.bfloat16, "cfg4 state u")
+    assert_state_parity(st, st_ref, torch.bfloat16, "cfg4")
 
 
 def test_decode_masked_rows_keep_state():
@@ -290,3 +290,64 @@ def test_semi_ar_full_block_equals_noncausal_flare():
     y, _ = flare_semi_autoregressive_trition(q, k, v, block_size=N, chunk_size=64)
     ref = O.brute_semi_ar(q, k, v, N)
     assert_parity(y, ref, torch.float32, "semi block=N")
+
+
+# --------------------------------------------------------------------------
+# Shapes served by the bf16 MFMA kernels (M in {128, 256}, D in {64, 128})
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("M,D", [(128, 64), (128, 128), (256, 64), (256, 128)])
+@pytest.mark.parametrize("N,chunk", [(77, None), (1000, 64), (1000, 96), (3000, None)])
+def test_mfma_shapes_bf16(M, D, N, chunk):
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_shapes", M, D, N, chunk)
+    B, H = 2, 2
+    q, k, v = seeded(31 + M + D, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5, device=DEV)
+    y = flare_autoregressive_triton(q, k, v, chunk_size=chunk)
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    assert_parity(y, ref, torch.bfloat16, f"mfma M={M} D={D} N={N} chunk={chunk}")
+
+
+@pytest.mark.parametrize("qk_std", [1.0, 3.0])
+def test_mfma_prefill_with_state_bf16(qk_std):
+    """Prefill from a cached state on the MFMA path, with larger score spreads."""
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("mfma_prefill_state", qk_std)
+    B, T, H, M, D = 2, 700, 2, 128, 64
+    q, k, v = seeded(77, B, 2 * T, H, M, D, D, torch.bfloat16, q_std=qk_std * D ** -0.5, device=DEV)
+    scale = 1.0
+    _, st = flare_autoregressive_prefill_triton(q, k[:, :T], v[:, :T], scale=scale)
+    y, st2 = flare_autoregressive_prefill_triton(q, k[:, T:], v[:, T:], state=st, scale=scale)
+    y_ref, st_ref = O.ar_recurrent(q, k, v, scale=scale, nthreads=16)
+    if qk_std <= 1.0:
+        assert_parity(y, y_ref[:, T:], torch.bfloat16, "mfma prefill with state")
+        assert_state_parity(st2, st_ref, torch.bfloat16, "mfma prefill")
+    else:   # sharp softmax: bf16 rounding dominates; the reference suite's noise-model policy
+        assert_noise_model(y, y_ref[:, T:], "mfma prefill with state (sharp)")
+        z = to_np(st2["u"]) / to_np(st2["d"])[..., None]
+        assert_noise_model(z, st_ref["u"] / st_ref["d"][..., None], "mfma prefill state z (sharp)")
+    y1, _ = flare_autoregressive_decode_triton(q, k[:, -1], v[:, -1], state=st2, scale=scale)
+    assert torch.isfinite(y1.float()).all()
+
+
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("qk_std", [0.5, 1.0, 2.0, 4.0])
+@pytest.mark.parametrize("dec_mode", ["shared", "sep_q", "sep_k"])
+def test_reference_correctness_suite_bf16(D, qk_std, dec_mode):
+    """The reference's bf16 correctness sweep (testing/suite_runners/correctness.py:33-113):
+    B=1, H=2, N=1024, M=128, q,k ~ qk_std N(0,1), scale D^-0.5, against the
+    fp64 two-SDPA definition.  D=64 runs the MFMA kernels (shared decoder)."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("ref_suite", D, qk_std, dec_mode)
+    B, H, N, M = 1, 2, 1024, 128
+    g = torch.Generator().manual_seed(int(100 * qk_std) + D)
+    q = (qk_std * torch.randn(H, M, D, generator=g)).bfloat16()
+    k = (qk_std * torch.randn(B, N, H, D, generator=g)).bfloat16()
+    v = torch.randn(B, N, H, D, generator=g).bfloat16()
+    qd = (qk_std * torch.randn(B, N, H, D, generator=g)).bfloat16() if dec_mode == "sep_q" else None
+    kd = (qk_std * torch.randn(H, M, D, generator=g)).bfloat16() if dec_mode == "sep_k" else None
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), scale=D ** -0.5,
+                                    Q_dec=None if qd is None else qd.to(DEV), K_dec=None if kd is None else kd.to(DEV))
+    ref = O.brute_ar(q, k, v, scale=D ** -0.5, Q_dec=qd, K_dec=kd)
+    assert_noise_model(y, ref, f"suite D={D} qk={qk_std} {dec_mode}")
+    if qk_std <= 1.0:
+        assert_parity(y, ref, torch.bfloat16, f"suite D={D} qk={qk_std} {dec_mode}")
