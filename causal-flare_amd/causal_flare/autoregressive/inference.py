@@ -238,8 +238,8 @@ def flare_autoregressive_prefill_triton(
 
     _require_gpu("flare_autoregressive_prefill", Q, K, V)
     st = None if state is None else _canonicalize_flare_state(state, B, H, M, D_value, K.device)
-    if st is not None:
-        st = {k: v.contiguous() for k, v in st.items()}
+    if st is not None:   # contiguous and 16-byte aligned (the scan reads u with 16-byte loads)
+        st = {k: (v.contiguous() if v.data_ptr() % 16 == 0 else v.contiguous().clone()) for k, v in st.items()}
     _, chunk = _resolve_chunk_size(None, B, T, H, M, D_value)
     qd, kd = (None, None) if shared else _decoder_args(Q, K, Q_dec, K_dec, sep_q, sep_k)
     profile_data = {"forward": {}} if profile else None

@@ -113,76 +113,66 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Phase 2.  grid = B*H*M workgroups of one wavefront; lane owns value columns
-// lane, lane+64, ... (Dv <= 256).  Summaries are overwritten in place by the
-// exclusive prefix; the next chunk's summary is loaded before the current
-// merge so the serial chain does not wait on memory.
+// Phase 2.  One thread per (b*h, latent, 4 value columns); 256-thread
+// workgroups.  A bandwidth kernel: every summary is read once and overwritten
+// in place by the exclusive prefix with 16-byte accesses.  The (max, den) pair
+// of a latent is re-derived by each of its Dv/4 threads (cheap, keeps the
+// kernel free of cross-thread traffic).  Chunks are loaded kScanBatch at a time
+// before their serial merges run, so one memory latency covers kScanBatch
+// merges.
 // ---------------------------------------------------------------------------
-constexpr int kScanCols = 4;
+constexpr int kScanBatch = 8;
 
-__global__ __launch_bounds__(64) void chunk_prefix_kernel(
+__global__ __launch_bounds__(256) void chunk_prefix_kernel(
     float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum, int NC, int M,
-    int Dv, const float* __restrict__ m0, const float* __restrict__ d0,
+    int Dv, int rows, const float* __restrict__ m0, const float* __restrict__ d0,
     const float* __restrict__ u0, float* __restrict__ m_fin, float* __restrict__ d_fin,
     float* __restrict__ u_fin) {
-    const int row = blockIdx.x;  // bh * M + m
+    const int D4 = Dv >> 2;
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * D4) return;
+    const int row = gid / D4, j = gid % D4;    // row = bh * M + m, value columns 4j .. 4j+3
     const int bh = row / M, m = row % M;
-    const int lane = threadIdx.x;
     float mc = m0 ? m0[row] : kNegInf;
     float dc = d0 ? d0[row] : 0.0f;
-    float uc[kScanCols];
+    float4 uc = u0 ? reinterpret_cast<const float4*>(u0)[(size_t)row * D4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const size_t base = (size_t)bh * NC * M + m;          // summary index of chunk 0
+    float4* num4 = reinterpret_cast<float4*>(cnum);
+    for (int c0 = 0; c0 < NC; c0 += kScanBatch) {
+        float bm[kScanBatch], bd[kScanBatch];
+        float4 bu[kScanBatch];
 #pragma unroll
-    for (int k = 0; k < kScanCols; ++k) {
-        const int col = lane + 64 * k;
-        uc[k] = (u0 && col < Dv) ? u0[(size_t)row * Dv + col] : 0.0f;
-    }
-    auto sidx = [&](int c) { return ((size_t)bh * NC + c) * M + m; };
-    float nm = cmax[sidx(0)], nd = cden[sidx(0)];
-    float nu[kScanCols];
+        for (int i = 0; i < kScanBatch; ++i) {
+            const bool in = c0 + i < NC;
+            const size_t si = base + (size_t)(c0 + i) * M;
+            bm[i] = in ? cmax[si] : kNegInf;
+            bd[i] = in ? cden[si] : 0.0f;
+            bu[i] = in ? num4[si * D4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
 #pragma unroll
-    for (int k = 0; k < kScanCols; ++k) {
-        const int col = lane + 64 * k;
-        nu[k] = col < Dv ? cnum[sidx(0) * Dv + col] : 0.0f;
-    }
-    for (int c = 0; c < NC; ++c) {
-        const float cm = nm, cd = nd;
-        float cu[kScanCols];
-#pragma unroll
-        for (int k = 0; k < kScanCols; ++k) cu[k] = nu[k];
-        if (c + 1 < NC) {
-            nm = cmax[sidx(c + 1)];
-            nd = cden[sidx(c + 1)];
-#pragma unroll
-            for (int k = 0; k < kScanCols; ++k) {
-                const int col = lane + 64 * k;
-                nu[k] = col < Dv ? cnum[sidx(c + 1) * Dv + col] : 0.0f;
+        for (int i = 0; i < kScanBatch; ++i) {
+            if (c0 + i >= NC) break;
+            const size_t si = base + (size_t)(c0 + i) * M;
+            if (j == 0) {
+                cmax[si] = mc;
+                cden[si] = dc;
             }
+            num4[si * D4 + j] = uc;
+            const MergeScales ms = merge_scales(mc, bm[i]);
+            dc = dc * ms.sa + bd[i] * ms.sb;
+            uc.x = uc.x * ms.sa + bu[i].x * ms.sb;
+            uc.y = uc.y * ms.sa + bu[i].y * ms.sb;
+            uc.z = uc.z * ms.sa + bu[i].z * ms.sb;
+            uc.w = uc.w * ms.sa + bu[i].w * ms.sb;
+            mc = ms.m_new;
         }
-        if (lane == 0) {
-            cmax[sidx(c)] = mc;
-            cden[sidx(c)] = dc;
-        }
-#pragma unroll
-        for (int k = 0; k < kScanCols; ++k) {
-            const int col = lane + 64 * k;
-            if (col < Dv) cnum[sidx(c) * Dv + col] = uc[k];
-        }
-        const MergeScales ms = merge_scales(mc, cm);
-        dc = dc * ms.sa + cd * ms.sb;
-#pragma unroll
-        for (int k = 0; k < kScanCols; ++k) uc[k] = uc[k] * ms.sa + cu[k] * ms.sb;
-        mc = ms.m_new;
     }
     if (m_fin) {
-        if (lane == 0) {
+        if (j == 0) {
             m_fin[row] = mc;
             d_fin[row] = dc;
         }
-#pragma unroll
-        for (int k = 0; k < kScanCols; ++k) {
-            const int col = lane + 64 * k;
-            if (col < Dv) u_fin[(size_t)row * Dv + col] = uc[k];
-        }
+        reinterpret_cast<float4*>(u_fin)[(size_t)row * D4 + j] = uc;
     }
 }
 
@@ -354,12 +344,15 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
 static int launch_prefix(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M,
                          int64_t Dv, const float* m0, const float* d0, const float* u0,
                          float* m_fin, float* d_fin, float* u_fin, hipStream_t stream) {
-    FLARE_REQUIRE(Dv <= 64 * kScanCols, "chunk_prefix: Dv=%lld exceeds %d", (long long)Dv, 64 * kScanCols);
+    FLARE_REQUIRE(Dv % 4 == 0, "chunk_prefix: Dv=%lld must be a multiple of 4", (long long)Dv);
+    FLARE_REQUIRE((((uintptr_t)cnum) & 15) == 0 && (!u0 || (((uintptr_t)u0) & 15) == 0) &&
+                  (!u_fin || (((uintptr_t)u_fin) & 15) == 0), "chunk_prefix: numerators must be 16-byte aligned");
     FLARE_REQUIRE((m0 && d0 && u0) || (!m0 && !d0 && !u0), "chunk_prefix: give all of m0/d0/u0 or none");
     FLARE_REQUIRE((m_fin && d_fin && u_fin) || (!m_fin && !d_fin && !u_fin),
                   "chunk_prefix: give all of m_fin/d_fin/u_fin or none");
-    hipLaunchKernelGGL(chunk_prefix_kernel, dim3((unsigned)(BH * M)), dim3(64), 0, stream, cmax, cden,
-                       cnum, (int)NC, (int)M, (int)Dv, m0, d0, u0, m_fin, d_fin, u_fin);
+    const int64_t threads = BH * M * (Dv / 4);
+    hipLaunchKernelGGL(chunk_prefix_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream, cmax,
+                       cden, cnum, (int)NC, (int)M, (int)Dv, (int)(BH * M), m0, d0, u0, m_fin, d_fin, u_fin);
     return check_launch("chunk_prefix_kernel");
 }
 

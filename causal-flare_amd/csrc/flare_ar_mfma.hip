@@ -59,6 +59,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.0f;            // log2 headroom before a reference max moves
 constexpr float kF16Max = 65504.0f;
+constexpr int kMaxPrepM = 256;           // latent bank held in LDS by the prepare kernel
 
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -190,7 +191,9 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
     constexpr int KS = D / 32;     // k-steps for the scores
     constexpr int DT = D / 16;     // value-column tiles
     constexpr int VP = T + 8;      // padded row of the transposed V tile
+    constexpr int QP = D + 8;      // padded row of Q in LDS
     __shared__ __attribute__((aligned(16))) f16 vtl[D * VP];
+    __shared__ __attribute__((aligned(16))) bf16 qsh[kMaxPrepM * QP];  // Q[h], M rows
     __shared__ int vbig;
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
@@ -201,12 +204,9 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
     const int g = lane >> 4, c = lane & 15;
     const int m0 = 32 * w;                       // this wave's 32 latents
 
-    bf16x8 qb[2][KS];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-        const bf16* qrow = Q + ((size_t)h * M + m0 + 16 * mt + c) * D;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qb[mt][ks] = load8<bf16x8>(qrow + 32 * ks + 8 * g);
+    for (int vi = tid; vi < M * D / 8; vi += nthr) {
+        const int m = vi / (D / 8), d8 = vi % (D / 8);
+        *reinterpret_cast<bf16x8*>(qsh + m * QP + 8 * d8) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * d8);
     }
     f32x4 U[2][DT];
 #pragma unroll
@@ -221,6 +221,16 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
     if (tid == 0) vbig = 0;
+    // K rows of the first subtile (A operands of S = K Q^T); each iteration
+    // prefetches the next subtile's rows while it works on the current one.
+    bf16x8 ka[2][KS];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        const int t = t_begin + 16 * ti + c;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+            ka[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
+    }
     for (int t0 = t_begin; t0 < t_end; t0 += T) {
         __syncthreads();
         if (stage_vt_f16<VP>(vtl, V, row0, stride, t0, t_end, 0, D, tid, nthr)) vbig = 1;
@@ -231,14 +241,19 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
+            for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)   // B operand: Q rows of this wave's latents
+                        acc[mt][ti] = mma(ka[ti][ks], load8<bf16x8>(qsh + (m0 + 16 * mt + c) * QP + 32 * ks + 8 * g),
+                                          acc[mt][ti]);
+#pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
-                const int t = t0 + 16 * ti + c;
+                const int t = t0 + T + 16 * ti + c;
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks) {
-                    const bf16x8 ka = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
-#pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka, qb[mt][ks], acc[mt][ti]);
-                }
+                for (int ks = 0; ks < KS; ++ks)
+                    ka[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
             }
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -424,6 +439,16 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     const int t_end = min(N, t_begin + chunk);
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
+    // K rows of the first subtile (B operands of S^T = Q K^T); each iteration
+    // prefetches the next subtile's rows right after its scores are formed.
+    bf16x8 kb[2][L::KS];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        const int t = t_begin + 16 * ti + c;
+#pragma unroll
+        for (int ks = 0; ks < L::KS; ++ks)
+            kb[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
+    }
     for (int t0 = t_begin; t0 < t_end; t0 += T) {
         // ---- V^T of this wave's value columns (wave-private rows of vtl), fp16
         const bool vbig = __any(stage_vt_f16<L::EP>(vtl, V, row0, stride, t0, t_end, dw0, L::DW, lane, 64));
@@ -435,18 +460,19 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             for (int mi = 0; mi < L::MT; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < L::KS; ++ks) {
-                bf16x8 kb[2];
-#pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    const int t = t0 + 16 * ti + c;
-                    kb[ti] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
-                }
 #pragma unroll
                 for (int mi = 0; mi < L::MT; ++mi) {
                     const bf16x8 qa = load8<bf16x8>(qs + (mw0 + 16 * mi + c) * L::QP + 32 * ks + 8 * g);
 #pragma unroll
-                    for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa, kb[ti], acc[mi][ti]);
+                    for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa, kb[ti][ks], acc[mi][ti]);
                 }
+            }
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti) {
+                const int t = t0 + T + 16 * ti + c;
+#pragma unroll
+                for (int ks = 0; ks < L::KS; ++ks)
+                    kb[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
             }
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi)
@@ -754,7 +780,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 using namespace mfma;
 
 bool mfma_prepare_supported(int dtype, int64_t M, int64_t Dk, int64_t Dv) {
-    return dtype == FLARE_BF16 && Dk == Dv && (Dk == 64 || Dk == 128) && M % 32 == 0 && M >= 32 && M <= 256;
+    return dtype == FLARE_BF16 && Dk == Dv && (Dk == 64 || Dk == 128) && M % 32 == 0 && M >= 32 && M <= kMaxPrepM;
 }
 
 bool mfma_output_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv) {
