@@ -416,6 +416,12 @@ int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype
     return launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, stream);
 }
 
+int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M, int64_t Dv,
+                         const float* m0, const float* d0, const float* u0, float* m_fin, float* d_fin,
+                         float* u_fin, hipStream_t stream) {
+    return launch_prefix(cmax, cden, cnum, BH, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, stream);
+}
+
 int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
     // Enough chunks to give every CU several workgroups, each chunk a multiple
     // of 64 tokens and at most 2048 long.

@@ -1,0 +1,145 @@
+// flare_mfma.h -- device helpers shared by the gfx950 MFMA kernels: operand
+// types, 16x16x32 bf16/fp16 MFMA wrappers, hi/lo splits, DPP row reductions and
+// the transposed V staging used by every chunk kernel.
+#pragma once
+
+#include "flare_common.h"
+
+namespace flare {
+namespace mfma {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int T = 32;       // tokens per subtile (= the MFMA K depth)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazy = 8.0f;            // log2 headroom before a reference max moves
+constexpr float kF16Max = 65504.0f;
+constexpr int kMaxPrepM = 256;           // latent bank held in LDS by the prepare kernel
+
+__device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// x = hi + lo, both halves of type TY.
+#define SPLIT2(TY, x, HI, LO)              \
+    do {                                   \
+        const float _x = (x);              \
+        const TY _h = (TY)_x;              \
+        HI = _h;                           \
+        LO = (TY)(_x - (float)_h);         \
+    } while (0)
+
+// DPP moves inside a 16-lane row.  Lanes whose source is outside the row read 0.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kQuadXor1 = 0xB1;       // quad_perm(1,0,3,2)
+constexpr int kQuadXor2 = 0x4E;       // quad_perm(2,3,0,1)
+constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowMirror = 0x140;
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+
+__device__ __forceinline__ float row_max16(float x) {
+    x = fmaxf(x, dpp<kQuadXor1>(x));
+    x = fmaxf(x, dpp<kQuadXor2>(x));
+    x = fmaxf(x, dpp<kRowHalfMirror>(x));
+    x = fmaxf(x, dpp<kRowMirror>(x));
+    return x;
+}
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp<kQuadXor1>(x);
+    x += dpp<kQuadXor2>(x);
+    x += dpp<kRowHalfMirror>(x);
+    x += dpp<kRowMirror>(x);
+    return x;
+}
+// Inclusive prefix sum over the 16 lanes of a row (Hillis-Steele).
+__device__ __forceinline__ float row_scan16(float x) {
+    x += dpp<kRowShr1>(x);
+    x += dpp<kRowShr2>(x);
+    x += dpp<kRowShr4>(x);
+    x += dpp<kRowShr8>(x);
+    return x;
+}
+// max / sum over the four 16-lane rows (lanes c, c+16, c+32, c+48)
+__device__ __forceinline__ float rows_max4(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16, 64));
+    return fmaxf(x, __shfl_xor(x, 32, 64));
+}
+__device__ __forceinline__ float rows_sum4(float x) {
+    x += __shfl_xor(x, 16, 64);
+    return x + __shfl_xor(x, 32, 64);
+}
+
+template <typename V8, typename V4>
+__device__ __forceinline__ V8 cat8(V4 lo, V4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+template <typename V8, typename E>
+__device__ __forceinline__ V8 load8(const E* p) { return *reinterpret_cast<const V8*>(p); }
+template <typename V4, typename E>
+__device__ __forceinline__ V4 load4(const E* p) { return *reinterpret_cast<const V4*>(p); }
+__device__ __forceinline__ bf16x8 zero8() {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+    return z;
+}
+
+__device__ __forceinline__ void store4(void* Y, size_t idx, f32x4 v, int out_dtype) {
+    if (out_dtype == FLARE_BF16) {
+        bf16x4 o;
+        o[0] = (bf16)v[0]; o[1] = (bf16)v[1]; o[2] = (bf16)v[2]; o[3] = (bf16)v[3];
+        *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(Y) + idx) = o;
+    } else {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(Y) + idx) = v;
+    }
+}
+
+// Stage V^T[d][tau] for the value columns [d0, d0+nd) of one subtile into LDS
+// as fp16 (row pitch P).  Threads [0, nthr) of the group take part.  Returns
+// whether this thread saw a value outside the fp16 range.
+template <int P>
+__device__ __forceinline__ bool stage_vt_f16(f16* vt, const bf16* V, size_t row0, size_t stride, int t0,
+                                             int t_end, int d0, int nd, int tid, int nthr) {
+    bool big = false;
+    for (int vi = tid; vi < T * nd / 8; vi += nthr) {
+        const int tau = vi / (nd / 8), d8 = vi % (nd / 8);
+        const int t = t0 + tau;
+        const bf16x8 v = t < t_end ? load8<bf16x8>(V + row0 + (size_t)t * stride + d0 + 8 * d8) : zero8();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = (float)v[e];
+            big |= fabsf(x) > kF16Max;
+            vt[(d0 + 8 * d8 + e) * P + tau] = (f16)x;
+        }
+    }
+    return big;
+}
+// Same, bf16 (used only when a subtile holds a value outside the fp16 range).
+template <int P>
+__device__ __forceinline__ void stage_vt_bf16(bf16* vt, const bf16* V, size_t row0, size_t stride, int t0,
+                                              int t_end, int d0, int nd, int tid, int nthr) {
+    for (int vi = tid; vi < T * nd / 8; vi += nthr) {
+        const int tau = vi / (nd / 8), d8 = vi % (nd / 8);
+        const int t = t0 + tau;
+        const bf16x8 v = t < t_end ? load8<bf16x8>(V + row0 + (size_t)t * stride + d0 + 8 * d8) : zero8();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = v[e];
+    }
+}
+
+}  // namespace mfma
+}  // namespace flare

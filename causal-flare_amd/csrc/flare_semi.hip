@@ -157,6 +157,24 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
     float* bden = (float*)(ws + align(per * sizeof(float)));
     float* bnum = (float*)(ws + 2 * align(per * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
+    const bool shared = Qdec == nullptr && Kdec == nullptr;
+    if ((mfma_phase_mask() & 3) == 3 && mfma_semi_supported(dtype, out_dtype, shared, M, Dk, Dv, block) &&
+        mfma_prepare_supported(dtype, M, Dk, Dv)) {
+        // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
+        // block-causal MFMA readout.  The summaries fit in the workspace since
+        // chunks are never shorter than blocks.
+        int64_t chunk = default_chunk(B, N, H, M, Dv);
+        chunk = ((chunk + block - 1) / block) * block;
+        if (chunk > N) chunk = N;
+        const int64_t NC = (N + chunk - 1) / chunk;
+        int rc = launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, bmax, bden, bnum, s);
+        if (rc) return rc;
+        rc = launch_prefix_public(bmax, bden, bnum, B * H, NC, M, Dv, nullptr, nullptr, nullptr, nullptr,
+                                  nullptr, nullptr, s);
+        if (rc) return rc;
+        return launch_semi_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, block, bmax, bden, bnum, Y,
+                                       out_dtype, lse_dec, lse_enc, s);
+    }
     int rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, block, bmax, bden, bnum, s);
     if (rc) return rc;
     hipLaunchKernelGGL(semi_scan_z_kernel, dim3((unsigned)(B * H * M)), dim3(64), 0, s, bmax, bden,

@@ -351,3 +351,19 @@ def test_reference_correctness_suite_bf16(D, qk_std, dec_mode):
     assert_noise_model(y, ref, f"suite D={D} qk={qk_std} {dec_mode}")
     if qk_std <= 1.0:
         assert_parity(y, ref, torch.bfloat16, f"suite D={D} qk={qk_std} {dec_mode}")
+
+
+@pytest.mark.parametrize("M,D", [(128, 64), (128, 128), (256, 64), (256, 128)])
+@pytest.mark.parametrize("block", [32, 64, 128])
+def test_semi_ar_mfma_shapes_bf16(M, D, block):
+    """Shapes served by the block-causal MFMA readout (block 128 only for M = 128)."""
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_mfma", M, D, block)
+    B, N, H = 2, 1024, 2
+    q, k, v = seeded(91 + M + D + block, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5, device=DEV)
+    y, aux = flare_semi_autoregressive_trition(q, k, v, block_size=block, chunk_size=32)
+    y_ref, lse_dec, lse_enc = O.semi_ar(q, k, v, block, 32, nthreads=16)
+    assert y.dtype == torch.bfloat16
+    assert_parity(y, y_ref, torch.bfloat16, f"semi mfma M={M} D={D} block={block}")
+    np.testing.assert_allclose(to_np(aux["LSE_dec"]), lse_dec, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(to_np(aux["LSE_enc"]), lse_enc, rtol=1e-4, atol=1e-4)
