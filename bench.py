@@ -79,12 +79,21 @@ def bench_prefill(torch, flare, steps, warmup):
         "roofline": {
             "bound": "mfma", "kernel": "chunk_output_kernel", "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": None, "whole_pass_tflops": whole, "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
+            "traffic": measured_traffic("chunk_output_mfma"), "whole_pass_tflops": whole,
+            "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
         },
     }
 
 
 def bench_decode(torch, flare, steps=256):
+    """Config 4: 64 sequences, 2048-token prefill, then `steps` decode steps with fresh k, v.
+
+    Two loops over the same steps: the eager Python API loop (one
+    flare_autoregressive_decode_triton call per step) and the same calls
+    captured once in a HIP graph and replayed (back-to-back kernels, no Python
+    between steps).  The state is reset from the prefill result before each
+    timed run, outside the timed region.
+    """
     dev = torch.device("cuda:0")
     torch.manual_seed(3)
     B, T, H, M, D = 64, 2048, 16, 128, 64
@@ -94,39 +103,100 @@ def bench_decode(torch, flare, steps=256):
     kd = torch.randn(steps, B, H, D).to(torch.bfloat16).to(dev)
     vd = torch.randn(steps, B, H, D).to(torch.bfloat16).to(dev)
     _, base = flare.flare_autoregressive_prefill_triton(q, k, v)
+    st = {kk: vv.clone() for kk, vv in base.items()}
 
-    def run():
-        st = {kk: vv.clone() for kk, vv in base.items()}
+    def reset():
+        for kk in st:
+            st[kk].copy_(base[kk])
         torch.cuda.synchronize()
+
+    def eager():
+        reset()
         t0 = time.perf_counter()
         for s in range(steps):
-            y, st = flare.flare_autoregressive_decode_triton(q, kd[s], vd[s], state=st)
+            flare.flare_autoregressive_decode_triton(q, kd[s], vd[s], state=st)
         torch.cuda.synchronize()
         return time.perf_counter() - t0
 
-    run()
-    dt = min(run() for _ in range(3))
-    # kernel-only time: events around one launch, averaged
-    st = {kk: vv.clone() for kk, vv in base.items()}
-    acc = 0.0
-    reps = 32
-    for s in range(reps):
-        (_, st), prof = flare.flare_autoregressive_decode_triton(q, kd[s], vd[s], state=st, profile=True)
-        acc += prof["forward"]["flare_autoregressive_decode_step"]
-    k_ms = acc / reps
+    eager()
+    dt_eager = min(eager() for _ in range(3))
+    # graph capture of the same step loop
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for s in range(3):
+            flare.flare_autoregressive_decode_triton(q, kd[s], vd[s], state=st)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for s in range(steps):
+            flare.flare_autoregressive_decode_triton(q, kd[s], vd[s], state=st)
+    times = []
+    for _ in range(5):
+        reset()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / 1e3)
+    dt_graph = min(times)
+    k_ms = dt_graph * 1e3 / steps
     state_bytes = 2 * (8 * M + 4 * M * D) * B * H
     io_bytes = B * H * D * 2 * 3 + H * M * D * 2
     bytes_step = state_bytes + io_bytes
     achieved = bytes_step / (k_ms * 1e-3) / 1e9
     return {
         "B": B, "H": H, "M": M, "D": D, "prefill_T": T, "steps": steps,
-        "tok_s": B * steps / dt, "ms_per_step": dt * 1e3 / steps, "kernel_ms": k_ms,
+        "tok_s": B * steps / dt_graph, "ms_per_step": k_ms,
+        "tok_s_eager_api_loop": B * steps / dt_eager, "ms_per_step_eager": dt_eager * 1e3 / steps,
         "roofline": {
             "bound": "hbm", "kernel": "decode_step_kernel", "achieved": achieved,
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
             "alg_bytes_per_step": bytes_step,
+            "note": "graph replay of 256 back-to-back steps; per-step time includes launch gaps",
         },
     }
+
+
+def bench_others(torch, flare):
+    """Informational timings of configs 2 and 5 (their parity is tested, they are not the headline)."""
+    def inputs(seed, B, N, H, M, D):
+        torch.manual_seed(seed)
+        q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16).cuda()
+        return q, torch.randn(B, N, H, D).to(torch.bfloat16).cuda(), torch.randn(B, N, H, D).to(torch.bfloat16).cuda()
+
+    def timed(fn, reps=20):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    out = {}
+    q, k, v = inputs(1, 4, 4096, 16, 128, 64)
+    dt = timed(lambda: flare.flare_autoregressive_triton(q, k, v))
+    out["config2_prefill"] = {"ms": dt * 1e3, "tok_s": 4 * 4096 / dt,
+                              "tflops_alg": 6 * 128 * 64 * 4 * 4096 * 16 / dt / 1e12}
+    q, k, v = inputs(4, 2, 8192, 16, 128, 64)
+    dt = timed(lambda: flare.flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=64))
+    out["config5_semi_ar"] = {"ms": dt * 1e3, "tok_s": 2 * 8192 / dt,
+                              "tflops_alg": 6 * 128 * 64 * 2 * 8192 * 16 / dt / 1e12}
+    return out
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprof PMC summary, if present."""
+    path = os.path.join(ROOT, "profiles", "traffic_cfg3_prefill.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) >= 2 and parts[0] == kernel + ":":
+            return float(parts[1])
+    return None
 
 
 def cpu_baseline():
@@ -155,6 +225,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="finish with a plain 1 GiB device-to-device copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: the causal FLARE hot path here is a single-GPU kernel "
@@ -165,6 +237,7 @@ def main():
 
     pre = bench_prefill(torch, flare, args.steps, args.warmup)
     dec = None if args.no_decode else bench_decode(torch, flare)
+    others = None if args.no_decode else bench_others(torch, flare)
     cpu = None if args.no_cpu else cpu_baseline()
     out = {
         "metric": "prefill tok/s (N=64k) & decode tok/s (B=64) on 1 MI355X; % of roofline",
@@ -185,9 +258,15 @@ def main():
         "roofline": pre["roofline"],
         "phase_ms": pre["phase_ms"],
         "decode": dec,
+        "other_configs": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
+    if args.calibration_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
 
 
 if __name__ == "__main__":
