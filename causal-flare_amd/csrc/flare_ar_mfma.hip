@@ -48,49 +48,54 @@ namespace flare {
 namespace mfma {
 
 // ---------------------------------------------------------------------------
-// Phase 1.  grid = (NC, B*H), M/32 waves.  Wave w owns latents 32w .. 32w+31
-// (two 16-latent tiles) and every value column.
+// Phase 1.  grid = (NC, B*H), NWP = M/32 waves.  Wave w owns latents
+// 32w .. 32w+31 (two 16-latent tiles; their Q rows stay in registers) and
+// every value column.  V and K of the next subtile are fetched while the
+// current one is processed; V^T is double-buffered in LDS so one barrier per
+// subtile suffices.  The per-latent maximum and den are kept per lane and
+// reduced over the four lanes of a latent only when a reference max moves
+// and at the end.
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(512) void chunk_prepare_mfma(
+template <int D, int NWP>
+__global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
-    int M, float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden,
-    float* __restrict__ cnum) {
+    float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum) {
+    constexpr int M = 32 * NWP;
+    constexpr int NT = 64 * NWP;
     constexpr int KS = D / 32;     // k-steps for the scores
     constexpr int DT = D / 16;     // value-column tiles
     constexpr int VP = T + 8;      // padded row of the transposed V tile
-    constexpr int QP = D + 8;      // padded row of Q in LDS
-    __shared__ __attribute__((aligned(16))) f16 vtl[D * VP];
-    __shared__ __attribute__((aligned(16))) bf16 qsh[kMaxPrepM * QP];  // Q[h], M rows
-    __shared__ int vbig;
+    __shared__ __attribute__((aligned(16))) f16 vtl[2][D * VP];
+    __shared__ int vbig[2];        // subtile index whose V^T buffer holds a value outside fp16
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
     const int NC = gridDim.x;
     const int b = bh / H, h = bh % H;
-    const int nthr = blockDim.x;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
     const int m0 = 32 * w;                       // this wave's 32 latents
 
-    for (int vi = tid; vi < M * D / 8; vi += nthr) {
-        const int m = vi / (D / 8), d8 = vi % (D / 8);
-        *reinterpret_cast<bf16x8*>(qsh + m * QP + 8 * d8) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * d8);
-    }
+    // B operands of S = K Q^T: Q rows of this wave's latents
+    bf16x8 qb[2][KS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qb[mt][ks] = load8<bf16x8>(Q + ((size_t)h * M + m0 + 16 * mt + c) * D + 32 * ks + 8 * g);
     f32x4 U[2][DT];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int di = 0; di < DT; ++di) U[mt][di] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // per latent m0 + 16 mt + c (replicated over the four rows g)
-    float R[2] = {kNegInf, kNegInf}, Rt[2] = {kNegInf, kNegInf}, den[2] = {0.f, 0.f};
+    // per latent m0 + 16 mt + c: R replicated over the four rows g; rt, dl per lane
+    float R[2] = {kNegInf, kNegInf}, rt[2] = {kNegInf, kNegInf}, dl[2] = {0.f, 0.f};
 
     const int t_begin = c_idx * chunk;
     const int t_end = min(N, t_begin + chunk);
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
-    if (tid == 0) vbig = 0;
-    // K rows of the first subtile (A operands of S = K Q^T); each iteration
-    // prefetches the next subtile's rows while it works on the current one.
+    if (tid < 2) vbig[tid] = -1;
+    VTile<D, NT> vt;
+    vt.load(V, row0, stride, t_begin, t_end, 0, tid);
     bf16x8 ka[2][KS];
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti) {
@@ -99,9 +104,12 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
         for (int ks = 0; ks < KS; ++ks)
             ka[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
     }
-    for (int t0 = t_begin; t0 < t_end; t0 += T) {
-        __syncthreads();
-        if (stage_vt_f16<VP>(vtl, V, row0, stride, t0, t_end, 0, D, tid, nthr)) vbig = 1;
+    __syncthreads();
+    int j = 0;
+    for (int t0 = t_begin; t0 < t_end; t0 += T, ++j) {
+        f16* vtj = vtl[j & 1];
+        if (vt.template store_f16<VP>(vtj, 0, tid)) vbig[j & 1] = j;
+        vt.load(V, row0, stride, t0 + T, t_end, 0, tid);
         // S = K Q^T, tokens as rows: s[mt][ti][r] = S[t = 16 ti + 4 g + r][m = 16 mt + c]
         float s[2][2][4];
         {
@@ -113,9 +121,7 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                    for (int mt = 0; mt < 2; ++mt)   // B operand: Q rows of this wave's latents
-                        acc[mt][ti] = mma(ka[ti][ks], load8<bf16x8>(qsh + (m0 + 16 * mt + c) * QP + 32 * ks + 8 * g),
-                                          acc[mt][ti]);
+                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka[ti][ks], qb[mt][ks], acc[mt][ti]);
 #pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
                 const int t = t0 + T + 16 * ti + c;
@@ -128,38 +134,38 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        s[mt][ti][r] = (t0 + 16 * ti + 4 * g + r < t_end) ? acc[mt][ti][r] * scale2 : kNegInf;
+                    for (int r = 0; r < 4; ++r) s[mt][ti][r] = acc[mt][ti][r] * scale2;
+            if (t0 + T > t_end) {      // the ragged last subtile
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (t0 + 16 * ti + 4 * g + r >= t_end) s[mt][ti][r] = kNegInf;
+            }
         }
-        // per-latent maxima (lazy reference), E, den
-        float e[2][2][4];
+        // lazy reference max: checked per lane, moved (exact max over the latent) rarely
+        float mx[2];
         bool need = false;
-        float gam[2];
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
-            float mx = kNegInf;
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[mt][ti][r]);
-            mx = rows_max4(mx);
-            Rt[mt] = fmaxf(Rt[mt], mx);
-            const bool mv = mx > R[mt] + kLazy;
-            need |= mv;
-            const float Rn = mv ? mx : R[mt];
-            gam[mt] = mv ? exp2f_fast(R[mt] - Rn) : 1.0f;     // 0 when R = -inf
-            R[mt] = Rn;
-            float es = 0.0f;
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    e[mt][ti][r] = exp2f_fast(s[mt][ti][r] - Rn);
-                    es += e[mt][ti][r];
-                }
-            den[mt] = den[mt] * gam[mt] + rows_sum4(es);
+            mx[mt] = fmaxf(fmaxf(fmaxf(s[mt][0][0], s[mt][0][1]), fmaxf(s[mt][0][2], s[mt][0][3])),
+                           fmaxf(fmaxf(s[mt][1][0], s[mt][1][1]), fmaxf(s[mt][1][2], s[mt][1][3])));
+            rt[mt] = fmaxf(rt[mt], mx[mt]);
+            need |= mx[mt] > R[mt] + kLazy;
         }
         if (__any(need)) {
+            float gam[2];
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float m4 = rows_max4(mx[mt]);
+                const bool mv = m4 > R[mt] + kLazy;
+                const float Rn = mv ? m4 : R[mt];
+                gam[mt] = mv ? exp2f_fast(R[mt] - Rn) : 1.0f;     // 0 when R = -inf
+                R[mt] = Rn;
+                dl[mt] *= gam[mt];
+            }
             // rows of U are latents 16 mt + 4 g + r: fetch their factors
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -170,8 +176,21 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
                     for (int di = 0; di < DT; ++di) U[mt][di][r] *= gr;
                 }
         }
-        __syncthreads();
-        if (!vbig) {
+        float e[2][2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            float es = 0.0f;
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    e[mt][ti][r] = exp2f_fast(s[mt][ti][r] - R[mt]);
+                    es += e[mt][ti][r];
+                }
+            dl[mt] += es;
+        }
+        __syncthreads();   // V^T of this subtile (and its range flag) visible
+        if (vbig[j & 1] != j) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
                 f16x8 ea;   // E^T[m = c][tau = pi(g, .)]
@@ -182,7 +201,7 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
                 }
 #pragma unroll
                 for (int di = 0; di < DT; ++di) {
-                    const f16* vr = vtl + (16 * di + c) * VP;
+                    const f16* vr = vtj + (16 * di + c) * VP;
                     const f16x8 vb = cat8<f16x8>(load4<f16x4>(vr + 4 * g), load4<f16x4>(vr + 16 + 4 * g));
                     U[mt][di] = mma(ea, vb, U[mt][di]);
                 }
@@ -190,10 +209,9 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
         } else {
             // a value outside the fp16 range: bf16 V and an exact hi/lo split of E
             __syncthreads();
-            bf16* vtb = reinterpret_cast<bf16*>(vtl);
-            stage_vt_bf16<VP>(vtb, V, row0, stride, t0, t_end, 0, D, tid, nthr);
+            bf16* vtb = reinterpret_cast<bf16*>(vtj);
+            stage_vt_bf16<VP>(vtb, V, row0, stride, t0, t_end, 0, D, tid, NT);
             __syncthreads();
-            if (tid == 0) vbig = 0;
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {
                 bf16x8 eh, el;
@@ -216,10 +234,12 @@ __global__ __launch_bounds__(512) void chunk_prepare_mfma(
     const size_t sbase = ((size_t)bh * NC + c_idx) * M;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
-        const float f = exp2f_fast(R[mt] - Rt[mt]);    // <= 1
+        const float Rt = rows_max4(rt[mt]);
+        const float den = rows_sum4(dl[mt]);
+        const float f = exp2f_fast(R[mt] - Rt);    // <= 1
         if (g == 0) {
-            cmax[sbase + m0 + 16 * mt + c] = Rt[mt] * kLn2;
-            cden[sbase + m0 + 16 * mt + c] = den[mt] * f;
+            cmax[sbase + m0 + 16 * mt + c] = Rt * kLn2;
+            cden[sbase + m0 + 16 * mt + c] = den * f;
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -244,10 +264,9 @@ struct OutLayout {
     static constexpr int DTW = DW / 16;      // value tiles per wave
     static constexpr int KS = D / 32;        // k-steps of the scores
     static constexpr int WP = M + 8;         // padded row of W1[t][m]
-    static constexpr int EP = T + 8;         // padded row of E^T[m][tau] and V^T[d][tau]
-    static constexpr int GP = T + 4;         // padded row of G^T [t][tau]
-    static constexpr int QP = D + 8;         // padded row of Q in LDS
-    static constexpr int GROWS = T / NW;     // rows of G each wave reduces
+    static constexpr int EP = T + 8;         // padded row of E^T[m][tau], V^T[d][tau], G^T[t][tau] (16-bit)
+    static constexpr int GP = 16 + 4;        // padded row of a 16x16 tile of the fp32 partials of G^T
+    static constexpr int KC = D / 8;         // 16-byte chunks of a K / Q row in LDS (XOR-swizzled slots)
     static_assert(MT % 2 == 0, "each wave needs an even number of latent tiles");
     static_assert(DW % 16 == 0, "value columns per wave must be a multiple of 16");
 };
@@ -259,15 +278,17 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype) {
     using L = OutLayout<M, D, NW>;
     __shared__ __attribute__((aligned(16))) f16 wl[T * L::WP];         // W1[t][m]
-    __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];        // E^T[m][tau]
-    __shared__ __attribute__((aligned(16))) f16 vtl[D * L::EP];        // V^T[d][tau] (bf16 when moved)
-    __shared__ __attribute__((aligned(16))) float gpl[NW * T * L::GP]; // partial G^T[t][tau] per wave
-    __shared__ __attribute__((aligned(16))) float gfl[T * L::GP];      // reduced G^T[t][tau]
-    __shared__ __attribute__((aligned(16))) float lsep[NW * T * 2];    // (max, sum) per wave/token
+    __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];        // E^T[m][tau] (fp16)
+    __shared__ __attribute__((aligned(16))) f16 vtl[D * L::EP];        // V^T[d][tau], rows wave-private
+    __shared__ __attribute__((aligned(16))) float gpl[NW * 3 * 16 * L::GP]; // partial G^T, 3 causal tiles per wave
+    __shared__ __attribute__((aligned(16))) f16 gfh[T * L::EP];        // G^T = hi + lo (fp16), causal
+    __shared__ __attribute__((aligned(16))) f16 gfo[T * L::EP];
+    __shared__ __attribute__((aligned(16))) float2 lsep[NW * T];       // (max, sum) per wave/token
     __shared__ __attribute__((aligned(16))) float gaml[M];             // rescale factor per latent
     __shared__ __attribute__((aligned(16))) float invd[M];             // 1 / d0 (0 if d0 = 0)
     __shared__ int moved[NW];                                           // wave moved a reference max
-    __shared__ __attribute__((aligned(16))) bf16 qs[M * L::QP];        // Q[h] (latent bank)
+    __shared__ __attribute__((aligned(16))) bf16 qs[M * D];            // Q[h] (latent bank), swizzled rows
+    __shared__ __attribute__((aligned(16))) bf16 ksl[T * D];           // K rows of the subtile, swizzled rows
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
     const int NC = gridDim.x;
@@ -277,9 +298,12 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     const int mw0 = w * L::MW;     // first latent of this wave's score slice
     const int dw0 = w * L::DW;     // first value column of this wave's state slice
 
-    for (int vi = tid; vi < M * D / 8; vi += L::NT) {
-        const int m = vi / (D / 8), d8 = vi % (D / 8);
-        *reinterpret_cast<bf16x8*>(qs + m * L::QP + 8 * d8) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * d8);
+    // Rows of Q and K in LDS hold 16-byte chunk j at slot j ^ (row mod KC), so
+    // that the 16 lanes reading one chunk of 16 consecutive rows hit distinct banks.
+    auto slot = [](int row, int j) { return j ^ (row & (L::KC - 1)); };
+    for (int vi = tid; vi < M * L::KC; vi += L::NT) {
+        const int m = vi / L::KC, j = vi % L::KC;
+        *reinterpret_cast<bf16x8*>(qs + m * D + 8 * slot(m, j)) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * j);
     }
     // Chunk prefix: max (log2 domain) and den of the score slice, and the
     // numerator U[all M][this wave's value columns].
@@ -301,25 +325,34 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 U[mi][di][r] = pnum[(pbase + 16 * mi + 4 * g + r) * D + dw0 + 16 * di + c];
-    __syncthreads();
 
     const int t_begin = c_idx * chunk;
     const int t_end = min(N, t_begin + chunk);
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
-    // K rows of the first subtile (B operands of S^T = Q K^T); each iteration
-    // prefetches the next subtile's rows right after its scores are formed.
-    bf16x8 kb[2][L::KS];
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti) {
-        const int t = t_begin + 16 * ti + c;
-#pragma unroll
-        for (int ks = 0; ks < L::KS; ++ks)
-            kb[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
-    }
+    VTile<L::DW, 64> vt;
+    vt.load(V, row0, stride, t_begin, t_end, dw0, lane);
+    // K rows of a subtile go straight from HBM to LDS (global_load_lds): each
+    // lane moves one 16-byte chunk into slot `lane` of its wave's 1 KiB; rows
+    // past the end of the sequence load row N-1 and are masked.  Issued for the
+    // next subtile once every wave has formed its scores, waited for before the
+    // barrier that precedes their use.
+    auto load_k = [&](int t0n) {
+        for (int e = tid; e < T * L::KC; e += L::NT) {
+            const int row = e / L::KC, sl = e % L::KC;
+            const int t = min(t0n + row, N - 1);
+            const bf16* src = K + row0 + (size_t)t * stride + 8 * slot(row, sl);
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(ksl + (e - lane) * 8),
+                                             16, 0, 0);
+        }
+    };
+    load_k(t_begin);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     for (int t0 = t_begin; t0 < t_end; t0 += T) {
-        // ---- V^T of this wave's value columns (wave-private rows of vtl), fp16
-        const bool vbig = __any(stage_vt_f16<L::EP>(vtl, V, row0, stride, t0, t_end, dw0, L::DW, lane, 64));
+        // ---- V^T of this wave's value columns (wave-private rows of vtl), fp16; fetch the next subtile
+        const bool vbig = __any(vt.template store_f16<L::EP>(vtl, dw0, lane));
+        vt.load(V, row0, stride, t0 + T, t_end, dw0, lane);
         // ---- S^T = Q K^T for this wave's latents, log2 domain, invalid tokens -inf
         float s[L::MT][2][4];
         {
@@ -327,151 +360,188 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ks = 0; ks < L::KS; ++ks) {
+            for (int kq = 0; kq < L::KS; ++kq) {
+                bf16x8 kb[2];
+#pragma unroll
+                for (int ti = 0; ti < 2; ++ti) {
+                    const int row = 16 * ti + c;
+                    kb[ti] = load8<bf16x8>(ksl + row * D + 8 * slot(row, 4 * kq + g));
+                }
 #pragma unroll
                 for (int mi = 0; mi < L::MT; ++mi) {
-                    const bf16x8 qa = load8<bf16x8>(qs + (mw0 + 16 * mi + c) * L::QP + 32 * ks + 8 * g);
+                    const int m = mw0 + 16 * mi + c;
+                    const bf16x8 qa = load8<bf16x8>(qs + m * D + 8 * slot(m, 4 * kq + g));
 #pragma unroll
-                    for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa, kb[ti][ks], acc[mi][ti]);
+                    for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa, kb[ti], acc[mi][ti]);
                 }
-            }
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti) {
-                const int t = t0 + T + 16 * ti + c;
-#pragma unroll
-                for (int ks = 0; ks < L::KS; ++ks)
-                    kb[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
             }
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    const bool valid = t0 + 16 * ti + c < t_end;
+                for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) s[mi][ti][r] = valid ? acc[mi][ti][r] * scale2 : kNegInf;
-                }
+                    for (int r = 0; r < 4; ++r) s[mi][ti][r] = acc[mi][ti][r] * scale2;
+            if (t0 + T > t_end) {      // the ragged last subtile
+#pragma unroll
+                for (int mi = 0; mi < L::MT; ++mi)
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (t0 + 16 * ti + c >= t_end) s[mi][ti][r] = kNegInf;
+            }
         }
-        // ---- per-latent reference max, E, cumulative den (rows of S^T, DPP over tokens)
-        bf16x4 ehi[L::MT][2], elo[L::MT][2];   // E = hi + lo (bf16), for G
-        float dt[L::MT][2][4], d0[L::MT][4];
+        // ---- lazy reference max: a per-lane check; the exact row max only when one moves
+        float gam[L::MT][4];
         bool need = false;
 #pragma unroll
         for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
-                const bool mv = mx > R[mi][r] + kLazy;
-                need |= mv;
-                const float Rn = mv ? mx : R[mi][r];
-                const float gam = mv ? exp2f_fast(R[mi][r] - Rn) : 1.0f;   // 0 when R = -inf
-                R[mi][r] = Rn;
-                const float e0 = exp2f_fast(s[mi][0][r] - Rn);
-                const float e1 = exp2f_fast(s[mi][1][r] - Rn);
-                SPLIT2(bf16, e0, ehi[mi][0][r], elo[mi][0][r]);
-                SPLIT2(bf16, e1, ehi[mi][1][r], elo[mi][1][r]);
-                const float base = dn[mi][r] * gam;
-                d0[mi][r] = base;
-                const float c0 = row_scan16(e0);
-                const float tot0 = row_sum16(e0);
-                const float c1 = row_scan16(e1);
-                const float tot1 = row_sum16(e1);
-                dt[mi][0][r] = base + c0;
-                dt[mi][1][r] = base + tot0 + c1;
-                dn[mi][r] = base + tot0 + tot1;
-                const int m = mw0 + 16 * mi + 4 * g + r;
-                if (c == 0) {
-                    gaml[m] = gam;
-                    invd[m] = base > 0.0f ? __builtin_amdgcn_rcpf(base) : 0.0f;
-                }
-                f16* er = etl + m * L::EP;     // E^T[m][tau] in fp16 for the update
-                er[c] = (f16)e0;
-                er[16 + c] = (f16)e1;
+                gam[mi][r] = 1.0f;
+                need |= fmaxf(s[mi][0][r], s[mi][1][r]) > R[mi][r] + kLazy;
             }
         const bool wave_moved = __any(need);     // a wave-wide vote: every lane takes part
-        if (lane == 0) moved[w] = wave_moved ? 1 : 0;
-        // ---- decoder log-sum-exp over the latent bank, per token (cols of S^T)
-#pragma unroll
-        for (int ti = 0; ti < 2; ++ti) {
-            float lm = kNegInf;
+        if (wave_moved) {
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) lm = fmaxf(lm, s[mi][ti][r]);
-            lm = rows_max4(lm);
-            float ls = 0.0f;
-            if (lm != kNegInf) {
+                for (int r = 0; r < 4; ++r) {
+                    const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
+                    const bool mv = mx > R[mi][r] + kLazy;
+                    const float Rn = mv ? mx : R[mi][r];
+                    gam[mi][r] = mv ? exp2f_fast(R[mi][r] - Rn) : 1.0f;   // 0 when R = -inf
+                    R[mi][r] = Rn;
+                }
+        }
+        // ---- decoder max over this wave's latents, per token (cols of S^T)
+        float lm[2], off[2];
 #pragma unroll
-                for (int mi = 0; mi < L::MT; ++mi)
+        for (int ti = 0; ti < 2; ++ti) {
+            float mx = kNegInf;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ls += exp2f_fast(s[mi][ti][r] - lm);
+            for (int mi = 0; mi < L::MT; ++mi)
+                mx = fmaxf(mx, fmaxf(fmaxf(s[mi][ti][0], s[mi][ti][1]), fmaxf(s[mi][ti][2], s[mi][ti][3])));
+            lm[ti] = rows_max4(mx);
+            off[ti] = lm[ti] == kNegInf ? 0.0f : lm[ti];
+        }
+        // ---- E = 2^(S - R) (hi + lo bf16 for G, fp16 E^T for the numerator), the
+        //      cumulative den d_t (DPP scans over the token lanes), p = 2^(S - lm),
+        //      and q = p / d_t
+        bf16x4 ehi[L::MT][2], elo[L::MT][2];
+        float q[L::MT][2][4], d0[L::MT][4];
+        float ls[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int mi = 0; mi < L::MT; ++mi) {
+            float e[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e0 = exp2f_fast(s[mi][0][r] - R[mi][r]);
+                const float e1 = exp2f_fast(s[mi][1][r] - R[mi][r]);
+                e[0][r] = e0;
+                e[1][r] = e1;
+                const int m = mw0 + 16 * mi + 4 * g + r;
+                etl[m * L::EP + c] = (f16)e0;
+                etl[m * L::EP + 16 + c] = (f16)e1;
+                const float c0 = row_scan16(e0);
+                const float c1 = row_scan16(e1);
+                const float base = dn[mi][r] * gam[mi][r];
+                const float b1 = base + row_bcast15(c0);
+                d0[mi][r] = base;
+                const float dt0 = base + c0, dt1 = b1 + c1;
+                dn[mi][r] = b1 + row_bcast15(c1);
+                const float p0 = exp2f_fast(s[mi][0][r] - off[0]);
+                const float p1 = exp2f_fast(s[mi][1][r] - off[1]);
+                ls[0] += p0;
+                ls[1] += p1;
+                q[mi][0][r] = dt0 > 0.0f ? p0 * __builtin_amdgcn_rcpf(dt0) : 0.0f;
+                q[mi][1][r] = dt1 > 0.0f ? p1 * __builtin_amdgcn_rcpf(dt1) : 0.0f;
             }
-            ls = rows_sum4(ls);
-            if (g == 0) {
-                lsep[(w * T + 16 * ti + c) * 2 + 0] = lm;
-                lsep[(w * T + 16 * ti + c) * 2 + 1] = ls;
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti) split_bf16x4(e[ti][0], e[ti][1], e[ti][2], e[ti][3], ehi[mi][ti], elo[mi][ti]);
+        }
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+            const float l = rows_sum4(ls[ti]);
+            if (g == 0) lsep[w * T + 16 * ti + c] = float2{lm[ti], l};
+        }
+        // per-latent rescale factor and 1 / d0: lanes c = 0..3 store latent rows r = c
+#pragma unroll
+        for (int mi = 0; mi < L::MT; ++mi) {
+            float gsel = gam[mi][0], dsel = d0[mi][0];
+#pragma unroll
+            for (int r = 1; r < 4; ++r) {
+                gsel = c == r ? gam[mi][r] : gsel;
+                dsel = c == r ? d0[mi][r] : dsel;
+            }
+            const float isel = dsel > 0.0f ? __builtin_amdgcn_rcpf(dsel) : 0.0f;
+            if (c < 4) {
+                gaml[mw0 + 16 * mi + 4 * g + c] = gsel;
+                invd[mw0 + 16 * mi + 4 * g + c] = isel;
             }
         }
-        __syncthreads();   // B1: lse partials, rescale factors, 1/d0, E^T visible
+        if (lane == 0) moved[w] = wave_moved ? 1 : 0;
+        __syncthreads();   // B1: lse partials, rescale factors, 1/d0, E^T visible; K rows consumed
+        if (t0 + T < t_end) load_k(t0 + T);
 
-        float lse[2];
+        // ---- f = 2^(lm_w - lse): alpha = p f, W2 = alpha / d_t = q f
+        float f[2];
 #pragma unroll
         for (int ti = 0; ti < 2; ++ti) {
             const int t = 16 * ti + c;
             float mm = kNegInf;
 #pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) mm = fmaxf(mm, lsep[(w2 * T + t) * 2]);
-            float ss = 0.0f;
+            for (int w2 = 0; w2 < NW; ++w2) mm = fmaxf(mm, lsep[w2 * T + t].x);
+            float ss = 0.0f;     // NaN only when mm = -inf (no valid token), not used then
 #pragma unroll
             for (int w2 = 0; w2 < NW; ++w2) {
-                const float m2 = lsep[(w2 * T + t) * 2];
-                if (m2 != kNegInf) ss += lsep[(w2 * T + t) * 2 + 1] * exp2f_fast(m2 - mm);
+                const float2 e2 = lsep[w2 * T + t];
+                ss += e2.y * exp2f_fast(e2.x - mm);
             }
-            lse[ti] = mm + __log2f(ss);
+            f[ti] = (mm == kNegInf) ? 0.0f : exp2f_fast(off[ti] - mm) * __builtin_amdgcn_rcpf(ss);
         }
-        // W1 (fp16 -> LDS) and W2 = hi + lo (bf16), one 32-latent block at a time,
-        // each block folded straight into the partial G^T[tau][t] = sum_m E W2.
-        f32x4 gacc[2][2];
+        // W1 = W2 d0 (fp16 -> LDS) and W2 = hi + lo (bf16), one 32-latent block at a
+        // time, each block folded straight into this wave's part of G^T[tau][t] = sum_m E W2.
+        f32x4 gacc[3];    // (t tile, tau tile) = (0,0), (1,0), (1,1); (0,1) is above the diagonal
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti) gacc[ti][0] = gacc[ti][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q3 = 0; q3 < 3; ++q3) gacc[q3] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < L::MT / 2; ++kk) {
             bf16x4 whi[2][2], wlo[2][2];    // [latent tile of the block][t tile]
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int mi = 2 * kk + j;
+            for (int jb = 0; jb < 2; ++jb) {
+                const int mi = 2 * kk + jb;
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) {
-                    const bool valid = t0 + 16 * ti + c < t_end;
+                    float w2v[4];
                     f16x4 w1;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const float d_t = dt[mi][ti][r];
-                        const float a = (valid && d_t > 0.0f) ? exp2f_fast(s[mi][ti][r] - lse[ti]) : 0.0f;
-                        const float w2v = a * (d_t > 0.0f ? __builtin_amdgcn_rcpf(d_t) : 0.0f);
-                        w1[r] = (f16)(w2v * d0[mi][r]);
-                        SPLIT2(bf16, w2v, whi[j][ti][r], wlo[j][ti][r]);
+                        w2v[r] = q[mi][ti][r] * f[ti];
+                        w1[r] = (f16)(w2v[r] * d0[mi][r]);
                     }
+                    split_bf16x4(w2v[0], w2v[1], w2v[2], w2v[3], whi[jb][ti], wlo[jb][ti]);
                     *reinterpret_cast<f16x4*>(wl + (16 * ti + c) * L::WP + mw0 + 16 * mi + 4 * g) = w1;
                 }
             }
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti)          // t tile (cols of G^T)
-#pragma unroll
-                for (int ui = 0; ui < 2; ++ui) {    // tau tile (rows of G^T)
-                    const bf16x8 wh = cat8<bf16x8>(whi[0][ti], whi[1][ti]);                  // W2^T[m][t]
-                    const bf16x8 wo = cat8<bf16x8>(wlo[0][ti], wlo[1][ti]);
-                    const bf16x8 eh = cat8<bf16x8>(ehi[2 * kk][ui], ehi[2 * kk + 1][ui]);    // E[tau][m]
-                    const bf16x8 eo = cat8<bf16x8>(elo[2 * kk][ui], elo[2 * kk + 1][ui]);
-                    gacc[ti][ui] = mma(eh, wh, gacc[ti][ui]);
-                    gacc[ti][ui] = mma(eo, wh, gacc[ti][ui]);
-                    gacc[ti][ui] = mma(eh, wo, gacc[ti][ui]);
-                }
+            for (int q3 = 0; q3 < 3; ++q3) {
+                const int ti = q3 == 0 ? 0 : 1, ui = q3 == 2 ? 1 : 0;
+                const bf16x8 wh = cat8<bf16x8>(whi[0][ti], whi[1][ti]);                  // W2^T[m][t]
+                const bf16x8 wo = cat8<bf16x8>(wlo[0][ti], wlo[1][ti]);
+                const bf16x8 e_h = cat8<bf16x8>(ehi[2 * kk][ui], ehi[2 * kk + 1][ui]);   // E[tau][m]
+                const bf16x8 e_o = cat8<bf16x8>(elo[2 * kk][ui], elo[2 * kk + 1][ui]);
+                gacc[q3] = mma(e_h, wh, gacc[q3]);
+                gacc[q3] = mma(e_o, wh, gacc[q3]);
+                gacc[q3] = mma(e_h, wo, gacc[q3]);
+            }
         }
+        // this wave's partial G^T: rows t = 16 ti + c, cols tau = 16 ui + 4 g .. + 3
 #pragma unroll
-        for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-            for (int ui = 0; ui < 2; ++ui)
-                *reinterpret_cast<f32x4*>(gpl + (w * T + 16 * ti + c) * L::GP + 16 * ui + 4 * g) = gacc[ti][ui];
+        for (int q3 = 0; q3 < 3; ++q3) {
+            const int ti = q3 == 0 ? 0 : 1, ui = q3 == 2 ? 1 : 0;
+            *reinterpret_cast<f32x4*>(gpl + ((w * 3 + q3) * 16 + c) * L::GP + 4 * g) = gacc[q3];
+        }
         // ---- move the numerator to the new reference maxima (rare after the first subtile)
         bool any_moved = false;
 #pragma unroll
@@ -488,13 +558,24 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
         }
         __syncthreads();   // B2: W1 and the G^T partials visible
 
-        // ---- reduce the G^T partials: wave w sums rows t in [w*GROWS, (w+1)*GROWS)
-        for (int e2 = lane; e2 < L::GROWS * T; e2 += 64) {
-            const int t = w * L::GROWS + e2 / T, tau = e2 % T;
-            float acc = 0.0f;
+        // ---- reduce the partials into the causal G^T = hi + lo (fp16), two entries per step
+        for (int e2 = tid; e2 < T * T / 2; e2 += L::NT) {
+            const int t = e2 / (T / 2), tau = 2 * (e2 % (T / 2));
+            float a0 = 0.0f, a1 = 0.0f;
+            if (tau <= t) {
+                const int q3 = (t >= 16) + (tau >= 16);
 #pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) acc += gpl[(w2 * T + t) * L::GP + tau];
-            gfl[t * L::GP + tau] = acc;
+                for (int w2 = 0; w2 < NW; ++w2) {
+                    const float2 pr = *reinterpret_cast<const float2*>(gpl + ((w2 * 3 + q3) * 16 + (t & 15)) * L::GP + (tau & 15));
+                    a0 += pr.x;
+                    a1 += pr.y;
+                }
+                if (tau + 1 > t) a1 = 0.0f;
+            }
+            f16x2 hh, ll;
+            split_f16_pair(a0, a1, hh, ll);
+            *reinterpret_cast<f16x2*>(gfh + t * L::EP + tau) = hh;
+            *reinterpret_cast<f16x2*>(gfo + t * L::EP + tau) = ll;
         }
         // ---- Y^T = z0^T W1^T with z0 = U / d0 (fp16 operands, both bounded)
         f32x4 yacc[L::DTW][2];
@@ -564,24 +645,17 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                 }
             }
         }
-        __syncthreads();   // B2b: the reduced G^T is visible
+        __builtin_amdgcn_s_waitcnt(0);     // this wave's K rows of the next subtile have landed
+        __syncthreads();   // B2b: the reduced G^T (and the next K rows) are visible
         if (!vbig) {
-            // ---- + V^T (G^T o causal), G = hi + lo (fp16) x V (fp16)
+            // ---- + V^T G^T, G = hi + lo (fp16) x V (fp16)
             f16x8 va[L::DTW];
 #pragma unroll
             for (int di = 0; di < L::DTW; ++di) va[di] = load8<f16x8>(vtl + (dw0 + 16 * di + c) * L::EP + 8 * g);
 #pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
-                const int t = 16 * ti + c;
-                const float* gr = gfl + t * L::GP + 8 * g;
-                const f32x4 ga = *reinterpret_cast<const f32x4*>(gr);
-                const f32x4 gb = *reinterpret_cast<const f32x4*>(gr + 4);
-                f16x8 gh, go;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    SPLIT2(f16, (8 * g + r <= t) ? ga[r] : 0.0f, gh[r], go[r]);
-                    SPLIT2(f16, (8 * g + 4 + r <= t) ? gb[r] : 0.0f, gh[4 + r], go[4 + r]);
-                }
+                const f16x8 gh = load8<f16x8>(gfh + (16 * ti + c) * L::EP + 8 * g);
+                const f16x8 go = load8<f16x8>(gfo + (16 * ti + c) * L::EP + 8 * g);
 #pragma unroll
                 for (int di = 0; di < L::DTW; ++di) {
                     yacc[di][ti] = mma(va[di], gh, yacc[di][ti]);
@@ -604,13 +678,11 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             for (int di = 0; di < L::DTW; ++di) va[di] = load8<bf16x8>(vtb + (dw0 + 16 * di + c) * L::EP + 8 * g);
 #pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
-                const int t = 16 * ti + c;
+                const f16x8 gh16 = load8<f16x8>(gfh + (16 * ti + c) * L::EP + 8 * g);
+                const f16x8 go16 = load8<f16x8>(gfo + (16 * ti + c) * L::EP + 8 * g);
                 bf16x8 gh, go;
 #pragma unroll
-                for (int e2 = 0; e2 < 8; ++e2) {
-                    const float x = gfl[t * L::GP + 8 * g + e2];
-                    SPLIT2(bf16, (8 * g + e2 <= t) ? x : 0.0f, gh[e2], go[e2]);
-                }
+                for (int e2 = 0; e2 < 8; ++e2) SPLIT2(bf16, (float)gh16[e2] + (float)go16[e2], gh[e2], go[e2]);
 #pragma unroll
                 for (int di = 0; di < L::DTW; ++di) {
                     yacc[di][ti] = mma(va[di], gh, yacc[di][ti]);
@@ -660,16 +732,29 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
                         int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
                         float* cnum, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_mfma: chunk must be a multiple of %d", T);
+    FLARE_REQUIRE(M % 32 == 0 && M >= 32 && M <= kMaxPrepM && (D == 64 || D == 128),
+                  "chunk_prepare_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
-    dim3 block((unsigned)(64 * (M / 32)));
     const float s2 = scale * kLog2e;
-    if (D == 64)
-        hipLaunchKernelGGL(chunk_prepare_mfma<64>, grid, block, 0, stream, (const bf16*)Q, (const bf16*)K,
-                           (const bf16*)V, (int)N, (int)H, (int)M, s2, (int)chunk, cmax, cden, cnum);
-    else
-        hipLaunchKernelGGL(chunk_prepare_mfma<128>, grid, block, 0, stream, (const bf16*)Q, (const bf16*)K,
-                           (const bf16*)V, (int)N, (int)H, (int)M, s2, (int)chunk, cmax, cden, cnum);
+    const int nwp = (int)(M / 32);
+#define FLARE_PREP(DD, NN)                                                                              \
+    hipLaunchKernelGGL((chunk_prepare_mfma<DD, NN>), grid, dim3(64 * NN), 0, stream, (const bf16*)Q,     \
+                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, cmax, cden, cnum)
+#define FLARE_PREP_D(DD)                      \
+    switch (nwp) {                            \
+        case 1: FLARE_PREP(DD, 1); break;     \
+        case 2: FLARE_PREP(DD, 2); break;     \
+        case 3: FLARE_PREP(DD, 3); break;     \
+        case 4: FLARE_PREP(DD, 4); break;     \
+        case 5: FLARE_PREP(DD, 5); break;     \
+        case 6: FLARE_PREP(DD, 6); break;     \
+        case 7: FLARE_PREP(DD, 7); break;     \
+        default: FLARE_PREP(DD, 8); break;    \
+    }
+    if (D == 64) { FLARE_PREP_D(64) } else { FLARE_PREP_D(128) }
+#undef FLARE_PREP_D
+#undef FLARE_PREP
     return check_launch("chunk_prepare_mfma");
 }
 

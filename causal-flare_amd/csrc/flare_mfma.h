@@ -21,7 +21,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.0f;            // log2 headroom before a reference max moves
 constexpr float kF16Max = 65504.0f;
-constexpr int kMaxPrepM = 256;           // latent bank held in LDS by the prepare kernel
+constexpr int kMaxPrepM = 256;           // largest latent bank of the prepare kernel (8 waves)
 
 __device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -39,6 +39,34 @@ __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_e
         HI = _h;                           \
         LO = (TY)(_x - (float)_h);         \
     } while (0)
+
+typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// (x0, x1) = hi + lo with bf16 halves: hi is the truncated upper half of each
+// float (exact), lo = x - hi rounded to bf16, so |x - hi - lo| <= 2^-16 |x|.
+__device__ __forceinline__ void split_bf16_pair(float x0, float x1, bf16x2& hi, bf16x2& lo) {
+    const unsigned b0 = __builtin_bit_cast(unsigned, x0), b1 = __builtin_bit_cast(unsigned, x1);
+    hi = __builtin_bit_cast(bf16x2, __builtin_amdgcn_perm(b1, b0, 0x07060302u));
+    const float l0 = x0 - __builtin_bit_cast(float, b0 & 0xffff0000u);
+    const float l1 = x1 - __builtin_bit_cast(float, b1 & 0xffff0000u);
+    lo = __builtin_convertvector(f32x2{l0, l1}, bf16x2);
+}
+// four floats -> bf16x4 hi / lo
+__device__ __forceinline__ void split_bf16x4(float x0, float x1, float x2, float x3, bf16x4& hi, bf16x4& lo) {
+    bf16x2 h01, l01, h23, l23;
+    split_bf16_pair(x0, x1, h01, l01);
+    split_bf16_pair(x2, x3, h23, l23);
+    hi = __builtin_shufflevector(h01, h23, 0, 1, 2, 3);
+    lo = __builtin_shufflevector(l01, l23, 0, 1, 2, 3);
+}
+// (x0, x1) = hi + lo with fp16 halves (hi rounded to nearest)
+__device__ __forceinline__ void split_f16_pair(float x0, float x1, f16x2& hi, f16x2& lo) {
+    hi = __builtin_convertvector(f32x2{x0, x1}, f16x2);
+    const f32x2 h = __builtin_convertvector(hi, f32x2);
+    lo = __builtin_convertvector(f32x2{x0 - h[0], x1 - h[1]}, f16x2);
+}
 
 // DPP moves inside a 16-lane row.  Lanes whose source is outside the row read 0.
 template <int CTRL>
@@ -73,6 +101,8 @@ __device__ __forceinline__ float row_scan16(float x) {
     x += dpp<kRowShr8>(x);
     return x;
 }
+// Lane 15 of each 16-lane row, broadcast over the row (DPP row_newbcast:15).
+__device__ __forceinline__ float row_bcast15(float x) { return dpp<0x15F>(x); }
 // max / sum over the four 16-lane rows (lanes c, c+16, c+32, c+48)
 __device__ __forceinline__ float rows_max4(float x) {
     x = fmaxf(x, __shfl_xor(x, 16, 64));
@@ -140,6 +170,76 @@ __device__ __forceinline__ void stage_vt_bf16(bf16* vt, const bf16* V, size_t ro
         for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = v[e];
     }
 }
+
+// One subtile of V[t0 .. t0+T) x [d0, d0+ND) held in registers, NTHR threads
+// of the group each holding NS 8-column slots, so that the next subtile can be
+// fetched from HBM while the current one is being used.
+template <int ND, int NTHR>
+struct VTile {
+    static constexpr int SLOTS = T * ND / 8;
+    static constexpr int NS = (SLOTS + NTHR - 1) / NTHR;
+    bf16x8 v[NS];
+
+    // Slot vi -> (token tau, 8-column chunk d8).  Row-major for at most two
+    // chunks per row; otherwise pairs of chunks x 32 tokens per 64 slots, so
+    // that the transposed 2-byte LDS stores of one instruction fall in
+    // distinct banks (row pitch 40 halves).
+    __device__ __forceinline__ static void slot(int vi, int& tau, int& d8) {
+        constexpr int NDC = ND / 8;
+        if (NDC <= 2) {
+            tau = vi / NDC;
+            d8 = vi % NDC;
+        } else {
+            tau = (vi >> 1) & 31;
+            d8 = (vi & 1) + 2 * ((vi >> 6) % (NDC / 2));
+        }
+    }
+    __device__ __forceinline__ void load(const bf16* V, size_t row0, size_t stride, int t0, int t_end, int d0,
+                                         int tid) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const int vi = tid + k * NTHR;
+            int tau, d8;
+            slot(vi, tau, d8);
+            const int t = t0 + tau;
+            v[k] = (vi < SLOTS && t < t_end) ? load8<bf16x8>(V + row0 + (size_t)t * stride + d0 + 8 * d8) : zero8();
+        }
+    }
+    // V^T[d][tau] (row pitch P) as fp16; returns whether a value exceeds the fp16 range.
+    template <int P>
+    __device__ __forceinline__ bool store_f16(f16* vt, int d0, int tid) const {
+        float big = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const int vi = tid + k * NTHR;
+            if (SLOTS % NTHR == 0 || vi < SLOTS) {
+                int tau, d8;
+                slot(vi, tau, d8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = (float)v[k][e];
+                    big = fmaxf(big, fabsf(x));
+                    vt[(d0 + 8 * d8 + e) * P + tau] = (f16)x;
+                }
+            }
+        }
+        return big > kF16Max;
+    }
+    // V^T[d][tau] (row pitch P), bf16 as loaded.
+    template <int P>
+    __device__ __forceinline__ void store_bf16(bf16* vt, int d0, int tid) const {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const int vi = tid + k * NTHR;
+            if (SLOTS % NTHR == 0 || vi < SLOTS) {
+                int tau, d8;
+                slot(vi, tau, d8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = v[k][e];
+            }
+        }
+    }
+};
 
 }  // namespace mfma
 }  // namespace flare

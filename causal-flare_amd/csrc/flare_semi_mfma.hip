@@ -94,6 +94,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const int t_end = min(N, t_begin + chunk);      // chunk and N are whole blocks
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
+    VTile<L::DW, 64> vt;
+    vt.load(V, row0, stride, t_begin, t_end, dw0, lane);
     bf16x8 kb[2][L::KS];
 #pragma unroll
     for (int ti = 0; ti < 2; ++ti)
@@ -104,7 +106,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     for (int blk0 = t_begin; blk0 < t_end; blk0 += L::BLOCK) {
         for (int j = 0; j < NSUB; ++j) {
             const int t0 = blk0 + j * T;
-            const bool vbig = __any(stage_vt_f16<L::EP>(vtl, V, row0, stride, t0, t_end, dw0, L::DW, lane, 64));
+            const bool vbig = __any(vt.template store_f16<L::EP>(vtl, dw0, lane));
+            vt.load(V, row0, stride, t0 + T, t_end, dw0, lane);
             // ---- S^T = Q K^T (log2 domain); prefetch the next subtile's K rows
             float s[L::MT][2][4];
             {
