@@ -66,6 +66,8 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     constexpr int DT = D / 16;     // value-column tiles
     constexpr int VP = T + 8;      // padded row of the transposed V tile
     __shared__ __attribute__((aligned(16))) f16 vtl[2][D * VP];
+    __shared__ __attribute__((aligned(16))) bf16 ksl[2][T * D];   // K rows of a subtile (swizzled)
+    __shared__ __attribute__((aligned(16))) bf16 qs[M * D];       // Q[h] (swizzled rows)
     __shared__ int vbig[2];        // subtile index whose V^T buffer holds a value outside fp16
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
@@ -75,12 +77,10 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     const int g = lane >> 4, c = lane & 15;
     const int m0 = 32 * w;                       // this wave's 32 latents
 
-    // B operands of S = K Q^T: Q rows of this wave's latents
-    bf16x8 qb[2][KS];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qb[mt][ks] = load8<bf16x8>(Q + ((size_t)h * M + m0 + 16 * mt + c) * D + 32 * ks + 8 * g);
+    for (int vi = tid; vi < M * D / 8; vi += NT) {
+        const int m = vi / (D / 8), jc = vi % (D / 8);
+        *reinterpret_cast<bf16x8*>(qs + m * D + 8 * swz<D>(m, jc)) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * jc);
+    }
     f32x4 U[2][DT];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -94,21 +94,20 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
     if (tid < 2) vbig[tid] = -1;
+    // K rows reach LDS directly (double-buffered, issued one subtile ahead);
+    // V comes through registers, also one subtile ahead.
     VTile<D, NT> vt;
+    rows_to_lds<D, NT>(ksl[0], K, row0, stride, t_begin, N, tid, lane);
     vt.load(V, row0, stride, t_begin, t_end, 0, tid);
-    bf16x8 ka[2][KS];
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti) {
-        const int t = t_begin + 16 * ti + c;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            ka[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
-    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int j = 0;
     for (int t0 = t_begin; t0 < t_end; t0 += T, ++j) {
         f16* vtj = vtl[j & 1];
+        const bf16* kj = ksl[j & 1];
         if (vt.template store_f16<VP>(vtj, 0, tid)) vbig[j & 1] = j;
+        const bool more = t0 + T < t_end;
+        if (more) rows_to_lds<D, NT>(ksl[(j + 1) & 1], K, row0, stride, t0 + T, N, tid, lane);
         vt.load(V, row0, stride, t0 + T, t_end, 0, tid);
         // S = K Q^T, tokens as rows: s[mt][ti][r] = S[t = 16 ti + 4 g + r][m = 16 mt + c]
         float s[2][2][4];
@@ -117,17 +116,19 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
+            for (int kq = 0; kq < KS; ++kq) {
+                bf16x8 ka[2], qb[2];
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
+                for (int ti = 0; ti < 2; ++ti) ka[ti] = load8<bf16x8>(kj + (16 * ti + c) * D + 8 * swz<D>(16 * ti + c, 4 * kq + g));
 #pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka[ti][ks], qb[mt][ks], acc[mt][ti]);
+                for (int mt = 0; mt < 2; ++mt) {
+                    const int m = m0 + 16 * mt + c;
+                    qb[mt] = load8<bf16x8>(qs + m * D + 8 * swz<D>(m, 4 * kq + g));
+                }
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti) {
-                const int t = t0 + T + 16 * ti + c;
+                for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-                    ka[ti][ks] = t < t_end ? load8<bf16x8>(K + row0 + (size_t)t * stride + 32 * ks + 8 * g) : zero8();
+                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka[ti], qb[mt], acc[mt][ti]);
             }
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -189,7 +190,9 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
                 }
             dl[mt] += es;
         }
-        __syncthreads();   // V^T of this subtile (and its range flag) visible
+        // this thread's K rows of the next subtile have landed (its V loads may still be in flight)
+        if (more) FLARE_WAIT_VMCNT((VTile<D, NT>::NS));
+        __syncthreads();   // V^T of this subtile (and its range flag), next K rows visible
         if (vbig[j & 1] != j) {
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt) {

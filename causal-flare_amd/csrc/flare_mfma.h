@@ -171,6 +171,38 @@ __device__ __forceinline__ void stage_vt_bf16(bf16* vt, const bf16* V, size_t ro
     }
 }
 
+// Rows of D bf16 values in LDS hold 16-byte chunk j at slot j ^ (row mod D/8):
+// the 16 lanes that read one chunk of 16 consecutive rows hit distinct banks.
+template <int D>
+__device__ __forceinline__ int swz(int row, int j) { return j ^ (row & (D / 8 - 1)); }
+
+// T rows t0 .. t0+T of a [.., stride] bf16 tensor (one (b,h): row0) straight
+// from HBM into swizzled LDS rows (global_load_lds: no registers), NTHR
+// threads each moving 16-byte chunks into consecutive 1 KiB pieces per wave.
+// Rows at or past `nrows` read row nrows-1 (their values are masked by the
+// caller).  Completion is tracked by vmcnt like any other global load.
+template <int D, int NTHR>
+__device__ __forceinline__ void rows_to_lds(bf16* dst, const bf16* src, size_t row0, size_t stride, int t0,
+                                            int nrows, int tid, int lane) {
+    constexpr int KC = D / 8;
+#pragma unroll
+    for (int e0 = 0; e0 < T * KC; e0 += NTHR) {
+        const int e = e0 + tid;
+        if (T * KC % NTHR == 0 || e < T * KC) {
+            const int row = e / KC, sl = e % KC;
+            const int t = min(t0 + row, nrows - 1);
+            __builtin_amdgcn_global_load_lds(src + row0 + (size_t)t * stride + 8 * swz<D>(row, sl),
+                                             (__attribute__((address_space(3))) void*)(dst + (e - lane) * 8), 16, 0, 0);
+        }
+    }
+}
+// Number of rows_to_lds loads each thread issues (for vmcnt bookkeeping).
+template <int D, int NTHR>
+constexpr int rows_to_lds_count() { return (T * (D / 8) + NTHR - 1) / NTHR; }
+
+// s_waitcnt vmcnt(n) with the other counters left alone (n <= 15).
+#define FLARE_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
 // One subtile of V[t0 .. t0+T) x [d0, d0+ND) held in registers, NTHR threads
 // of the group each holding NS 8-column slots, so that the next subtile can be
 // fetched from HBM while the current one is being used.
