@@ -288,7 +288,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     __shared__ __attribute__((aligned(16))) f16 gfo[T * L::EP];
     __shared__ __attribute__((aligned(16))) float2 lsep[NW * T];       // (max, sum) per wave/token
     __shared__ __attribute__((aligned(16))) float gaml[M];             // rescale factor per latent
-    __shared__ __attribute__((aligned(16))) float invd[M];             // 1 / d0 (0 if d0 = 0)
+    __shared__ __attribute__((aligned(16))) float d0l[M];              // den at the subtile start (after moves)
     __shared__ int moved[NW];                                           // wave moved a reference max
     __shared__ __attribute__((aligned(16))) bf16 qs[M * D];            // Q[h] (latent bank), swizzled rows
     __shared__ __attribute__((aligned(16))) bf16 ksl[T * D];           // K rows of the subtile, swizzled rows
@@ -311,23 +311,29 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     // Chunk prefix: max (log2 domain) and den of the score slice, and the
     // numerator U[all M][this wave's value columns].
     const size_t pbase = ((size_t)bh * NC + c_idx) * M;
+    // The reference R of a latent starts at the prefix's log-sum-exp, so that
+    // den starts at 1 and the numerator at the prefix's normalised z.
     float R[L::MT][4], dn[L::MT][4];
 #pragma unroll
     for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = mw0 + 16 * mi + 4 * g + r;
-            R[mi][r] = pmax[pbase + m] * kLog2e;
-            dn[mi][r] = pden[pbase + m];
+            const float pd = pden[pbase + m];
+            R[mi][r] = pd > 0.0f ? pmax[pbase + m] * kLog2e + __log2f(pd) : kNegInf;
+            dn[mi][r] = pd > 0.0f ? 1.0f : 0.0f;
         }
     f32x4 U[L::MTA][L::DTW];
 #pragma unroll
     for (int mi = 0; mi < L::MTA; ++mi)
 #pragma unroll
-        for (int di = 0; di < L::DTW; ++di)
+        for (int r = 0; r < 4; ++r) {
+            const float pd = pden[pbase + 16 * mi + 4 * g + r];
+            const float ip = pd > 0.0f ? 1.0f / pd : 0.0f;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                U[mi][di][r] = pnum[(pbase + 16 * mi + 4 * g + r) * D + dw0 + 16 * di + c];
+            for (int di = 0; di < L::DTW; ++di)
+                U[mi][di][r] = pnum[(pbase + 16 * mi + 4 * g + r) * D + dw0 + 16 * di + c] * ip;
+        }
 
     const int t_begin = c_idx * chunk;
     const int t_end = min(N, t_begin + chunk);
@@ -394,7 +400,10 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                             if (t0 + 16 * ti + c >= t_end) s[mi][ti][r] = kNegInf;
             }
         }
-        // ---- lazy reference max: a per-lane check; the exact row max only when one moves
+        // ---- lazy reference: R moves when a score exceeds it by more than kLazy
+        //      (to the exact row max) or when den has grown past 2^kDen (by
+        //      log2 den), so E <= 2^kLazy and den, U / max|v| stay below 2^kDen
+        //      at every subtile start.  Checked per lane; moved rarely.
         float gam[L::MT][4];
         bool need = false;
 #pragma unroll
@@ -402,7 +411,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 gam[mi][r] = 1.0f;
-                need |= fmaxf(s[mi][0][r], s[mi][1][r]) > R[mi][r] + kLazy;
+                need |= (fmaxf(s[mi][0][r], s[mi][1][r]) > R[mi][r] + kLazy) | (dn[mi][r] > kDenMax);
             }
         const bool wave_moved = __any(need);     // a wave-wide vote: every lane takes part
         if (wave_moved) {
@@ -411,9 +420,15 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
-                    const bool mv = mx > R[mi][r] + kLazy;
-                    const float Rn = mv ? mx : R[mi][r];
-                    gam[mi][r] = mv ? exp2f_fast(R[mi][r] - Rn) : 1.0f;   // 0 when R = -inf
+                    float Rn = mx > R[mi][r] + kLazy ? mx : R[mi][r];
+                    float g1 = exp2f_fast(R[mi][r] - Rn);                  // 0 when R = -inf
+                    const float dd = dn[mi][r] * g1;
+                    if (dd > kDenMax) {
+                        const float lg = __log2f(dd);
+                        Rn += lg;
+                        g1 = exp2f_fast(R[mi][r] - Rn);
+                    }
+                    gam[mi][r] = Rn == R[mi][r] ? 1.0f : g1;
                     R[mi][r] = Rn;
                 }
         }
@@ -468,7 +483,8 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             const float l = rows_sum4(ls[ti]);
             if (g == 0) lsep[w * T + 16 * ti + c] = float2{lm[ti], l};
         }
-        // per-latent rescale factor and 1 / d0: lanes c = 0..3 store latent rows r = c
+        // per-latent rescale factor and den at the subtile start (read by every
+        // wave when any wave moved a reference): lanes c = 0..3 store rows r = c
 #pragma unroll
         for (int mi = 0; mi < L::MT; ++mi) {
             float gsel = gam[mi][0], dsel = d0[mi][0];
@@ -477,15 +493,17 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                 gsel = c == r ? gam[mi][r] : gsel;
                 dsel = c == r ? d0[mi][r] : dsel;
             }
-            const float isel = dsel > 0.0f ? __builtin_amdgcn_rcpf(dsel) : 0.0f;
             if (c < 4) {
                 gaml[mw0 + 16 * mi + 4 * g + c] = gsel;
-                invd[mw0 + 16 * mi + 4 * g + c] = isel;
+                d0l[mw0 + 16 * mi + 4 * g + c] = dsel;
             }
         }
         if (lane == 0) moved[w] = wave_moved ? 1 : 0;
         __syncthreads();   // B1: lse partials, rescale factors, 1/d0, E^T visible; K rows consumed
         if (t0 + T < t_end) load_k(t0 + T);
+        bool any_moved = false;     // some wave moved a reference in this subtile
+#pragma unroll
+        for (int w2 = 0; w2 < NW; ++w2) any_moved |= moved[w2] != 0;
 
         // ---- f = 2^(lm_w - lse): alpha = p f, W2 = alpha / d_t = q f
         float f[2];
@@ -521,7 +539,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         w2v[r] = q[mi][ti][r] * f[ti];
-                        w1[r] = (f16)(w2v[r] * d0[mi][r]);
+                        w1[r] = (f16)(any_moved ? w2v[r] * d0[mi][r] : w2v[r]);
                     }
                     split_bf16x4(w2v[0], w2v[1], w2v[2], w2v[3], whi[jb][ti], wlo[jb][ti]);
                     *reinterpret_cast<f16x4*>(wl + (16 * ti + c) * L::WP + mw0 + 16 * mi + 4 * g) = w1;
@@ -545,14 +563,16 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             const int ti = q3 == 0 ? 0 : 1, ui = q3 == 2 ? 1 : 0;
             *reinterpret_cast<f32x4*>(gpl + ((w * 3 + q3) * 16 + c) * L::GP + 4 * g) = gacc[q3];
         }
-        // ---- move the numerator to the new reference maxima (rare after the first subtile)
-        bool any_moved = false;
-#pragma unroll
-        for (int w2 = 0; w2 < NW; ++w2) any_moved |= moved[w2] != 0;
+        // ---- a subtile where some reference moved (rare after the first): move the
+        //      numerator and normalise it to z0 = U / d0 for the readout
         if (any_moved) {
 #pragma unroll
             for (int mi = 0; mi < L::MTA; ++mi) {
-                const f32x4 gm = *reinterpret_cast<const f32x4*>(gaml + 16 * mi + 4 * g);
+                const f32x4 ga = *reinterpret_cast<const f32x4*>(gaml + 16 * mi + 4 * g);
+                const f32x4 da = *reinterpret_cast<const f32x4*>(d0l + 16 * mi + 4 * g);
+                f32x4 gm;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gm[r] = da[r] > 0.0f ? ga[r] / da[r] : 0.0f;
 #pragma unroll
                 for (int di = 0; di < L::DTW; ++di)
 #pragma unroll
@@ -580,7 +600,9 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             *reinterpret_cast<f16x2*>(gfh + t * L::EP + tau) = hh;
             *reinterpret_cast<f16x2*>(gfo + t * L::EP + tau) = ll;
         }
-        // ---- Y^T = z0^T W1^T with z0 = U / d0 (fp16 operands, both bounded)
+        // ---- Y^T = U^T W2^T at the subtile start.  No reference moved: d >= 1 so
+        //      W2 <= 1 and |U| <= kDenMax max|v| (fp16 operands).  Some moved: the
+        //      normalised pair z0 = U / d0, W1 = W2 d0 <= alpha instead.
         f32x4 yacc[L::DTW][2];
 #pragma unroll
         for (int di = 0; di < L::DTW; ++di)
@@ -594,21 +616,19 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                 const f16* wr = wl + (16 * ti + c) * L::WP + 32 * kk;
                 wb[ti] = cat8<f16x8>(load4<f16x4>(wr + 4 * g), load4<f16x4>(wr + 16 + 4 * g));
             }
-            const f32x4 ilo = *reinterpret_cast<const f32x4*>(invd + 32 * kk + 4 * g);
-            const f32x4 ihi = *reinterpret_cast<const f32x4*>(invd + 32 * kk + 16 + 4 * g);
 #pragma unroll
             for (int di = 0; di < L::DTW; ++di) {
                 f16x8 za;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    za[r] = (f16)(U[2 * kk][di][r] * ilo[r]);
-                    za[4 + r] = (f16)(U[2 * kk + 1][di][r] * ihi[r]);
+                    za[r] = (f16)U[2 * kk][di][r];
+                    za[4 + r] = (f16)U[2 * kk + 1][di][r];
                 }
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) yacc[di][ti] = mma(za, wb[ti], yacc[di][ti]);
             }
         }
-        {   // |z0| <= max|v|: only a value column with |v| > 65504 overflows fp16 -- redo in bf16
+        {   // an fp16 overflow (|v| beyond 65504 / kDenMax): redo in bf16 with z0, W1
             bool bad = false;
 #pragma unroll
             for (int di = 0; di < L::DTW; ++di)
@@ -632,15 +652,13 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                             wb[ti][4 + e2] = (bf16)(float)wr[16 + 4 * g + e2];
                         }
                     }
-                    const f32x4 ilo = *reinterpret_cast<const f32x4*>(invd + 32 * kk + 4 * g);
-                    const f32x4 ihi = *reinterpret_cast<const f32x4*>(invd + 32 * kk + 16 + 4 * g);
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di) {
                         bf16x8 za;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            za[r] = (bf16)(U[2 * kk][di][r] * ilo[r]);
-                            za[4 + r] = (bf16)(U[2 * kk + 1][di][r] * ihi[r]);
+                            za[r] = (bf16)U[2 * kk][di][r];
+                            za[4 + r] = (bf16)U[2 * kk + 1][di][r];
                         }
 #pragma unroll
                         for (int ti = 0; ti < 2; ++ti) yacc[di][ti] = mma(za, wb[ti], yacc[di][ti]);
@@ -650,6 +668,16 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
         }
         __builtin_amdgcn_s_waitcnt(0);     // this wave's K rows of the next subtile have landed
         __syncthreads();   // B2b: the reduced G^T (and the next K rows) are visible
+        if (any_moved) {    // back from z0 to the numerator
+#pragma unroll
+            for (int mi = 0; mi < L::MTA; ++mi) {
+                const f32x4 da = *reinterpret_cast<const f32x4*>(d0l + 16 * mi + 4 * g);
+#pragma unroll
+                for (int di = 0; di < L::DTW; ++di)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) U[mi][di][r] *= da[r];
+            }
+        }
         if (!vbig) {
             // ---- + V^T G^T, G = hi + lo (fp16) x V (fp16)
             f16x8 va[L::DTW];

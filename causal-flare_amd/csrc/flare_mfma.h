@@ -20,6 +20,7 @@ constexpr int T = 32;       // tokens per subtile (= the MFMA K depth)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.0f;            // log2 headroom before a reference max moves
+constexpr float kDenMax = 16.0f;         // den (relative to the reference) that moves it in the output kernel
 constexpr float kF16Max = 65504.0f;
 constexpr int kMaxPrepM = 256;           // largest latent bank of the prepare kernel (8 waves)
 
