@@ -38,7 +38,7 @@ def _resolve_chunk_size(chunk_size, B, N, H, M, Dv, validate_only=False) -> tupl
     The reference's default chunk is 64 (training.py:328-337) and must be a
     multiple of 16 (:344).  Chunk length only changes fp32 rounding, so when
     neither ``chunk_size`` nor FLARE_CHUNK_SIZE is given the library's own
-    policy (long chunks, ~2048 workgroups) is used.
+    policy (about one chunk workgroup per compute unit) is used.
     """
     explicit = chunk_size
     if explicit is None:

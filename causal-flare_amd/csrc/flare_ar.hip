@@ -423,14 +423,25 @@ int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int6
 }
 
 int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
-    // Enough chunks to give every CU several workgroups, each chunk a multiple
-    // of 64 tokens and at most 2048 long.
+    // One round of chunk workgroups over the device: about one (chunk, b, h)
+    // per compute unit.  Longer chunks mean fewer, cheaper summaries (phase 2
+    // and the summary traffic of phases 1 and 3 shrink with them); each chunk
+    // is a multiple of 64 tokens, between 64 and 8192.
+    static int cus = 0;
+    if (cus <= 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            cus = n;
+        else
+            cus = 256;
+    }
     const int64_t BH = B * H;
-    int64_t target_chunks = (2048 + BH - 1) / BH;  // ~2048 workgroups in phases 1 and 3
+    const int64_t target_chunks = (cus + BH - 1) / BH;
     int64_t c = (N + target_chunks - 1) / target_chunks;
     c = ((c + 63) / 64) * 64;
     if (c < 64) c = 64;
-    if (c > 2048) c = 2048;
+    if (c > 8192) c = 8192;
     return c;
 }
 
