@@ -424,7 +424,7 @@ int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int6
 
 int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
     // One round of chunk workgroups over the device: about one (chunk, b, h)
-    // per compute unit.  Longer chunks mean fewer, cheaper summaries (phase 2
+    // per resident workgroup slot.  Longer chunks mean fewer, cheaper summaries (phase 2
     // and the summary traffic of phases 1 and 3 shrink with them); each chunk
     // is a multiple of 64 tokens, between 64 and 8192.
     static int cus = 0;
@@ -437,7 +437,10 @@ int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
             cus = 256;
     }
     const int64_t BH = B * H;
-    const int64_t target_chunks = (cus + BH - 1) / BH;
+    // the large-bank output kernel fills a compute unit with one workgroup;
+    // smaller banks fit two
+    const int64_t per_cu = (M * Dv >= 256 * 128) ? 1 : 2;
+    const int64_t target_chunks = (per_cu * cus + BH - 1) / BH;
     int64_t c = (N + target_chunks - 1) / target_chunks;
     c = ((c + 63) / 64) * 64;
     if (c < 64) c = 64;

@@ -163,7 +163,10 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
         // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
         // block-causal MFMA readout.  The summaries fit in the workspace since
         // chunks are never shorter than blocks.
-        int64_t chunk = default_chunk(B, N, H, M, Dv);
+        // ~2048 chunk workgroups (several per compute unit), whole blocks each
+        const int64_t target = (2048 + B * H - 1) / (B * H);
+        int64_t chunk = (N + target - 1) / target;
+        if (chunk > 2048) chunk = 2048;
         chunk = ((chunk + block - 1) / block) * block;
         if (chunk > N) chunk = N;
         const int64_t NC = (N + chunk - 1) / chunk;
