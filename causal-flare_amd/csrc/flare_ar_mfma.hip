@@ -792,6 +792,8 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, hipStream_t stream) {
+    if (output_pc_enabled())
+        return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, stream);
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));

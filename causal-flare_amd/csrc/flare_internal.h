@@ -32,6 +32,18 @@ inline int mfma_phase_mask() {
     return mask;
 }
 inline bool mfma_enabled() { return mfma_phase_mask() != 0; }
+// FLARE_OUTPUT_KERNEL=single selects the single-role phase-3 MFMA kernel
+// instead of the producer/consumer one (A/B checks).  Read once per process.
+inline bool output_pc_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("FLARE_OUTPUT_KERNEL");
+        return !(e && e[0] == 's');
+    }();
+    return on;
+}
+int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
+                     const float* pnum, void* Y, int out_dtype, hipStream_t stream);
 }  // namespace flare
 
 namespace flare {

@@ -69,6 +69,15 @@ __device__ __forceinline__ void split_f16_pair(float x0, float x1, f16x2& hi, f1
     lo = __builtin_convertvector(f32x2{x0 - h[0], x1 - h[1]}, f16x2);
 }
 
+// q[0..3] = hi + lo with fp16 halves (hi rounded to nearest)
+__device__ __forceinline__ void split_f16x4(const float q[4], f16x4& hi, f16x4& lo) {
+    f16x2 h01, l01, h23, l23;
+    split_f16_pair(q[0], q[1], h01, l01);
+    split_f16_pair(q[2], q[3], h23, l23);
+    hi = __builtin_shufflevector(h01, h23, 0, 1, 2, 3);
+    lo = __builtin_shufflevector(l01, l23, 0, 1, 2, 3);
+}
+
 // DPP moves inside a 16-lane row.  Lanes whose source is outside the row read 0.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -112,6 +121,14 @@ __device__ __forceinline__ float rows_max4(float x) {
 __device__ __forceinline__ float rows_sum4(float x) {
     x += __shfl_xor(x, 16, 64);
     return x + __shfl_xor(x, 32, 64);
+}
+
+// max over the 64 lanes, as a wave-uniform value: DPP within rows, then the
+// four row maxima read as scalars (no lane-index registers)
+__device__ __forceinline__ float wave_max_dpp(float x) {
+    const int b = __builtin_bit_cast(int, row_max16(x));
+    auto lane_f = [b](int l) { return __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, l)); };
+    return fmaxf(fmaxf(lane_f(0), lane_f(16)), fmaxf(lane_f(32), lane_f(48)));
 }
 
 template <typename V8, typename V4>
@@ -177,6 +194,15 @@ __device__ __forceinline__ void stage_vt_bf16(bf16* vt, const bf16* V, size_t ro
 template <int D>
 __device__ __forceinline__ int swz(int row, int j) { return j ^ (row & (D / 8 - 1)); }
 
+// One 16-byte global_load_lds per lane: lane l's 16 bytes at `src` land at
+// LDS byte offset 16 l from `wave_dst` (the wave's base).  A plain function so
+// that templates instantiated more than once in a translation unit call one
+// definition of the builtin (clang's host pass rejects the repeated inline
+// builtin in template substitution).
+__device__ __forceinline__ void global_to_lds16(const bf16* src, bf16* wave_dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)wave_dst, 16, 0, 0);
+}
+
 // T rows t0 .. t0+T of a [.., stride] bf16 tensor (one (b,h): row0) straight
 // from HBM into swizzled LDS rows (global_load_lds: no registers), NTHR
 // threads each moving 16-byte chunks into consecutive 1 KiB pieces per wave.
@@ -192,11 +218,42 @@ __device__ __forceinline__ void rows_to_lds(bf16* dst, const bf16* src, size_t r
         if (T * KC % NTHR == 0 || e < T * KC) {
             const int row = e / KC, sl = e % KC;
             const int t = min(t0 + row, nrows - 1);
-            __builtin_amdgcn_global_load_lds(src + row0 + (size_t)t * stride + 8 * swz<D>(row, sl),
-                                             (__attribute__((address_space(3))) void*)(dst + (e - lane) * 8), 16, 0, 0);
+            global_to_lds16(src + row0 + (size_t)t * stride + 8 * swz<D>(row, sl), dst + (e - lane) * 8);
         }
     }
 }
+// The T rows t0 .. t0+T of a [.., stride] bf16 tensor (one (b,h): row0) held in
+// registers by NTHR threads (16-byte chunks), then stored to LDS rows of D
+// values with chunk j at slot j ^ (row mod D/8).  Rows at or past `nrows` read
+// row nrows-1 (their values are masked by the caller).
+template <int D, int NTHR>
+struct KRows {
+    static constexpr int KC = D / 8;
+    static constexpr int NK = (T * KC + NTHR - 1) / NTHR;
+    bf16x8 v[NK];
+    __device__ __forceinline__ void load(const bf16* src, size_t row0, size_t stride, int t0, int nrows, int tid) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int e = tid + k * NTHR;
+            if (T * KC % NTHR == 0 || e < T * KC) {
+                const int row = e / KC, j = e % KC;
+                const int t = min(t0 + row, nrows - 1);
+                v[k] = load8<bf16x8>(src + row0 + (size_t)t * stride + 8 * j);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(bf16* dst, int tid) const {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int e = tid + k * NTHR;
+            if (T * KC % NTHR == 0 || e < T * KC) {
+                const int row = e / KC, j = e % KC;
+                *reinterpret_cast<bf16x8*>(dst + row * D + 8 * swz<D>(row, j)) = v[k];
+            }
+        }
+    }
+};
+
 // Number of rows_to_lds loads each thread issues (for vmcnt bookkeeping).
 template <int D, int NTHR>
 constexpr int rows_to_lds_count() { return (T * (D / 8) + NTHR - 1) / NTHR; }
@@ -257,6 +314,30 @@ struct VTile {
             }
         }
         return big > kF16Max;
+    }
+    // Largest |v| this thread holds.
+    __device__ __forceinline__ float absmax(int tid) const {
+        float big = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NS; ++k)
+            if (SLOTS % NTHR == 0 || tid + k * NTHR < SLOTS)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) big = fmaxf(big, fabsf((float)v[k][e]));
+        return big;
+    }
+    // V^T[d][tau] (row pitch P) as fp16 of v * sc (sc a power of two).
+    template <int P>
+    __device__ __forceinline__ void store_f16_scaled(f16* vt, int d0, int tid, float sc) const {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const int vi = tid + k * NTHR;
+            if (SLOTS % NTHR == 0 || vi < SLOTS) {
+                int tau, d8;
+                slot(vi, tau, d8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = (f16)((float)v[k][e] * sc);
+            }
+        }
     }
     // V^T[d][tau] (row pitch P), bf16 as loaded.
     template <int P>

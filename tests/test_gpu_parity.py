@@ -307,6 +307,32 @@ def test_mfma_shapes_bf16(M, D, N, chunk):
     assert_parity(y, ref, torch.bfloat16, f"mfma M={M} D={D} N={N} chunk={chunk}")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_mfma_large_values_bf16(M, D):
+    """Values far outside fp16 (|v| up to 1e5, also at a chunk start) on the MFMA
+    path: the output kernel keeps V and the numerator under a power-of-two scale."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_large_values", M, D)
+    B, N, H = 1, 3000, 2
+    q, k, v = seeded(57 + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    v = v.float()
+    v[:, 500:510] *= 1e5      # inside a chunk
+    v[:, 1024:1030, 1] *= 3e4  # the start of a chunk (prefix z large for the next ones)
+    v = v.bfloat16()
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), chunk_size=256)
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    a, b = to_np(y), np.asarray(ref, np.float64)
+    assert np.isfinite(a).all(), "non-finite output with large values"
+    # tokens before the first outlier: the ordinary bf16 bar
+    assert_parity(y[:, :500], ref[:, :500], torch.bfloat16, f"mfma large values, before M={M} D={D}")
+    # after it: fp16 MFMA operands carry ~2^-12 relative error per term, and outputs that
+    # cancel terms of size 1e5 keep that error in absolute terms; bound the error by the
+    # output scale of each (b, h) sequence
+    scale = np.abs(b[:, 500:]).max(axis=(1, 3), keepdims=True)
+    err = float((np.abs(a[:, 500:] - b[:, 500:]) / scale).max())
+    assert err <= 1e-2, f"mfma large values M={M} D={D}: max |err| / max |ref| = {err:.3e}"
+
+
 @pytest.mark.parametrize("qk_std", [1.0, 3.0])
 def test_mfma_prefill_with_state_bf16(qk_std):
     """Prefill from a cached state on the MFMA path, with larger score spreads."""
