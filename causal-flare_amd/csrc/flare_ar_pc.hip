@@ -31,6 +31,8 @@
 // reference.py:446-496) regrouped into 16x16x32 contractions; operand
 // precision is that of the single-role kernel in flare_ar_mfma.hip, except
 // that G = W2 E uses the fp16 E of the numerator update on the common path.
+#include <type_traits>
+
 #include "flare_common.h"
 #include "flare_internal.h"
 #include "flare_mfma.h"
@@ -67,7 +69,10 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype) {
     using L = PCLayout<M, D>;
-    __shared__ __attribute__((aligned(16))) bf16 ksl[2][T * D];                  // K rows (swizzled)
+    // K rows of the even / odd subtiles (swizzled); two arrays rather than one so
+    // that reads of one never wait on the DMA that fills the other
+    __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
+    __shared__ __attribute__((aligned(16))) bf16 ksl1[T * D];
     __shared__ __attribute__((aligned(16))) f16 etl[2][M * L::EP];              // E^T[m][tau]
     __shared__ __attribute__((aligned(16))) f16 wl[2][T * L::WP];               // q or q d0, [t][m]
     __shared__ __attribute__((aligned(16))) float gpl[2][L::NP * 3 * 16 * L::GP];  // partial G, 3 causal tiles
@@ -95,7 +100,6 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
     if (w < L::NP) {
         // =========================== producer ===========================
         const int mp0 = w * L::MP;
-        constexpr int NTP = 64 * L::NP;
         // Q rows of this wave's latents as MFMA A operands (rows m, k = d)
         bf16x8 qa[L::MTP][L::KS];
 #pragma unroll
@@ -146,21 +150,33 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
         };
         refresh_ar();
         if (tid == 0) psync = 0;
-        // K rows of the next subtile travel through registers (loaded at the start of
-        // an iteration, written to swizzled LDS at its end), so that no LDS access of
-        // the iteration waits on them
-        KRows<D, NTP> kr;
-        kr.load(K, row0, stride, t_begin, N, tid);
-        kr.store(ksl[0], tid);
+        // The four producers meet (consumers never take part): each adds one arrival
+        // and waits for the count of meeting n (1, 2, ...), once per subtile.
+        auto meet = [&](int n) {
+            if (lane == 0) __hip_atomic_fetch_add(&psync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            while (__hip_atomic_load(&psync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < L::NP * n)
+                __builtin_amdgcn_s_sleep(1);
+        };
+        rows_to_lds<D, 64 * L::NP>(ksl0, K, row0, stride, t_begin, N, tid, lane);
+        FLARE_WAIT_VMCNT(0);
         __syncthreads();   // B0: K rows of subtile 0 and the lane tables visible
-        for (int j = 0; j <= NS; ++j) {
+        // One subtile per call.  The buffer parity is a compile-time constant, so each LDS
+        // buffer below is one fixed array; the next subtile's K rows go by DMA
+        // (global_load_lds) into the other K array while this one is read.
+        auto subtile = [&](auto parity, int j) {
+            constexpr int buf = decltype(parity)::value;
+            const bf16* kj = buf ? ksl1 : ksl0;
+            bf16* knext = buf ? ksl0 : ksl1;
+            // Lane-derived values (LDS addresses above all) are rebuilt from an opaque
+            // copy of the lane id each subtile instead of being held across the loop.
+            int lq = lane;
+            asm volatile("" : "+v"(lq));
+            const int c = lq & 15, g = lq >> 4;
             if (j < NS) {
-                const int buf = j & 1;
                 const int t0 = t_begin + T * j;
-                if (j + 1 < NS) kr.load(K, row0, stride, t0 + T, N, tid);
+                if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
                 // ---- raw scores A = Q K^T for this wave's latents (S = scale2 A):
                 //      acc[mi][ti][r] = A[t = 16 ti + c][m = 16 mi + 4 g + r], -inf for invalid tokens
-                const bf16* kj = ksl[buf];
                 const bool ragged = t0 + T > t_end;
                 f32x4 acc[L::MTP][2];
 #pragma unroll
@@ -292,9 +308,7 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
                         if (g == 0) lsep[buf][w * T + 16 * ti + c] = float2{lm[ti], l};
                     }
                 }
-                if (lane == 0) __hip_atomic_fetch_add(&psync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                while (__hip_atomic_load(&psync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < L::NP * (j + 1))
-                    __builtin_amdgcn_s_sleep(1);
+                meet(j + 1);
                 float fw[2];
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) {
@@ -317,21 +331,22 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
                 f32x4 gacc[3];    // G_w^T tiles (t tile, tau tile) = (0,0), (1,0), (1,1)
 #pragma unroll
                 for (int q3 = 0; q3 < 3; ++q3) gacc[q3] = f32x4{0.f, 0.f, 0.f, 0.f};
-                // E^T of latent tile mi (fp16) to LDS, and its cumulative sums over the subtile
-                // d_t - d0 = sum_{tau<=t} E16 by MFMA against tri (the same fp16 E as the
-                // numerator update); dcum[ti][r] is for t = 16 ti + c, m = 16 mi + 4 g + r.
+                // E^T of latent tile mi (fp16) to LDS, and the cumulative den over the subtile
+                // d_t = d0 + sum_{tau<=t} E16 by MFMA against tri with d0 as the accumulator's
+                // start (the same fp16 E as the numerator update); dcum[ti][r] is d_t for
+                // t = 16 ti + c, m = 16 mi + 4 g + r.
                 auto cumulate = [&](int mi, const float (&em)[2][4], f16x4 (&e16)[2], f32x4 (&dcum)[2]) {
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) e16[ti][r] = (f16)em[ti][r];
+                        e16[ti] = __builtin_convertvector((f32x4{em[ti][0], em[ti][1], em[ti][2], em[ti][3]}), f16x4);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) et[(mp0 + 16 * mi + 4 * g + r) * L::EP + 16 * ti + c] = e16[ti][r];
                     }
                     const f16x8 ea = load8<f16x8>(et + (mp0 + 16 * mi + c) * L::EP + 8 * g);
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti)
-                        dcum[ti] = mma(ea, load8<f16x8>(tril + (ti * 64 + lane) * 8), f32x4{0.f, 0.f, 0.f, 0.f});
+                        dcum[ti] = mma(ea, load8<f16x8>(tril + (ti * 64 + lane) * 8),
+                                       f32x4{dn[mi][0], dn[mi][1], dn[mi][2], dn[mi][3]});
                 };
                 dnbig = false;
                 if (!slow) {
@@ -352,14 +367,14 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) {
                                     const float p = e[mi][ti][r] * (ar[r] * bt[ti]);     // alpha
-                                    q[r] = p * __builtin_amdgcn_rcpf(dn[mi][r] + dcum[ti][r]);
+                                    q[r] = p * __builtin_amdgcn_rcpf(dcum[ti][r]);
                                 }
                                 split_f16x4(q, whi[jb][ti], wlo[jb][ti]);
                                 *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::WP + mp0 + 16 * mi + 4 * g) = whi[jb][ti];
                             }
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {      // den at the subtile end (column t = 31)
-                                dn[mi][r] += row_bcast15(dcum[1][r]);
+                                dn[mi][r] = row_bcast15(dcum[1][r]);
                                 dnbig |= dn[mi][r] > kDenMax;
                             }
                         }
@@ -437,9 +452,13 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
 #pragma unroll
                 for (int q3 = 0; q3 < 3; ++q3)
                     *reinterpret_cast<f32x4*>(gpl[buf] + ((w * 3 + q3) * 16 + c) * L::GP + 4 * g) = gacc[q3];
-                if (j + 1 < NS) kr.store(ksl[buf ^ 1], tid);
+                FLARE_WAIT_VMCNT(0);     // this wave's K rows of the next subtile have landed
             }
             __syncthreads();   // hand-off: subtile j's operands visible, subtile j-1's consumed
+        };
+        for (int j = 0; j <= NS; j += 2) {
+            subtile(std::integral_constant<int, 0>{}, j);
+            if (j + 1 <= NS) subtile(std::integral_constant<int, 1>{}, j + 1);
         }
     } else {
         // =========================== consumer ===========================
@@ -487,6 +506,9 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
                 const int j = it - 1;
                 const int buf = j & 1;
                 const int t0 = t_begin + T * j;
+                int mv[L::NP];     // read ahead of this wave's V^T stores (LDS requests stay in order)
+#pragma unroll
+                for (int w2 = 0; w2 < L::NP; ++w2) mv[w2] = movedl[buf][w2];
                 float vlane = vt.absmax(lane) * vs;
                 vlane = __builtin_isfinite(vlane) ? vlane : 0.0f;   // inf / nan propagate unscaled
                 if (__any(vlane > L::kVCap)) {      // rare: rescale the wave's columns
@@ -504,9 +526,6 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
                 }
                 if (vs == 1.0f) vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, 1.0f);
                 else vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, vs);
-                int mv[L::NP];
-#pragma unroll
-                for (int w2 = 0; w2 < L::NP; ++w2) mv[w2] = movedl[buf][w2];
                 // ---- readout at the subtile start: y = sum_m W1[t,m] U[m]; for the latents of a
                 //      producer group that moved a reference, z0 = U / d0 against W1 = W2 d0
                 auto normalise = [&](int w2, bool back) {
@@ -557,41 +576,42 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
                 for (int w2 = 0; w2 < L::NP; ++w2)
                     if (mv[w2]) normalise(w2, true);    // back from z0 to the (rescaled) numerator
                 vt.load(V, row0, stride, t0 + T, t_end, dc0, lane);   // the next subtile's V
-                // ---- G[t][tau] = sum_w G_w[t][tau] (tau <= t) for this lane's B operand:
-                //      t = 16 ti + c, tau = 8 g .. 8 g + 7; split hi + lo (fp16)
+                // ---- G^T B operands: t = 16 ti + c, tau = 8 g .. 8 g + 7 (hi + lo, fp16)
                 f16x8 gh[2], go[2];
+                {
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    const int t = 16 * ti + c;
-                    const int ui = g >> 1;     // tau tile
-                    float ga[8];
+                    for (int ti = 0; ti < 2; ++ti) {    // sum the producers' partial tiles here
+                        const int t = 16 * ti + c;
+                        const int ui = g >> 1;     // tau tile
+                        float ga[8];
 #pragma unroll
-                    for (int e2 = 0; e2 < 8; ++e2) ga[e2] = 0.0f;
-                    if (ui <= ti) {
-                        const int q3 = ti + ui;     // (0,0) -> 0, (1,0) -> 1, (1,1) -> 2
+                        for (int e2 = 0; e2 < 8; ++e2) ga[e2] = 0.0f;
+                        if (ui <= ti) {
+                            const int q3 = ti + ui;     // (0,0) -> 0, (1,0) -> 1, (1,1) -> 2
 #pragma unroll
-                        for (int w2 = 0; w2 < L::NP; ++w2) {
-                            const float* src = gpl[buf] + ((w2 * 3 + q3) * 16 + c) * L::GP + 8 * (g & 1);
-                            const f32x4 a0 = *reinterpret_cast<const f32x4*>(src);
-                            const f32x4 a1 = *reinterpret_cast<const f32x4*>(src + 4);
+                            for (int w2 = 0; w2 < L::NP; ++w2) {
+                                const float* src = gpl[buf] + ((w2 * 3 + q3) * 16 + c) * L::GP + 8 * (g & 1);
+                                const f32x4 a0 = *reinterpret_cast<const f32x4*>(src);
+                                const f32x4 a1 = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
-                            for (int e2 = 0; e2 < 4; ++e2) {
-                                ga[e2] += a0[e2];
-                                ga[4 + e2] += a1[e2];
+                                for (int e2 = 0; e2 < 4; ++e2) {
+                                    ga[e2] += a0[e2];
+                                    ga[4 + e2] += a1[e2];
+                                }
                             }
+#pragma unroll
+                            for (int e2 = 0; e2 < 8; ++e2)
+                                if (8 * g + e2 > t) ga[e2] = 0.0f;
                         }
 #pragma unroll
-                        for (int e2 = 0; e2 < 8; ++e2)
-                            if (8 * g + e2 > t) ga[e2] = 0.0f;
-                    }
-#pragma unroll
-                    for (int e2 = 0; e2 < 8; e2 += 2) {
-                        f16x2 hh, ll;
-                        split_f16_pair(ga[e2], ga[e2 + 1], hh, ll);
-                        gh[ti][e2] = hh[0];
-                        gh[ti][e2 + 1] = hh[1];
-                        go[ti][e2] = ll[0];
-                        go[ti][e2 + 1] = ll[1];
+                        for (int e2 = 0; e2 < 8; e2 += 2) {
+                            f16x2 hh, ll;
+                            split_f16_pair(ga[e2], ga[e2 + 1], hh, ll);
+                            gh[ti][e2] = hh[0];
+                            gh[ti][e2 + 1] = hh[1];
+                            go[ti][e2] = ll[0];
+                            go[ti][e2 + 1] = ll[1];
+                        }
                     }
                 }
                 const f16* et = etl[buf];
