@@ -77,9 +77,9 @@ def bench_prefill(torch, flare, steps, warmup):
         "B": B, "N": N, "H": H, "M": M, "D": D, "ms_per_step": ms, "tok_s": tok_s,
         "phase_ms": phases, "alg_tflop_per_step": flops / 1e12,
         "roofline": {
-            "bound": "mfma", "kernel": "chunk_output_kernel", "achieved": achieved,
+            "bound": "mfma", "kernel": "chunk_output_pc", "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": measured_traffic("chunk_output_mfma"), "whole_pass_tflops": whole,
+            "traffic": measured_traffic("chunk_output_pc"), "whole_pass_tflops": whole,
             "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
         },
     }

@@ -67,7 +67,6 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     constexpr int VP = T + 8;      // padded row of the transposed V tile
     __shared__ __attribute__((aligned(16))) f16 vtl[2][D * VP];
     __shared__ __attribute__((aligned(16))) bf16 ksl[2][T * D];   // K rows of a subtile (swizzled)
-    __shared__ __attribute__((aligned(16))) bf16 qs[M * D];       // Q[h] (swizzled rows)
     __shared__ int vbig[2];        // subtile index whose V^T buffer holds a value outside fp16
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
@@ -77,10 +76,13 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     const int g = lane >> 4, c = lane & 15;
     const int m0 = 32 * w;                       // this wave's 32 latents
 
-    for (int vi = tid; vi < M * D / 8; vi += NT) {
-        const int m = vi / (D / 8), jc = vi % (D / 8);
-        *reinterpret_cast<bf16x8*>(qs + m * D + 8 * swz<D>(m, jc)) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * jc);
-    }
+    // this wave's Q rows as MFMA B operands (n = m, k = d), held in registers
+    bf16x8 qb[2][KS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kq = 0; kq < KS; ++kq)
+            qb[mt][kq] = load8<bf16x8>(Q + ((size_t)h * M + m0 + 16 * mt + c) * D + 32 * kq + 8 * g);
     f32x4 U[2][DT];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
@@ -94,12 +96,13 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
     if (tid < 2) vbig[tid] = -1;
-    // K rows reach LDS directly (double-buffered, issued one subtile ahead);
+    // K rows go through registers (loaded a subtile ahead, stored before the barrier);
     // V comes through registers, also one subtile ahead.
     VTile<D, NT> vt;
-    rows_to_lds<D, NT>(ksl[0], K, row0, stride, t_begin, N, tid, lane);
+    KRows<D, NT> kr;
+    kr.load(K, row0, stride, t_begin, N, tid);
+    kr.store(ksl[0], tid);
     vt.load(V, row0, stride, t_begin, t_end, 0, tid);
-    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     int j = 0;
     for (int t0 = t_begin; t0 < t_end; t0 += T, ++j) {
@@ -107,7 +110,10 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
         const bf16* kj = ksl[j & 1];
         if (vt.template store_f16<VP>(vtj, 0, tid)) vbig[j & 1] = j;
         const bool more = t0 + T < t_end;
-        if (more) rows_to_lds<D, NT>(ksl[(j + 1) & 1], K, row0, stride, t0 + T, N, tid, lane);
+        // the next subtile's K rows through registers (stored to LDS before this
+        // subtile's barrier) and its V rows (staged at the next subtile's start);
+        // K is issued first, so that waiting for it leaves the V loads in flight
+        if (more) kr.load(K, row0, stride, t0 + T, N, tid);
         vt.load(V, row0, stride, t0 + T, t_end, 0, tid);
         // S = K Q^T, tokens as rows: s[mt][ti][r] = S[t = 16 ti + 4 g + r][m = 16 mt + c]
         float s[2][2][4];
@@ -117,18 +123,13 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
             for (int mt = 0; mt < 2; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kq = 0; kq < KS; ++kq) {
-                bf16x8 ka[2], qb[2];
+                bf16x8 ka[2];
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) ka[ti] = load8<bf16x8>(kj + (16 * ti + c) * D + 8 * swz<D>(16 * ti + c, 4 * kq + g));
 #pragma unroll
-                for (int mt = 0; mt < 2; ++mt) {
-                    const int m = m0 + 16 * mt + c;
-                    qb[mt] = load8<bf16x8>(qs + m * D + 8 * swz<D>(m, 4 * kq + g));
-                }
-#pragma unroll
                 for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka[ti], qb[mt], acc[mt][ti]);
+                    for (int mt = 0; mt < 2; ++mt) acc[mt][ti] = mma(ka[ti], qb[mt][kq], acc[mt][ti]);
             }
 #pragma unroll
             for (int mt = 0; mt < 2; ++mt)
@@ -190,8 +191,7 @@ __global__ __launch_bounds__(64 * NWP) void chunk_prepare_mfma(
                 }
             dl[mt] += es;
         }
-        // this thread's K rows of the next subtile have landed (its V loads may still be in flight)
-        if (more) FLARE_WAIT_VMCNT((VTile<D, NT>::NS));
+        if (more) kr.store(ksl[(j + 1) & 1], tid);
         __syncthreads();   // V^T of this subtile (and its range flag), next K rows visible
         if (vbig[j & 1] != j) {
 #pragma unroll
