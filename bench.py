@@ -151,7 +151,7 @@ def bench_decode(torch, flare, steps=256):
         "tok_s": B * steps / dt_graph, "ms_per_step": k_ms,
         "tok_s_eager_api_loop": B * steps / dt_eager, "ms_per_step_eager": dt_eager * 1e3 / steps,
         "roofline": {
-            "bound": "hbm", "kernel": "decode_step_kernel", "achieved": achieved,
+            "bound": "hbm", "kernel": "decode_step_fast", "achieved": achieved,
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
             "alg_bytes_per_step": bytes_step,
             "note": "graph replay of 256 back-to-back steps; per-step time includes launch gaps",

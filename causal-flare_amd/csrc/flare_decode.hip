@@ -154,6 +154,121 @@ __global__ __launch_bounds__(kDecNT) void decode_step_kernel(
     }
 }
 
+// Fast step for the common shapes: M = RG * ROWS latents and Dv = 4 * NT4 value
+// columns with RG = 256 / NT4, so every thread owns ROWS rows of one float4
+// column of u.  Those rows, and m / d of the thread's latent, are loaded at the
+// very start; their HBM latency overlaps the scores and the softmax, and the
+// update is applied from registers.  Q rows are read with 16-byte loads.
+template <typename T, int ROWS, int NT4>
+__global__ __launch_bounds__(kDecNT) void decode_step_fast(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
+    const T* __restrict__ Qdec, const T* __restrict__ Kdec, const int32_t* __restrict__ mask,
+    int H, int M, int Dk, int Dv, float scale, bool shared, float* __restrict__ mst,
+    float* __restrict__ dst, float* __restrict__ ust, void* __restrict__ Y, int out_dtype) {
+    constexpr int RG = kDecNT / NT4;
+    extern __shared__ float smem[];
+    float* kv = smem;                 // [Dk]
+    float* qd = kv + Dk;              // [Dk]
+    float* vv = qd + Dk;              // [Dv]
+    float* av = vv + Dv;              // [M] decoder scores
+    float* gam = av + M;              // [M]
+    float* eta = gam + M;             // [M]
+    float* wts = eta + M;             // [M]
+    float* red = wts + M;             // [8]
+    float4* ypart = reinterpret_cast<float4*>(smem + ((2 * Dk + Dv + 4 * M + 8 + 3) & ~3));  // [RG][NT4]
+
+    const int bh = blockIdx.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x;
+    const int jt = tid % NT4, rg = tid / NT4;
+    if (mask != nullptr && mask[b] == 0) {
+        for (int j = tid; j < Dv; j += kDecNT) store_out_dec(Y, (size_t)bh * Dv + j, 0.0f, out_dtype);
+        return;
+    }
+    // prefetch: this thread's rows of u and the state of latent m = tid
+    float4* u4 = reinterpret_cast<float4*>(ust + (size_t)bh * M * Dv);
+    float4 ur[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) ur[r] = u4[(size_t)(rg + r * RG) * NT4 + jt];
+    const size_t si = (size_t)bh * M + tid;
+    const bool own = tid < M;
+    const float m_old = own ? mst[si] : 0.0f;
+    const float d_old = own ? dst[si] : 0.0f;
+    const size_t kvoff = (size_t)bh * Dk;
+    for (int j = tid; j < Dk; j += kDecNT) {
+        kv[j] = to_f32(K[kvoff + j]);
+        if (!shared) qd[j] = to_f32(Qdec[kvoff + j]);
+    }
+    for (int j = tid; j < Dv; j += kDecNT) vv[j] = to_f32(V[(size_t)bh * Dv + j]);
+    __syncthreads();
+
+    // scores: thread m dots its Q row (16-byte loads; Q[h] is shared by the batch, L2-resident)
+    constexpr int CH = 16 / sizeof(T);
+    float amax = kNegInf;
+    if (own) {
+        auto dot = [&](const T* row, const float* x) {
+            float acc = 0.0f;
+#pragma unroll 4
+            for (int d0 = 0; d0 < Dk; d0 += CH) {
+                union { uint4 raw; T el[CH]; } qv;
+                qv.raw = *reinterpret_cast<const uint4*>(row + d0);
+#pragma unroll
+                for (int e = 0; e < CH; ++e) acc += to_f32(qv.el[e]) * x[d0 + e];
+            }
+            return acc;
+        };
+        const float s = dot(Q + ((size_t)h * M + tid) * Dk, kv) * scale;
+        const float a = shared ? s : dot(Kdec + ((size_t)h * M + tid) * Dk, qd) * scale;
+        const MergeScales ts = token_scales(m_old, s);
+        const float dn = d_old * ts.sa + ts.sb;
+        mst[si] = ts.m_new;
+        dst[si] = dn;
+        gam[tid] = ts.sa;
+        eta[tid] = ts.sb;
+        wts[tid] = dn > 0.0f ? dn : 1.0f;
+        av[tid] = a;
+        amax = a;
+    }
+    amax = block_max<kDecNT>(amax, red);
+    const float ea = own ? __expf(av[tid] - amax) : 0.0f;
+    const float asum = block_sum<kDecNT>(ea, red);
+    if (own) wts[tid] = ea / (asum * wts[tid]);
+    __syncthreads();
+
+    // numerator update and readout from the prefetched rows
+    const float4 vj = reinterpret_cast<const float4*>(vv)[jt];
+    float4 y4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int m = rg + r * RG;
+        const float g = gam[m], e = eta[m], w = wts[m];
+        float4 x = ur[r];
+        x.x = x.x * g + e * vj.x;
+        x.y = x.y * g + e * vj.y;
+        x.z = x.z * g + e * vj.z;
+        x.w = x.w * g + e * vj.w;
+        u4[(size_t)m * NT4 + jt] = x;
+        y4.x += w * x.x;
+        y4.y += w * x.y;
+        y4.z += w * x.z;
+        y4.w += w * x.w;
+    }
+    ypart[rg * NT4 + jt] = y4;
+    __syncthreads();
+    if (tid < NT4) {
+        float4 acc = ypart[tid];
+        for (int g2 = 1; g2 < RG; ++g2) {
+            const float4 p = ypart[g2 * NT4 + tid];
+            acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+        }
+        const size_t yo = (size_t)bh * Dv + 4 * tid;
+        store_out_dec(Y, yo + 0, acc.x, out_dtype);
+        store_out_dec(Y, yo + 1, acc.y, out_dtype);
+        store_out_dec(Y, yo + 2, acc.z, out_dtype);
+        store_out_dec(Y, yo + 3, acc.w, out_dtype);
+    }
+}
+
 }  // namespace flare
 
 using namespace flare;
@@ -176,6 +291,49 @@ extern "C" int flare_decode_step(const void* Q, const void* K, const void* V, co
     FLARE_REQUIRE(sm <= 64 * 1024, "decode_step: shape too large for LDS");
     (void)NT4;
     hipStream_t s = (hipStream_t)stream;
+    // fast path: M = (256 / NT4) * ROWS with Dv = 4 * NT4, M <= 256, Dk a multiple of 16 bytes
+    {
+        const int64_t D4 = Dv / 4;
+        const int64_t esz = dtype == FLARE_F32 ? 4 : 2;
+        const bool pow2 = D4 > 0 && D4 <= kDecNT && (D4 & (D4 - 1)) == 0;
+        const int64_t RG = pow2 ? kDecNT / D4 : 0;
+        const int64_t rows = RG ? M / RG : 0;
+        const bool aligned = ((uintptr_t)Q & 15) == 0 && (!Kdec || ((uintptr_t)Kdec & 15) == 0);
+        if (pow2 && M <= kDecNT && rows * RG == M && (Dk * esz) % 16 == 0 && aligned &&
+            (rows == 1 || rows == 2 || rows == 4 || rows == 8 || rows == 16)) {
+#define FLARE_DEC_FAST(TY, RW, N4)                                                                         \
+    hipLaunchKernelGGL((decode_step_fast<TY, RW, N4>), dim3((unsigned)(B * H)), dim3(kDecNT), sm, s,        \
+                       (const TY*)Q, (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd, mask, (int)H, \
+                       (int)M, (int)Dk, (int)Dv, scale, shared, m, d, u, y, out_dtype)
+#define FLARE_DEC_ROWS(TY, N4)                                   \
+    switch (rows) {                                              \
+        case 1: FLARE_DEC_FAST(TY, 1, N4); break;                \
+        case 2: FLARE_DEC_FAST(TY, 2, N4); break;                \
+        case 4: FLARE_DEC_FAST(TY, 4, N4); break;                \
+        case 8: FLARE_DEC_FAST(TY, 8, N4); break;                \
+        default: FLARE_DEC_FAST(TY, 16, N4); break;              \
+    }
+#define FLARE_DEC_N4(TY)                                         \
+    switch (D4) {                                                \
+        case 1: FLARE_DEC_ROWS(TY, 1) break;                     \
+        case 2: FLARE_DEC_ROWS(TY, 2) break;                     \
+        case 4: FLARE_DEC_ROWS(TY, 4) break;                     \
+        case 8: FLARE_DEC_ROWS(TY, 8) break;                     \
+        case 16: FLARE_DEC_ROWS(TY, 16) break;                   \
+        case 32: FLARE_DEC_ROWS(TY, 32) break;                   \
+        case 64: FLARE_DEC_ROWS(TY, 64) break;                   \
+        case 128: FLARE_DEC_ROWS(TY, 128) break;                 \
+        default: FLARE_DEC_ROWS(TY, 256) break;                  \
+    }
+            if (dtype == FLARE_BF16) { FLARE_DEC_N4(__hip_bfloat16) }
+            else if (dtype == FLARE_F16) { FLARE_DEC_N4(__half) }
+            else { FLARE_DEC_N4(float) }
+#undef FLARE_DEC_N4
+#undef FLARE_DEC_ROWS
+#undef FLARE_DEC_FAST
+            return check_launch("decode_step_fast");
+        }
+    }
 #define FLARE_DEC(TY)                                                                          \
     hipLaunchKernelGGL(decode_step_kernel<TY>, dim3((unsigned)(B * H)), dim3(kDecNT), sm, s,     \
                        (const TY*)Q, (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd,   \
