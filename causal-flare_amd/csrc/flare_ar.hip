@@ -437,9 +437,9 @@ int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
             cus = 256;
     }
     const int64_t BH = B * H;
-    // the large-bank output kernel fills a compute unit with one workgroup;
-    // smaller banks fit two
-    const int64_t per_cu = (M * Dv >= 256 * 128) ? 1 : 2;
+    // the output kernel fills a compute unit with one workgroup, except for the
+    // small banks (M * Dv below 128 x 128), where two share it
+    const int64_t per_cu = (M * Dv >= 128 * 128) ? 1 : 2;
     const int64_t target_chunks = (per_cu * cus + BH - 1) / BH;
     int64_t c = (N + target_chunks - 1) / target_chunks;
     c = ((c + 63) / 64) * 64;

@@ -2,9 +2,10 @@
 // wave-specialised producer and consumer waves (bf16 inputs, shared
 // encoder/decoder weights, M in {128, 256}, D in {64, 128}).
 //
-// One workgroup of 8 waves replays one chunk of one (b,h) in 32-token subtiles.
-// Waves 0-3 (producers) own M/4 latents each; waves 4-7 (consumers) own D/4
-// value columns each and the numerator U[M][their columns] in registers.  In
+// One workgroup of 2 NPW waves replays one chunk of one (b,h) in 32-token
+// subtiles.  Waves 0 .. NPW-1 (producers) own M/NPW latents each; the other NPW
+// waves (consumers) own D/NPW value columns each and the numerator
+// U[M][their columns] in registers.  In
 // iteration j the producers turn subtile j into its softmax operands while the
 // consumers fold subtile j-1 into the output and the state, so that on every
 // SIMD one VALU-heavy producer wave runs beside one MFMA-heavy consumer wave.
@@ -20,7 +21,7 @@
 //   y_t       = sum_m W2[t,m] U[m] + sum_{tau<=t} G[t,tau] v_tau,   then U += E^T V
 // Per subtile each producer forms S for its latents, E (fp16 E^T to LDS) and
 // the cumulative den (an MFMA of E16 against a triangular ones matrix), and
-// publishes its partial (max, sum) of the token softmax; the four producers
+// publishes its partial (max, sum) of the token softmax; the producers
 // meet at an LDS counter (consumers never wait there) and each scales its own
 // weights by f_w(t) = 2^(lm_w(t) - lse_t).  alpha = E 2^(R - Rmax) 2^(Rmax - lm_w)
 // f_w reuses E (no second exponential) while Rmax - lm_w stays in range.  The
@@ -40,10 +41,10 @@
 namespace flare {
 namespace mfma {
 
-template <int M, int D>
+template <int M, int D, int NPW>
 struct PCLayout {
-    static constexpr int NP = 4;             // producer waves
-    static constexpr int NCW = 4;            // consumer waves
+    static constexpr int NP = NPW;           // producer waves
+    static constexpr int NCW = NPW;          // consumer waves
     static constexpr int NT = 64 * (NP + NCW);
     static constexpr int MP = M / NP;        // latents per producer
     static constexpr int MTP = MP / 16;      // latent tiles per producer
@@ -63,12 +64,12 @@ struct PCLayout {
     static_assert(DC % 16 == 0, "value columns per consumer must be a multiple of 16");
 };
 
-template <int M, int D>
-__global__ __launch_bounds__(512, 1) void chunk_output_pc(
+template <int M, int D, int NPW>
+__global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype) {
-    using L = PCLayout<M, D>;
+    using L = PCLayout<M, D, NPW>;
     // K rows of the even / odd subtiles (swizzled); two arrays rather than one so
     // that reads of one never wait on the DMA that fills the other
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(512, 1) void chunk_output_pc(
         };
         refresh_ar();
         if (tid == 0) psync = 0;
-        // The four producers meet (consumers never take part): each adds one arrival
+        // The producers meet (consumers never take part): each adds one arrival
         // and waits for the count of meeting n (1, 2, ...), once per subtile.
         auto meet = [&](int n) {
             if (lane == 0) __hip_atomic_fetch_add(&psync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -664,14 +665,16 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_OUT_PC(MM, DD)                                                                            \
-    hipLaunchKernelGGL((chunk_output_pc<MM, DD>), grid, dim3(512), 0, stream, (const bf16*)Q,            \
+#define FLARE_OUT_PC(MM, DD, NW)                                                                         \
+    hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
                        (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y, \
                        out_dtype)
-    if (M == 128 && D == 64) FLARE_OUT_PC(128, 64);
-    else if (M == 128 && D == 128) FLARE_OUT_PC(128, 128);
-    else if (M == 256 && D == 64) FLARE_OUT_PC(256, 64);
-    else FLARE_OUT_PC(256, 128);
+    // The 128 x 64 bank runs 2 + 2 waves (72 KiB of LDS: two workgroups share a CU);
+    // the larger banks 4 + 4 (one workgroup fills a CU).
+    if (M == 128 && D == 64) FLARE_OUT_PC(128, 64, 2);
+    else if (M == 128 && D == 128) FLARE_OUT_PC(128, 128, 4);
+    else if (M == 256 && D == 64) FLARE_OUT_PC(256, 64, 4);
+    else FLARE_OUT_PC(256, 128, 4);
 #undef FLARE_OUT_PC
     return check_launch("chunk_output_pc");
 }
