@@ -762,6 +762,8 @@ bool mfma_output_supported(int dtype, int out_dtype, bool shared, int64_t M, int
 int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                         int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
                         float* cnum, hipStream_t stream) {
+    if (output_pc_enabled() && (M == 128 || M == 256))
+        return launch_prepare_pc(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, stream);
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_mfma: chunk must be a multiple of %d", T);
     FLARE_REQUIRE(M % 32 == 0 && M >= 32 && M <= kMaxPrepM && (D == 64 || D == 128),
                   "chunk_prepare_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);

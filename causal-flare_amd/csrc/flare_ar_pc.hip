@@ -652,6 +652,239 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Phase 1 with the same wave roles: chunk summaries (max, den, num) of one chunk
+// of one (b,h), the reference's flare_chunk_prepare (training.py:914-1018).
+// Producers form S = K Q^T with tokens as rows (lane: 4 tokens of one latent),
+// keep the lazy reference R, the true max and den per latent, and write
+// E^T (fp16, 8-byte stores) for the subtile; consumers fold it into
+// U[M][their columns] += E^T V.  Same hand-off, K DMA and V scaling as the
+// output kernel above.  The summary is returned relative to the true chunk
+// max: (max, den 2^(R - max), U 2^(R - max)) in natural-log units.
+// ---------------------------------------------------------------------------
+template <int M, int D, int NPW>
+__global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
+    const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
+    float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum) {
+    using L = PCLayout<M, D, NPW>;
+    __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
+    __shared__ __attribute__((aligned(16))) bf16 ksl1[T * D];
+    __shared__ __attribute__((aligned(16))) f16 etl[2][M * L::EP];              // E^T[m][tau]
+    __shared__ __attribute__((aligned(16))) float gaml[2][M];                   // rescale factor (moved groups)
+    __shared__ int movedl[2][L::NP];
+    __shared__ __attribute__((aligned(16))) f16 vtl[D * L::EP];                 // V^T, consumer-private rows
+    __shared__ __attribute__((aligned(16))) float fl[M];                        // 2^(R - max) at the end
+
+    const int c_idx = blockIdx.x, bh = blockIdx.y;
+    const int NC = gridDim.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int t_begin = c_idx * chunk;
+    const int t_end = min(N, t_begin + chunk);
+    const int NS = (t_end - t_begin + T - 1) / T;
+    const size_t stride = (size_t)H * D;
+    const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
+    const size_t sbase = ((size_t)bh * NC + c_idx) * M;
+
+    if (w < L::NP) {
+        // =========================== producer ===========================
+        const int mp0 = w * L::MP;
+        // Q rows of this wave's latents as MFMA B operands (n = m, k = d)
+        bf16x8 qb[L::MTP][L::KS];
+#pragma unroll
+        for (int mt = 0; mt < L::MTP; ++mt)
+#pragma unroll
+            for (int kq = 0; kq < L::KS; ++kq)
+                qb[mt][kq] = load8<bf16x8>(Q + ((size_t)h * M + mp0 + 16 * mt + c) * D + 32 * kq + 8 * g);
+        // per latent m = mp0 + 16 mt + c (replicated over g): reference R and true max rt
+        // (log2 units); dl is this lane's part of den
+        float R[L::MTP], rt[L::MTP], dl[L::MTP];
+#pragma unroll
+        for (int mt = 0; mt < L::MTP; ++mt) {
+            R[mt] = kNegInf;
+            rt[mt] = kNegInf;
+            dl[mt] = 0.0f;
+        }
+        rows_to_lds<D, 64 * L::NP>(ksl0, K, row0, stride, t_begin, N, tid, lane);
+        FLARE_WAIT_VMCNT(0);
+        __syncthreads();   // B0
+        auto subtile = [&](auto parity, int j) {
+            constexpr int buf = decltype(parity)::value;
+            const bf16* kj = buf ? ksl1 : ksl0;
+            bf16* knext = buf ? ksl0 : ksl1;
+            int lq = lane;
+            asm volatile("" : "+v"(lq));
+            const int c = lq & 15, g = lq >> 4;
+            if (j < NS) {
+                const int t0 = t_begin + T * j;
+                if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
+                // ---- A = K Q^T, tokens as rows: acc[mt][ti][r] = A[t = 16 ti + 4 g + r][m = 16 mt + c]
+                f32x4 acc[L::MTP][2];
+#pragma unroll
+                for (int mt = 0; mt < L::MTP; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kq = 0; kq < L::KS; ++kq) {
+                    bf16x8 ka[2];
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        const int row = 16 * ti + c;
+                        ka[ti] = load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g));
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < L::MTP; ++mt)
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) acc[mt][ti] = mma(ka[ti], qb[mt][kq], acc[mt][ti]);
+                }
+                if (t0 + T > t_end) {      // the ragged last subtile
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (t0 + 16 * ti + 4 * g + r >= t_end)
+#pragma unroll
+                                for (int mt = 0; mt < L::MTP; ++mt) acc[mt][ti][r] = kNegInf;
+                }
+                // ---- lazy reference: checked per lane, moved (to the exact max over the latent) rarely
+                float mx[L::MTP];
+                bool need = false;
+#pragma unroll
+                for (int mt = 0; mt < L::MTP; ++mt) {
+                    mx[mt] = fmaxf(fmaxf(fmaxf(acc[mt][0][0], acc[mt][0][1]), fmaxf(acc[mt][0][2], acc[mt][0][3])),
+                                   fmaxf(fmaxf(acc[mt][1][0], acc[mt][1][1]), fmaxf(acc[mt][1][2], acc[mt][1][3]))) * scale2;
+                    rt[mt] = fmaxf(rt[mt], mx[mt]);
+                    need |= mx[mt] > R[mt] + kLazy;
+                }
+                const bool moved = __any(need);
+                if (moved) {
+#pragma unroll
+                    for (int mt = 0; mt < L::MTP; ++mt) {
+                        const float m4 = rows_max4(mx[mt]);
+                        const bool mv = m4 > R[mt] + kLazy;
+                        const float Rn = mv ? m4 : R[mt];
+                        const float gam = mv ? exp2f_fast(R[mt] - Rn) : 1.0f;     // 0 when R = -inf
+                        R[mt] = Rn;
+                        dl[mt] *= gam;
+                        if (g == 0) gaml[buf][mp0 + 16 * mt + c] = gam;
+                    }
+                }
+                if (lane == 0) movedl[buf][w] = moved ? 1 : 0;
+                // ---- E = 2^(S - R): den partial, and E^T (fp16) to LDS, four tokens per store
+                f16* et = etl[buf];
+#pragma unroll
+                for (int mt = 0; mt < L::MTP; ++mt) {
+                    float es = 0.0f;
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        f32x4 e;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            e[r] = exp2f_fast(fmaf(acc[mt][ti][r], scale2, -R[mt]));
+                            es += e[r];
+                        }
+                        *reinterpret_cast<f16x4*>(et + (mp0 + 16 * mt + c) * L::EP + 16 * ti + 4 * g) =
+                            __builtin_convertvector(e, f16x4);
+                    }
+                    dl[mt] += es;
+                }
+                FLARE_WAIT_VMCNT(0);     // this wave's K rows of the next subtile have landed
+            }
+            __syncthreads();   // hand-off: subtile j's E^T visible, subtile j-1's consumed
+        };
+        for (int j = 0; j <= NS; j += 2) {
+            subtile(std::integral_constant<int, 0>{}, j);
+            if (j + 1 <= NS) subtile(std::integral_constant<int, 1>{}, j + 1);
+        }
+        // ---- the summary relative to the true chunk max
+#pragma unroll
+        for (int mt = 0; mt < L::MTP; ++mt) {
+            const float Rt = rows_max4(rt[mt]);
+            const float den = rows_sum4(dl[mt]);
+            const float f = Rt == kNegInf ? 0.0f : exp2f_fast(R[mt] - Rt);    // <= 1
+            if (g == 0) {
+                const int m = mp0 + 16 * mt + c;
+                cmax[sbase + m] = Rt * kLn2;
+                cden[sbase + m] = den * f;
+                fl[m] = f;
+            }
+        }
+        __syncthreads();   // fl visible
+    } else {
+        // =========================== consumer ===========================
+        const int cw = w - L::NP;
+        const int dc0 = cw * L::DC;
+        f32x4 U[L::MTA][L::DTC];
+#pragma unroll
+        for (int mi = 0; mi < L::MTA; ++mi)
+#pragma unroll
+            for (int di = 0; di < L::DTC; ++di) U[mi][di] = f32x4{0.f, 0.f, 0.f, 0.f};
+        float vs = 1.0f;     // V' = V vs, U' = U vs (powers of two keep |V'| <= kVCap)
+        VTile<L::DC, 64> vt;
+        vt.load(V, row0, stride, t_begin, t_end, dc0, lane);
+        __syncthreads();   // B0
+        for (int it = 0; it <= NS; ++it) {
+            if (it > 0) {
+                const int j = it - 1;
+                const int buf = j & 1;
+                const int t0 = t_begin + T * j;
+                int mv[L::NP];
+#pragma unroll
+                for (int w2 = 0; w2 < L::NP; ++w2) mv[w2] = movedl[buf][w2];
+                float vlane = vt.absmax(lane) * vs;
+                vlane = __builtin_isfinite(vlane) ? vlane : 0.0f;
+                if (__any(vlane > L::kVCap)) {
+                    int e;
+                    frexpf(wave_max_dpp(vlane) / L::kVCap, &e);
+                    const float f = ldexpf(1.0f, -e);
+                    vs *= f;
+#pragma unroll
+                    for (int mi = 0; mi < L::MTA; ++mi)
+#pragma unroll
+                        for (int di = 0; di < L::DTC; ++di) U[mi][di] *= f;
+                }
+                if (vs == 1.0f) vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, 1.0f);
+                else vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, vs);
+                vt.load(V, row0, stride, t0 + T, t_end, dc0, lane);   // the next subtile's V
+                // rescale the rows of groups that moved a reference
+#pragma unroll
+                for (int w2 = 0; w2 < L::NP; ++w2)
+                    if (mv[w2]) {
+#pragma unroll
+                        for (int mt = 0; mt < L::MTP; ++mt) {
+                            const int mi = w2 * L::MTP + mt;
+                            const f32x4 ga = *reinterpret_cast<const f32x4*>(gaml[buf] + 16 * mi + 4 * g);
+#pragma unroll
+                            for (int di = 0; di < L::DTC; ++di) U[mi][di] *= ga;
+                        }
+                    }
+                // ---- U' += E^T V' (fp16 x fp16)
+                const f16* et = etl[buf];
+                f16x8 va[L::DTC];
+#pragma unroll
+                for (int di = 0; di < L::DTC; ++di) va[di] = load8<f16x8>(vtl + (dc0 + 16 * di + c) * L::EP + 8 * g);
+#pragma unroll
+                for (int mi = 0; mi < L::MTA; ++mi) {
+                    const f16x8 ea = load8<f16x8>(et + (16 * mi + c) * L::EP + 8 * g);
+#pragma unroll
+                    for (int di = 0; di < L::DTC; ++di) U[mi][di] = mma(ea, va[di], U[mi][di]);
+                }
+            }
+            __syncthreads();   // hand-off
+        }
+        __syncthreads();   // the producers' fl
+        const float iv = 1.0f / vs;
+#pragma unroll
+        for (int mi = 0; mi < L::MTA; ++mi) {
+            const f32x4 fa = *reinterpret_cast<const f32x4*>(fl + 16 * mi + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int di = 0; di < L::DTC; ++di)
+                    cnum[(sbase + 16 * mi + 4 * g + r) * D + dc0 + 16 * di + c] = U[mi][di][r] * fa[r] * iv;
+        }
+    }
+}
+
 }  // namespace mfma
 
 using namespace mfma;
@@ -677,6 +910,31 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
     else FLARE_OUT_PC(256, 128, 4);
 #undef FLARE_OUT_PC
     return check_launch("chunk_output_pc");
+}
+
+}  // namespace flare
+
+namespace flare {
+using namespace mfma;
+
+int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                      int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
+                      hipStream_t stream) {
+    FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_pc: chunk must be a multiple of %d", T);
+    FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
+                  "chunk_prepare_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    const int64_t NC = (N + chunk - 1) / chunk;
+    dim3 grid((unsigned)NC, (unsigned)(B * H));
+    const float s2 = scale * kLog2e;
+#define FLARE_PREP_PC(MM, DD, NW)                                                                            \
+    hipLaunchKernelGGL((chunk_prepare_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,       \
+                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, cmax, cden, cnum)
+    if (M == 128 && D == 64) FLARE_PREP_PC(128, 64, 2);
+    else if (M == 128 && D == 128) FLARE_PREP_PC(128, 128, 4);
+    else if (M == 256 && D == 64) FLARE_PREP_PC(256, 64, 4);
+    else FLARE_PREP_PC(256, 128, 4);
+#undef FLARE_PREP_PC
+    return check_launch("chunk_prepare_pc");
 }
 
 }  // namespace flare

@@ -41,6 +41,9 @@ inline bool output_pc_enabled() {
     }();
     return on;
 }
+int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                      int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
+                      hipStream_t stream);
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, hipStream_t stream);
