@@ -667,8 +667,10 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum) {
     using L = PCLayout<M, D, NPW>;
+    // K rows of subtiles j = 0, 1, 2 mod 3: fetched by DMA two subtiles ahead
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
     __shared__ __attribute__((aligned(16))) bf16 ksl1[T * D];
+    __shared__ __attribute__((aligned(16))) bf16 ksl2[T * D];
     __shared__ __attribute__((aligned(16))) f16 etl[2][M * L::EP];              // E^T[m][tau]
     __shared__ __attribute__((aligned(16))) float gaml[2][M];                   // rescale factor (moved groups)
     __shared__ int movedl[2][L::NP];
@@ -706,19 +708,27 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
             rt[mt] = kNegInf;
             dl[mt] = 0.0f;
         }
+        constexpr int NKL = rows_to_lds_count<D, 64 * L::NP>();   // DMA loads per lane per subtile
         rows_to_lds<D, 64 * L::NP>(ksl0, K, row0, stride, t_begin, N, tid, lane);
+        if (NS > 1) rows_to_lds<D, 64 * L::NP>(ksl1, K, row0, stride, t_begin + T, N, tid, lane);
         FLARE_WAIT_VMCNT(0);
-        __syncthreads();   // B0
-        auto subtile = [&](auto parity, int j) {
-            constexpr int buf = decltype(parity)::value;
-            const bf16* kj = buf ? ksl1 : ksl0;
-            bf16* knext = buf ? ksl0 : ksl1;
+        lds_barrier();   // B0
+        // one subtile per call; j mod 3 is a compile-time constant so that each K
+        // buffer is one fixed array
+        auto subtile = [&](auto phase, int j) {
+            constexpr int k3 = decltype(phase)::value;
+            constexpr int buf = k3 & 1;     // unused when j is odd/even mixed below
+            (void)buf;
+            const bf16* kj = k3 == 0 ? ksl0 : (k3 == 1 ? ksl1 : ksl2);
+            bf16* kfar = k3 == 0 ? ksl2 : (k3 == 1 ? ksl0 : ksl1);
             int lq = lane;
             asm volatile("" : "+v"(lq));
             const int c = lq & 15, g = lq >> 4;
             if (j < NS) {
+                const int buf = j & 1;
                 const int t0 = t_begin + T * j;
-                if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
+                const bool far = j + 2 < NS;
+                if (far) rows_to_lds<D, 64 * L::NP>(kfar, K, row0, stride, t0 + 2 * T, N, 64 * w + lq, lq);
                 // ---- A = K Q^T, tokens as rows: acc[mt][ti][r] = A[t = 16 ti + 4 g + r][m = 16 mt + c]
                 f32x4 acc[L::MTP][2];
 #pragma unroll
@@ -787,13 +797,16 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                     }
                     dl[mt] += es;
                 }
-                FLARE_WAIT_VMCNT(0);     // this wave's K rows of the next subtile have landed
+                // this wave's K rows of the next subtile have landed (those of j + 2 may not)
+                if (far) FLARE_WAIT_VMCNT(NKL);
+                else FLARE_WAIT_VMCNT(0);
             }
-            __syncthreads();   // hand-off: subtile j's E^T visible, subtile j-1's consumed
+            lds_barrier();   // hand-off: subtile j's E^T visible, subtile j-1's consumed
         };
-        for (int j = 0; j <= NS; j += 2) {
+        for (int j = 0; j <= NS; j += 3) {
             subtile(std::integral_constant<int, 0>{}, j);
             if (j + 1 <= NS) subtile(std::integral_constant<int, 1>{}, j + 1);
+            if (j + 2 <= NS) subtile(std::integral_constant<int, 2>{}, j + 2);
         }
         // ---- the summary relative to the true chunk max
 #pragma unroll
@@ -808,7 +821,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                 fl[m] = f;
             }
         }
-        __syncthreads();   // fl visible
+        lds_barrier();   // fl visible
     } else {
         // =========================== consumer ===========================
         const int cw = w - L::NP;
@@ -819,9 +832,11 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 #pragma unroll
             for (int di = 0; di < L::DTC; ++di) U[mi][di] = f32x4{0.f, 0.f, 0.f, 0.f};
         float vs = 1.0f;     // V' = V vs, U' = U vs (powers of two keep |V'| <= kVCap)
-        VTile<L::DC, 64> vt;
+        // V of subtiles j (vt) and j + 1 (vn) in registers: fetched two subtiles ahead
+        VTile<L::DC, 64> vt, vn;
         vt.load(V, row0, stride, t_begin, t_end, dc0, lane);
-        __syncthreads();   // B0
+        vn.load(V, row0, stride, t_begin + T, t_end, dc0, lane);
+        lds_barrier();   // B0
         for (int it = 0; it <= NS; ++it) {
             if (it > 0) {
                 const int j = it - 1;
@@ -844,7 +859,8 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                 }
                 if (vs == 1.0f) vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, 1.0f);
                 else vt.template store_f16_scaled<L::EP>(vtl, dc0, lane, vs);
-                vt.load(V, row0, stride, t0 + T, t_end, dc0, lane);   // the next subtile's V
+                vt = vn;
+                vn.load(V, row0, stride, t0 + 2 * T, t_end, dc0, lane);   // V of subtile j + 2
                 // rescale the rows of groups that moved a reference
 #pragma unroll
                 for (int w2 = 0; w2 < L::NP; ++w2)
@@ -869,9 +885,9 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                     for (int di = 0; di < L::DTC; ++di) U[mi][di] = mma(ea, va[di], U[mi][di]);
                 }
             }
-            __syncthreads();   // hand-off
+            lds_barrier();   // hand-off
         }
-        __syncthreads();   // the producers' fl
+        lds_barrier();   // the producers' fl
         const float iv = 1.0f / vs;
 #pragma unroll
         for (int mi = 0; mi < L::MTA; ++mi) {

@@ -258,6 +258,18 @@ struct KRows {
 template <int D, int NTHR>
 constexpr int rows_to_lds_count() { return (T * (D / 8) + NTHR - 1) / NTHR; }
 
+// Workgroup barrier that orders LDS only: this wave's LDS requests complete
+// (lgkmcnt 0), then s_barrier.  Unlike __syncthreads() it does not wait for
+// global loads still in flight (prefetches, or DMA into LDS, whose completion
+// the caller waits for with vmcnt where needed); the asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);     // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // s_waitcnt vmcnt(n) with the other counters left alone (n <= 15).
 #define FLARE_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
 
