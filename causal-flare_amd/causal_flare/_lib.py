@@ -22,6 +22,7 @@ HEADER_FUNCTIONS = (
     "flare_chunk_output",
     "flare_ar_forward_workspace_size",
     "flare_ar_forward",
+    "flare_ar_forward_masked",
     "flare_ar_default_chunk",
     "flare_decode_step",
     "flare_semi_ar_workspace_size",
@@ -55,6 +56,9 @@ def _declare(lib):
     lib.flare_ar_forward_workspace_size.argtypes = [_i64] * 6
     lib.flare_ar_default_chunk.restype = _i64
     lib.flare_ar_default_chunk.argtypes = [_i64] * 5
+    lib.flare_ar_forward_masked.restype = _i
+    lib.flare_ar_forward_masked.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 6
+                                            + [_vp, _i, _vp, _vp, _sz, _vp])
     lib.flare_ar_forward.restype = _i
     lib.flare_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 6
                                      + [_vp, _i, _vp, _sz, _vp])

@@ -218,23 +218,13 @@ def flare_autoregressive_prefill_triton(
         st = _canonicalize_flare_state(state, B, H, M, D_value, K.device)
         return torch.empty((B, 0, H, D_value), device=K.device, dtype=V.dtype), st
 
+    token_mask = None
     if attention_mask is not None:
+        # The reference runs a masked prefill as the decode step token by token
+        # (inference.py:663-695): a masked token leaves the state unchanged and gets
+        # y = 0.  The chunked kernels apply the same rule to the whole sequence.
         if not bool((attention_mask != 0).all().item()):
-            # Masked prefill = the decode recurrence token by token, the
-            # reference's own semantics for this case (inference.py:663-695).
-            st = _canonicalize_flare_state(state, B, H, M, D_value, K.device)
-            st = {k: v.clone() for k, v in st.items()} if state is not None else st
-            y_steps = []
-            for t in range(T):
-                q_dec_t = None if shared else (Q_dec[:, t] if sep_q else None)
-                k_dec_t = None if shared else (K_dec if sep_k else None)
-                y_t, st = flare_autoregressive_decode_triton(
-                    Q=Q, K=K[:, t], V=V[:, t], state=st, Q_dec=q_dec_t, K_dec=k_dec_t, scale=scale,
-                    input_precision=input_precision, attention_mask=attention_mask[:, t],
-                )
-                y_steps.append(y_t)
-            return torch.cat(y_steps, dim=1), st
-        attention_mask = None
+            token_mask = (attention_mask != 0).to(device=K.device, dtype=torch.int32).contiguous()
 
     _require_gpu("flare_autoregressive_prefill", Q, K, V)
     st = None if state is None else _canonicalize_flare_state(state, B, H, M, D_value, K.device)
@@ -245,7 +235,7 @@ def flare_autoregressive_prefill_triton(
     profile_data = {"forward": {}} if profile else None
     Y, next_state = run_chunked_forward(
         Q, K, V, qd, kd, scale=float(scale), chunk=chunk, out_dtype=V.dtype, state=st,
-        want_state=True, timings=profile_data["forward"] if profile else None,
+        want_state=True, timings=profile_data["forward"] if profile else None, token_mask=token_mask,
     )
     if profile:
         _refresh_profile_totals(profile_data)

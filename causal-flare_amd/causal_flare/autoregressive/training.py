@@ -65,8 +65,11 @@ def _prep(t, dtype):
 
 
 def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
-                        want_state=False, timings=None):
-    """Launch phases 1-3; returns (Y, final_state or None).  Inputs are validated by the caller."""
+                        want_state=False, timings=None, token_mask=None):
+    """Launch phases 1-3; returns (Y, final_state or None).  Inputs are validated by the caller.
+
+    token_mask: optional int32 [B, N] (nonzero = keep); a masked token adds nothing
+    to the state and gets y = 0."""
     H, M, Dk = Q.shape
     B, N, _, Dv = V.shape
     device = K.device
@@ -90,13 +93,20 @@ def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
     P = _lib.ptr
     fin_ptrs = (P(fin["m"]), P(fin["d"]), P(fin["u"])) if fin else (None, None, None)
     NC = (N + chunk - 1) // chunk
-    if timings is None:
+    if timings is None or token_mask is not None:
         nbytes = lib.flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk)
         ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
-        rc = lib.flare_ar_forward(P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv,
-                                  float(scale), chunk, P(m0), P(d0), P(u0), *fin_ptrs, P(Y),
-                                  out_code, P(ws), nbytes, stream)
-        _lib.check(rc, "flare_ar_forward")
+        if token_mask is None:
+            rc = lib.flare_ar_forward(P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv,
+                                      float(scale), chunk, P(m0), P(d0), P(u0), *fin_ptrs, P(Y),
+                                      out_code, P(ws), nbytes, stream)
+            _lib.check(rc, "flare_ar_forward")
+        else:
+            tm = token_mask.to(device=device, dtype=torch.int32).contiguous()
+            rc = lib.flare_ar_forward_masked(P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv,
+                                             float(scale), chunk, P(m0), P(d0), P(u0), *fin_ptrs, P(Y),
+                                             out_code, P(tm), P(ws), nbytes, stream)
+            _lib.check(rc, "flare_ar_forward_masked")
         return Y, fin
     timer = _PhaseTimer(device, timings)
     cmax = torch.empty((B * H, NC, M), device=device, dtype=torch.float32)

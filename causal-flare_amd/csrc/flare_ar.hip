@@ -37,7 +37,7 @@ template <typename T>
 __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, int N, int H,
     int M, int Dk, int Dv, float scale, int chunk, float* __restrict__ cmax,
-    float* __restrict__ cden, float* __restrict__ cnum) {
+    float* __restrict__ cden, float* __restrict__ cnum, const int32_t* __restrict__ tmask) {
     extern __shared__ float smem[];
     float* k_tile = smem;                       // [TT][Dk]
     float* v_tile = k_tile + kPrepTT * Dk;      // [TT][Dv]
@@ -70,8 +70,8 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
         __syncthreads();
         for (int p = tid; p < kPrepTT * kPrepMT; p += kNT) {
             const int i = p / kPrepMT, mm = mbase + p % kPrepMT;
-            float s = kNegInf;
-            if (i < nt && mm < M) {
+            float s = kNegInf;     // also for a masked token: it adds nothing to the summary
+            if (i < nt && mm < M && (tmask == nullptr || tmask[(size_t)b * N + t0 + i] != 0)) {
                 const T* qrow = q_h + (size_t)mm * Dk;
                 const float* kr = k_tile + i * Dk;
                 float acc = 0.0f;
@@ -83,6 +83,7 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
         __syncthreads();
         for (int i = 0; i < nt; ++i) {
             const float s = s_tile[i * kPrepMT + ml];
+            if (s == kNegInf) continue;     // a masked token (no update; keeps mx = -inf safe)
             const float m_new = fmaxf(mx, s);
             const float r = __expf(mx - m_new);     // mx = -inf on the first token -> 0
             const float e = __expf(s - m_new);
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     const T* __restrict__ Qdec, const T* __restrict__ Kdec, int N, int H, int M, int Dk, int Dv,
     int DT, int TT, float scale, int chunk, bool shared, const float* __restrict__ pmax,
     const float* __restrict__ pden, const float* __restrict__ pnum, void* __restrict__ Y,
-    int out_dtype, float* __restrict__ lse_dec) {
+    int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask) {
     extern __shared__ float smem[];
     const int R = kNT / DT;
     float* k_tile = smem;                                   // [TT][Dk]
@@ -251,6 +252,13 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
         __syncthreads();
         for (int p = tid; p < nt * M; p += kNT) {
             const int i = p / M, m = p % M;
+            if (tmask != nullptr && tmask[(size_t)b * N + t0 + i] == 0) {
+                // a masked token: s = a = -inf leaves the state unchanged and gives y = 0
+                // (inference.py:395-397, 476-478)
+                s_tile[p] = kNegInf;
+                if (!shared) a_tile[p] = kNegInf;
+                continue;
+            }
             const T* qrow = q_h + (size_t)m * Dk;
             const float* kr = k_tile + i * Dk;
             float acc = 0.0f;
@@ -275,7 +283,7 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
                 float sm = 0.0f;
                 for (int m = lane; m < M; m += 64) sm += __expf(asrc[i * M + m] - mxv);
                 sm = wave_sum(sm);
-                if (lane == 0) lse[i] = mxv + __logf(sm);
+                if (lane == 0) lse[i] = mxv == kNegInf ? kNegInf : mxv + __logf(sm);   // -inf: a masked token
             }
         }
         __syncthreads();
@@ -290,7 +298,7 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
                 gam[m] = ts.sa;
                 eta[m] = ts.sb;
                 const float a = shared ? s : a_tile[i * M + m];
-                wts[m] = __expf(a - li) / (dn > 0.0f ? dn : 1.0f);
+                wts[m] = li == kNegInf ? 0.0f : __expf(a - li) / (dn > 0.0f ? dn : 1.0f);
             }
             __syncthreads();
             const float vc = v_tile[i * DT + col];
@@ -322,9 +330,13 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
 static int launch_prepare(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum,
-                          hipStream_t stream) {
-    if ((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv))
-        return launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, stream);
+                          hipStream_t stream, const int32_t* tmask = nullptr) {
+    if ((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv)) {
+        if (output_pc_enabled() && (M == 128 || M == 256))
+            return launch_prepare_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, tmask, stream);
+        if (tmask == nullptr)
+            return launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, stream);
+    }
     FLARE_REQUIRE(Dv <= 4 * kPrepCols, "chunk_prepare: Dv=%lld exceeds %d", (long long)Dv, 4 * kPrepCols);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)((M + kPrepMT - 1) / kPrepMT));
@@ -333,7 +345,7 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
 #define FLARE_PREP(TY)                                                                          \
     hipLaunchKernelGGL(chunk_prepare_kernel<TY>, grid, dim3(kNT), sm, stream,                   \
                        (const TY*)Q, (const TY*)K, (const TY*)V, (int)N, (int)H, (int)M,         \
-                       (int)Dk, (int)Dv, scale, (int)chunk, cmax, cden, cnum)
+                       (int)Dk, (int)Dv, scale, (int)chunk, cmax, cden, cnum, tmask)
     if (dtype == FLARE_BF16) FLARE_PREP(__hip_bfloat16);
     else if (dtype == FLARE_F16) FLARE_PREP(__half);
     else FLARE_PREP(float);
@@ -371,11 +383,12 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
                          int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
                          const float* pden, const float* pnum, void* Y, int out_dtype,
-                         float* lse_dec, hipStream_t stream) {
+                         float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr) {
     const bool shared = Qdec == nullptr && Kdec == nullptr;
     if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr &&
-        mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv))
-        return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, stream);
+        mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled()))
+        return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
+                                  tmask, stream);
     const int DT = pick_dt(M, Dv);
     FLARE_REQUIRE(DT > 0, "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
                   (long long)M, (long long)Dv);
@@ -396,7 +409,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
     hipLaunchKernelGGL((chunk_output_kernel<TY, RW>), grid, dim3(kNT), sm, stream, (const TY*)Q, \
                        (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd, (int)N, (int)H,  \
                        (int)M, (int)Dk, (int)Dv, DT, TT, scale, (int)chunk, shared, pmax, pden,   \
-                       pnum, Y, out_dtype, lse_dec)
+                       pnum, Y, out_dtype, lse_dec, tmask)
 #define FLARE_OUT_ROWS(TY)                   \
     if (rows <= 8) FLARE_OUT(TY, 8);         \
     else if (rows <= 16) FLARE_OUT(TY, 16);  \
@@ -504,6 +517,16 @@ int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qd
                      const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
                      void* Y, int out_dtype, void* workspace, size_t workspace_bytes,
                      void* stream) {
+    return flare_ar_forward_masked(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, m0, d0, u0,
+                                   m_fin, d_fin, u_fin, Y, out_dtype, nullptr, workspace, workspace_bytes, stream);
+}
+
+int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const void* Qdec,
+                            const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                            int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                            const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                            void* Y, int out_dtype, const int32_t* token_mask, void* workspace,
+                            size_t workspace_bytes, void* stream) {
     FLARE_REQUIRE(Q && K && V && Y, "ar_forward: null pointer");
     FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0, "ar_forward: sizes must be positive");
     if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
@@ -520,12 +543,12 @@ int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qd
     float* cden = (float*)(ws + align(per * sizeof(float)));
     float* cnum = (float*)(ws + 2 * align(per * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
-    int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s);
+    int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s, token_mask);
     if (rc) return rc;
     rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
-                         cnum, Y, out_dtype, nullptr, s);
+                         cnum, Y, out_dtype, nullptr, s, token_mask);
 }
 
 }  // extern "C"

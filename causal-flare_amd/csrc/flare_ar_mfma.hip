@@ -763,7 +763,7 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
                         int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
                         float* cnum, hipStream_t stream) {
     if (output_pc_enabled() && (M == 128 || M == 256))
-        return launch_prepare_pc(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, stream);
+        return launch_prepare_pc(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, nullptr, stream);
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_mfma: chunk must be a multiple of %d", T);
     FLARE_REQUIRE(M % 32 == 0 && M >= 32 && M <= kMaxPrepM && (D == 64 || D == 128),
                   "chunk_prepare_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
@@ -793,9 +793,11 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
-                       const float* pden, const float* pnum, void* Y, int out_dtype, hipStream_t stream) {
+                       const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
+                       hipStream_t stream) {
     if (output_pc_enabled())
-        return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, stream);
+        return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, stream);
+    FLARE_REQUIRE(tmask == nullptr, "chunk_output_mfma: token masks need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));

@@ -68,7 +68,7 @@ template <int M, int D, int NPW>
 __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
-    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype) {
+    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, const int32_t* __restrict__ tmask) {
     using L = PCLayout<M, D, NPW>;
     // K rows of the even / odd subtiles (swizzled); two arrays rather than one so
     // that reads of one never wait on the DMA that fills the other
@@ -175,6 +175,16 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
             const int c = lq & 15, g = lq >> 4;
             if (j < NS) {
                 const int t0 = t_begin + T * j;
+                // token mask of this lane's tokens (loaded before the DMA, so waiting for it
+                // leaves the DMA in flight); a masked token has S = -inf everywhere
+                bool keep[2] = {true, true};
+                if (tmask != nullptr) {
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        const int t = t0 + 16 * ti + c;
+                        keep[ti] = t >= t_end || tmask[(size_t)b * N + t] != 0;
+                    }
+                }
                 if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
                 // ---- raw scores A = Q K^T for this wave's latents (S = scale2 A):
                 //      acc[mi][ti][r] = A[t = 16 ti + c][m = 16 mi + 4 g + r], -inf for invalid tokens
@@ -195,10 +205,10 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 #pragma unroll
                         for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa[mi][kq], kb[ti], acc[mi][ti]);
                 }
-                if (ragged) {
+                if (ragged || tmask != nullptr) {
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti)
-                        if (t0 + 16 * ti + c >= t_end)
+                        if (t0 + 16 * ti + c >= t_end || !keep[ti])
 #pragma unroll
                             for (int mi = 0; mi < L::MTP; ++mi) acc[mi][ti] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
                 }
@@ -209,7 +219,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 #pragma unroll
                     for (int kq = 0; kq < L::KS; ++kq)
                         a = mma(qa[mi][kq], load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g)), a);
-                    if (ragged && t0 + row >= t_end) a = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+                    if ((ragged && t0 + row >= t_end) || !keep[ti]) a = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
                     return a;
                 };
                 // ---- E = 2^(S - R) against the current references; a reference moves
@@ -223,6 +233,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                         e[mi][0][r] = exp2f_fast(fmaf(acc[mi][0][r], scale2, -R[mi][r]));
                         e[mi][1][r] = exp2f_fast(fmaf(acc[mi][1][r], scale2, -R[mi][r]));
                         emax = fmaxf(emax, fmaxf(e[mi][0][r], e[mi][1][r]));
+                        dnbig |= R[mi][r] == kNegInf;   // no reference yet (fully masked so far): general path
                     }
                 // token max over this wave's latents (log2 units; -inf for invalid tokens)
                 float lm[2];
@@ -402,7 +413,8 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 #pragma unroll
                             for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) em[ti][r] = exp2f_fast(fmaf(sc[ti][r], scale2, -R[mi][r]));
+                                for (int r = 0; r < 4; ++r)
+                                    em[ti][r] = R[mi][r] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[ti][r], scale2, -R[mi][r]));
                             // E^T (fp16) to LDS; the cumulative den in fp32 (DPP scans over the token
                             // lanes): here E may lie far below the fp16 range
                             f32x4 dcum[2];
@@ -665,7 +677,8 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 template <int M, int D, int NPW>
 __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
-    float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum) {
+    float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum,
+    const int32_t* __restrict__ tmask) {
     using L = PCLayout<M, D, NPW>;
     // K rows of subtiles j = 0, 1, 2 mod 3: fetched by DMA two subtiles ahead
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
@@ -728,6 +741,17 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                 const int buf = j & 1;
                 const int t0 = t_begin + T * j;
                 const bool far = j + 2 < NS;
+                // token mask of this lane's tokens t = 16 ti + 4 g + r (loaded before the DMA)
+                bool keep[2][4] = {{true, true, true, true}, {true, true, true, true}};
+                if (tmask != nullptr) {
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int t = t0 + 16 * ti + 4 * g + r;
+                            keep[ti][r] = t >= t_end || tmask[(size_t)b * N + t] != 0;
+                        }
+                }
                 if (far) rows_to_lds<D, 64 * L::NP>(kfar, K, row0, stride, t0 + 2 * T, N, 64 * w + lq, lq);
                 // ---- A = K Q^T, tokens as rows: acc[mt][ti][r] = A[t = 16 ti + 4 g + r][m = 16 mt + c]
                 f32x4 acc[L::MTP][2];
@@ -746,12 +770,12 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 #pragma unroll
                         for (int ti = 0; ti < 2; ++ti) acc[mt][ti] = mma(ka[ti], qb[mt][kq], acc[mt][ti]);
                 }
-                if (t0 + T > t_end) {      // the ragged last subtile
+                if (t0 + T > t_end || tmask != nullptr) {      // the ragged last subtile, masked tokens
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (t0 + 16 * ti + 4 * g + r >= t_end)
+                            if (t0 + 16 * ti + 4 * g + r >= t_end || !keep[ti][r])
 #pragma unroll
                                 for (int mt = 0; mt < L::MTP; ++mt) acc[mt][ti][r] = kNegInf;
                 }
@@ -779,17 +803,19 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                     }
                 }
                 if (lane == 0) movedl[buf][w] = moved ? 1 : 0;
-                // ---- E = 2^(S - R): den partial, and E^T (fp16) to LDS, four tokens per store
+                // ---- E = 2^(S - R): den partial, and E^T (fp16) to LDS, four tokens per store.
+                //      A latent with no reference yet (every token so far masked) has E = 0.
                 f16* et = etl[buf];
 #pragma unroll
                 for (int mt = 0; mt < L::MTP; ++mt) {
+                    const float nR = R[mt] == kNegInf ? kNegInf : -R[mt];
                     float es = 0.0f;
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
                         f32x4 e;
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            e[r] = exp2f_fast(fmaf(acc[mt][ti][r], scale2, -R[mt]));
+                            e[r] = exp2f_fast(fmaf(acc[mt][ti][r], scale2, nR));
                             es += e[r];
                         }
                         *reinterpret_cast<f16x4*>(et + (mp0 + 16 * mt + c) * L::EP + 16 * ti + 4 * g) =
@@ -907,7 +933,7 @@ using namespace mfma;
 
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
-                     const float* pnum, void* Y, int out_dtype, hipStream_t stream) {
+                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
@@ -917,7 +943,7 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
 #define FLARE_OUT_PC(MM, DD, NW)                                                                         \
     hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
                        (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y, \
-                       out_dtype)
+                       out_dtype, tmask)
     // The 128 x 64 bank runs 2 + 2 waves (72 KiB of LDS: two workgroups share a CU);
     // the larger banks 4 + 4 (one workgroup fills a CU).
     if (M == 128 && D == 64) FLARE_OUT_PC(128, 64, 2);
@@ -935,7 +961,7 @@ using namespace mfma;
 
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      hipStream_t stream) {
+                      const int32_t* tmask, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_prepare_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
@@ -944,7 +970,7 @@ int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, in
     const float s2 = scale * kLog2e;
 #define FLARE_PREP_PC(MM, DD, NW)                                                                            \
     hipLaunchKernelGGL((chunk_prepare_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,       \
-                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, cmax, cden, cnum)
+                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, cmax, cden, cnum, tmask)
     if (M == 128 && D == 64) FLARE_PREP_PC(128, 64, 2);
     else if (M == 128 && D == 128) FLARE_PREP_PC(128, 128, 4);
     else if (M == 256 && D == 64) FLARE_PREP_PC(256, 64, 4);

@@ -17,7 +17,8 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
                         float* cnum, hipStream_t stream);
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
-                       const float* pden, const float* pnum, void* Y, int out_dtype, hipStream_t stream);
+                       const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
+                       hipStream_t stream);
 
 // FLARE_DISABLE_MFMA=1 routes every shape to the scalar-fp32 kernels (A/B checks);
 // FLARE_MFMA_PHASES=<bits> keeps the MFMA kernel only for phase 1 (bit 0) and/or
@@ -43,10 +44,10 @@ inline bool output_pc_enabled() {
 }
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      hipStream_t stream);
+                      const int32_t* tmask, hipStream_t stream);
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
-                     const float* pnum, void* Y, int out_dtype, hipStream_t stream);
+                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, hipStream_t stream);
 }  // namespace flare
 
 namespace flare {

@@ -100,6 +100,20 @@ int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qd
                      void* Y, int out_dtype, void* workspace, size_t workspace_bytes,
                      void* stream);
 
+/*
+ * flare_ar_forward with a per-token mask: token_mask [B, N] (int32, nonzero =
+ * keep) may be NULL.  A masked token adds nothing to the latent state and gets
+ * y = 0, the semantics of the reference's masked prefill, which runs the decode
+ * step token by token with attention_mask[:, t] (inference.py:663-695, masked
+ * decode rows at :395-397 and :476-478); here the chunked kernels apply it.
+ */
+int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const void* Qdec,
+                            const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                            int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                            const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                            void* Y, int out_dtype, const int32_t* token_mask, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* The chunk length flare_ar_forward uses when called with chunk <= 0. */
 int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 

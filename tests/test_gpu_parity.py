@@ -197,6 +197,50 @@ def test_prefill_with_initial_state_and_mask():
     assert_parity(stm["u"], stm_ref["u"], torch.float32, "masked state u")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_masked_prefill_mfma_bf16(M, D, with_state):
+    """Masked prefill on the bf16 MFMA kernels: the first 40 tokens masked (so a
+    chunk starts with no reference), scattered tokens, a whole chunk and a chunk
+    boundary; against the reference's token-by-token decode semantics
+    (inference.py:663-695) restated in the oracle."""
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("masked_prefill_mfma", M, D, with_state)
+    B, T, H = 2, 1100, 2
+    q, k, v = seeded(97 + M, B, 2 * T, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    st = st_o = None
+    if with_state:
+        _, st = flare_autoregressive_prefill_triton(q.to(DEV), k[:, :T].to(DEV), v[:, :T].to(DEV))
+        _, st_o = O.ar_recurrent(q, k[:, :T], v[:, :T], nthreads=16)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[:, :40] = 0
+    mask[0, 100:103] = 0
+    mask[1, 256:512] = 0
+    mask[1, 700:760] = 0
+    mask[0, T - 1] = 0
+    y, st2 = flare_autoregressive_prefill_triton(q.to(DEV), k[:, T:].to(DEV), v[:, T:].to(DEV), state=st,
+                                                 attention_mask=mask.to(DEV))
+    y_ref, st_ref = O.ar_recurrent(q, k[:, T:], v[:, T:], state=st_o, attention_mask=mask, nthreads=16)
+    assert torch.all(y[mask == 0].float() == 0), "masked tokens must give y = 0"
+    assert_parity(y, y_ref, torch.bfloat16, f"masked prefill M={M} D={D} state={with_state}")
+    assert_state_parity(st2, st_ref, torch.bfloat16, "masked prefill")
+
+
+def test_masked_prefill_leading_tokens_fp32():
+    """fp32 (scalar kernels): the first tokens of the sequence masked, no initial state."""
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("masked_prefill_fp32")
+    B, T, H, M, D = 2, 300, 2, 64, 32
+    q, k, v = seeded(5, B, T, H, M, D, D, torch.float32)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[:, :70] = 0
+    mask[1, 150:160] = 0
+    y, st = flare_autoregressive_prefill_triton(q.to(DEV), k.to(DEV), v.to(DEV), attention_mask=mask.to(DEV))
+    y_ref, st_ref = O.ar_recurrent(q, k, v, attention_mask=mask, nthreads=16)
+    assert_parity(y, y_ref, torch.float32, "masked prefill fp32")
+    assert_state_parity(st, st_ref, torch.float32, "masked prefill fp32")
+
+
 def test_cfg4_decode_bf16():
     """BASELINE config 4 (reduced steps): B=64, H=16, M=128, D=64, 2048-token prefill then decode."""
     from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
