@@ -24,6 +24,8 @@ HEADER_FUNCTIONS = (
     "flare_ar_forward",
     "flare_ar_forward_masked",
     "flare_ar_default_chunk",
+    "flare_ar_backward_workspace_size",
+    "flare_ar_backward",
     "flare_decode_step",
     "flare_semi_ar_workspace_size",
     "flare_semi_ar_forward",
@@ -62,6 +64,10 @@ def _declare(lib):
     lib.flare_ar_forward.restype = _i
     lib.flare_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 6
                                      + [_vp, _i, _vp, _sz, _vp])
+    lib.flare_ar_backward_workspace_size.restype = _sz
+    lib.flare_ar_backward_workspace_size.argtypes = [_i64] * 6
+    lib.flare_ar_backward.restype = _i
+    lib.flare_ar_backward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f] + [_vp] * 7 + [_vp, _sz, _vp])
     lib.flare_decode_step.restype = _i
     lib.flare_decode_step.argtypes = [_vp] * 6 + [_i] + [_i64] * 5 + [_f] + [_vp] * 3 + [_vp, _i, _vp]
     lib.flare_semi_ar_workspace_size.restype = _sz

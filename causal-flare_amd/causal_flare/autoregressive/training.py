@@ -10,8 +10,9 @@ HIP kernels from ``libflare_mi355x.so``:
 (reference kernels flare_chunk_prepare :914, flare_chunk_prefix :1021,
 flare_chunk_decoder_lse :1106 + flare_chunk_fwd :1189).
 
-The backward pass is not part of this build; calling ``.backward()`` through
-the output raises ``NotImplementedError``.
+The backward pass (reference ``_chunked_flare_lse_backward_impl``,
+training.py:4369-4918) runs as HIP kernels through ``flare_ar_backward``; it
+recomputes the chunk statistics from the saved inputs and output.
 """
 from __future__ import annotations
 
@@ -124,6 +125,39 @@ def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
     return Y, fin
 
 
+def run_chunked_backward(Q, K, V, qd, kd, Y, dY, *, scale):
+    """Launch flare_ar_backward; returns (dQ, dK, dV, dQ_dec, dK_dec) in the
+    inputs' dtypes (None for a decoder tensor that was not separate)."""
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    if dY is None:
+        return None, None, None, None, None
+    if N == 0:
+        return tuple(None if t is None else torch.zeros_like(t) for t in (Q, K, V, qd, kd))
+    if M > 256 or Dk > 256 or Dv > 512:
+        raise NotImplementedError(
+            f"The MI355X FLARE backward supports M <= 256, D_score <= 256 and D_value <= 512; "
+            f"got M={M}, D_score={Dk}, D_value={Dv}."
+        )
+    device = K.device
+    cdt = _compute_dtype(Q, K, V, qd, kd)
+    code = _lib.dtype_code(cdt)
+    q, k, v, qdc, kdc, y, dy = (_prep(t, cdt) for t in (Q, K, V, qd, kd, Y, dY))
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqd = torch.empty_like(qdc) if qdc is not None else None
+    dkd = torch.empty_like(kdc) if kdc is not None else None
+    lib = _lib.lib()
+    nbytes = lib.flare_ar_backward_workspace_size(B, N, H, M, Dk, Dv)
+    ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+    P = _lib.ptr
+    rc = lib.flare_ar_backward(P(q), P(k), P(v), P(qdc), P(kdc), code, B, N, H, M, Dk, Dv, float(scale),
+                               P(y), P(dy), P(dq), P(dk), P(dv), P(dqd), P(dkd), P(ws), nbytes,
+                               _lib.stream_of(device))
+    _lib.check(rc, "flare_ar_backward")
+    cast = lambda g, ref: None if g is None else g.to(ref.dtype)
+    return cast(dq, Q), cast(dk, K), cast(dv, V), cast(dqd, qd), cast(dkd, kd)
+
+
 class AutoRegressiveFLARE(autograd.Function):
     """Forward of causal FLARE (reference ``training.py:731-905``)."""
 
@@ -153,6 +187,7 @@ class AutoRegressiveFLARE(autograd.Function):
         # Output in the compute dtype of K (training.py:322-324, 724-727).
         out_dtype = K.dtype if K.dtype in (torch.bfloat16, torch.float16) else torch.float32
         profile_data = {"forward": {}, "backward": {}} if profile else None
+        qd = kd = None
         if N == 0:
             Y = torch.empty((B, 0, H, D_value), device=K.device, dtype=out_dtype)
         else:
@@ -162,16 +197,21 @@ class AutoRegressiveFLARE(autograd.Function):
                 Q, K, V, qd, kd, scale=scale, chunk=chunk, out_dtype=out_dtype,
                 timings=profile_data["forward"] if profile else None,
             )
+        ctx.scale = scale
+        ctx.sep = (qd is not None, kd is not None)
+        ctx.save_for_backward(Q, K, V, qd, kd, Y)
         if profile:
             _refresh_profile_totals(profile_data)
             return Y, profile_data
         return Y
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "The MI355X causal FLARE build implements the forward pass only; backward is not available."
-        )
+    def backward(ctx, dY, *_unused):
+        """Gradients of Q, K, V (and Q_dec, K_dec when separate): reference
+        _chunked_flare_lse_backward_impl (training.py:4369-4918)."""
+        Q, K, V, qd, kd, Y = ctx.saved_tensors
+        grads = run_chunked_backward(Q, K, V, qd, kd, Y, dY, scale=ctx.scale)
+        return (*grads[:3], None, None, None, None, *grads[3:])
 
 
 def flare_autoregressive_triton(

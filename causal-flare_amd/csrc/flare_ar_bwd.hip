@@ -1,0 +1,805 @@
+// flare_ar_bwd.hip -- backward of the chunked causal FLARE forward (scalar-fp32 kernels).
+//
+// Replaces the reference's _chunked_flare_lse_backward_impl
+// (causal_flare/autoregressive/training.py:4369-4918): given dY, the forward's
+// inputs and its output Y, produce dQ, dK, dV and, for separate decoder
+// weights, dQ_dec and dK_dec.
+//
+// Per (b, h) and latent m, with encoder scores s_tm = scale k_t.q_m, decoder
+// scores a_tm = scale qd_t.kd_m, alpha_t = softmax_m(a_t), running den
+// D_tm = sum_{tau<=t} e^{s_tau m} = e^{L_tm}, z_tm = U_tm / D_tm and
+// y_t = sum_m alpha_tm z_tm, the gradients with g_t = dY_t are
+//     gz_tm  = g_t . z_tm                     gy_t = g_t . y_t
+//     da_tm  = alpha_tm (gz_tm - gy_t)
+//     ds_tm  = sum_{t >= tau} e^{s_tau m - L_tm} alpha_tm (g_t . v_tau - gz_tm)
+//     dv_tau = sum_{t >= tau} sum_m e^{s_tau m - L_tm} alpha_tm g_t
+// and dQ, dK, dQ_dec, dK_dec are contractions of ds and da with K, Q, Qd, Kd.
+// Every factor e^{s_tau - L_t} (t >= tau) is <= 1: D_t contains e^{s_tau}.
+//
+// The sequence is cut into chunks of kBT tokens.  Inside a chunk the pairs
+// (tau, t) are summed exactly; later chunks enter through a reverse scan:
+//     X_c,m = sum_{t > end_c} e^{Lend_c - L_tm} alpha_tm g_t      (Dv vector)
+//     Y_c,m = sum_{t > end_c} e^{Lend_c - L_tm} alpha_tm gz_tm
+// with Lend_c = L at the last token of chunk c, so that for tau in chunk c the
+// later-chunk terms are e^{s_tau - Lend_c} (v_tau . X_c - Y_c) in ds and
+// sum_m e^{s_tau - Lend_c} X_c in dv; both factors stay <= 1.  The chunk's
+// starting state (max, den, num) comes from the forward's own prepare and
+// prefix kernels run at chunk kBT.
+//
+// Kernels, in launch order:
+//   bwd_stats    s, L, alpha per (t, m)                   grid (NC, BH)
+//   bwd_gz       c = alpha gz per (t, m)                  grid (NC, BH)
+//   bwd_gy       gy = dY . Y per token                    grid (tokens)
+//   bwd_summary  per-chunk terms of X, Y                  grid (NC, BH, Dv/64)
+//   bwd_carry    reverse scan over chunks -> X_c, Y_c     grid (BH M Dv/4)
+//   bwd_dv       dV                                        grid (NC, BH, Dv/64)
+//   bwd_ds       ds (written over s)                      grid (NC, BH)
+//   bwd_dk       dK, dQ_dec per token                     grid (N/16, BH)
+//   bwd_dq       dQ, dK_dec partial sums per token group  grid (NG, BH, Dk/64)
+//   bwd_reduce   sum of the partials over (b, group)
+#include <stdio.h>
+
+#include "flare_common.h"
+#include "flare_internal.h"
+
+namespace flare {
+
+constexpr int kBT = 64;        // tokens per backward chunk
+constexpr int kBNT = 256;      // threads per workgroup; thread m owns latent m (M <= 256)
+constexpr int kBSlab = 64;     // value / key columns per LDS slab
+constexpr int kBP = 65;        // padded pitch of [64][64] LDS tiles
+constexpr int kBTok = 16;      // tokens per tile in the token-row kernels
+constexpr int kBGroup = 512;   // tokens per partial sum of dQ / dK_dec
+
+__device__ __forceinline__ size_t tok_index(int b, int t, int h, int N, int H, int D) {
+    return (((size_t)b * N + t) * H + h) * D;
+}
+
+// ---------------------------------------------------------------------------
+// bwd_stats: per chunk, scores s (encoder), L = log of the running den from
+// the chunk's starting state, and the decoder weights alpha.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ Qd, const T* __restrict__ Kd,
+    int N, int H, int M, int Dk, float scale, bool shared, const float* __restrict__ pmax,
+    const float* __restrict__ pden, float* __restrict__ S, float* __restrict__ L, float* __restrict__ AL) {
+    __shared__ float kt[kBTok * 256];
+    __shared__ float qdt[kBTok * 256];
+    __shared__ float at[kBTok * 256];
+    __shared__ float lse[kBTok];
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
+    const bool act = m < M;
+    const int t0 = c * kBT, nt = min(kBT, N - t0);
+    float mx = kNegInf, dn = 0.0f;
+    if (act) {
+        mx = pmax[((size_t)bh * NC + c) * M + m];
+        dn = pden[((size_t)bh * NC + c) * M + m];
+    }
+    const T* qrow = Q + ((size_t)h * M + (act ? m : 0)) * Dk;
+    const T* kdrow = Kd + ((size_t)h * M + (act ? m : 0)) * Dk;
+    for (int i0 = 0; i0 < nt; i0 += kBTok) {
+        const int ni = min(kBTok, nt - i0);
+        __syncthreads();
+        for (int e = tid; e < kBTok * Dk; e += kBNT) {
+            const int i = e / Dk, d = e % Dk;
+            const size_t gi = tok_index(b, t0 + i0 + i, h, N, H, Dk) + d;
+            kt[e] = i < ni ? to_f32(K[gi]) : 0.0f;
+            if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
+        }
+        __syncthreads();
+        if (act) {
+            float as[kBTok], aa[kBTok];
+#pragma unroll
+            for (int i = 0; i < kBTok; ++i) as[i] = aa[i] = 0.0f;
+            for (int d = 0; d < Dk; d += 4) {
+                const float q0 = to_f32(qrow[d]), q1 = to_f32(qrow[d + 1]), q2 = to_f32(qrow[d + 2]),
+                            q3 = to_f32(qrow[d + 3]);
+#pragma unroll
+                for (int i = 0; i < kBTok; ++i) {
+                    const float* kr = kt + i * Dk + d;
+                    as[i] += kr[0] * q0 + kr[1] * q1 + kr[2] * q2 + kr[3] * q3;
+                }
+                if (!shared) {
+                    const float k0 = to_f32(kdrow[d]), k1 = to_f32(kdrow[d + 1]), k2 = to_f32(kdrow[d + 2]),
+                                k3 = to_f32(kdrow[d + 3]);
+#pragma unroll
+                    for (int i = 0; i < kBTok; ++i) {
+                        const float* qr = qdt + i * Dk + d;
+                        aa[i] += qr[0] * k0 + qr[1] * k1 + qr[2] * k2 + qr[3] * k3;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < kBTok; ++i) {
+                if (i < ni) {
+                    const float s = as[i] * scale;
+                    const MergeScales ts = token_scales(mx, s);
+                    dn = dn * ts.sa + ts.sb;
+                    mx = ts.m_new;
+                    const size_t o = ((size_t)bh * N + t0 + i0 + i) * M + m;
+                    S[o] = s;
+                    L[o] = mx + __logf(dn);
+                    at[i * M + m] = shared ? s : aa[i] * scale;
+                }
+            }
+        }
+        __syncthreads();
+        {   // decoder log-sum-exp per token: wavefront w handles tokens w, w+4, ...
+            const int w = tid >> 6, lane = tid & 63;
+            for (int i = w; i < ni; i += kBNT / 64) {
+                float v = kNegInf;
+                for (int mm = lane; mm < M; mm += 64) v = fmaxf(v, at[i * M + mm]);
+                v = wave_max(v);
+                float sm = 0.0f;
+                for (int mm = lane; mm < M; mm += 64) sm += __expf(at[i * M + mm] - v);
+                sm = wave_sum(sm);
+                if (lane == 0) lse[i] = v + __logf(sm);
+            }
+        }
+        __syncthreads();
+        if (act) {
+            for (int i = 0; i < ni; ++i)
+                AL[((size_t)bh * N + t0 + i0 + i) * M + m] = __expf(at[i * M + m] - lse[i]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Shared by bwd_gz and bwd_ds: GV[t][tau] = g_t . v_tau over one chunk, from
+// column slabs staged in LDS.  Thread (t = tid / 4, tau = 16 (tid % 4) + j).
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void stage_slab(float* dst, const T* __restrict__ src, int b, int t0, int nt, int h,
+                                           int N, int H, int D, int d0, int ds) {
+    for (int e = threadIdx.x; e < kBT * kBSlab; e += kBNT) {
+        const int i = e / kBSlab, d = e % kBSlab;
+        dst[i * kBP + d] = (i < nt && d < ds) ? to_f32(src[tok_index(b, t0 + i, h, N, H, D) + d0 + d]) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ void gv_accumulate(float (&gv)[16], const float* gs, const float* vs, int ds) {
+    const int t = threadIdx.x >> 2, tq = (threadIdx.x & 3) * 16;
+    for (int d = 0; d < ds; ++d) {
+        const float gval = gs[t * kBP + d];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) gv[j] += gval * vs[(tq + j) * kBP + d];
+    }
+}
+
+__device__ __forceinline__ void gv_store(const float (&gv)[16], float* gvl) {
+    const int t = threadIdx.x >> 2, tq = (threadIdx.x & 3) * 16;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) gvl[t * kBP + tq + j] = gv[j];
+}
+
+// ---------------------------------------------------------------------------
+// bwd_gz: c_tm = alpha_tm gz_tm with
+//   gz_tm = e^{pm_m - L_tm} (g_t . pu_m) + sum_{tau <= t} e^{s_tau m - L_tm} (g_t . v_tau)
+// (pm, pu: the chunk's starting max and numerator, pu relative to pm).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
+    const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv,
+    const float* __restrict__ pmax, const float* __restrict__ pnum, const float* __restrict__ S,
+    const float* __restrict__ L, const float* __restrict__ AL, float* __restrict__ C) {
+    __shared__ float st[kBT * 256];
+    __shared__ float gvl[kBT * kBP];
+    __shared__ float gs[kBT * kBP];
+    __shared__ float vs[kBT * kBP];
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
+    const bool act = m < M;
+    const int t0 = c * kBT, nt = min(kBT, N - t0);
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    for (int e = tid; e < nt * M; e += kBNT) st[e] = S[rbase + e];
+    float gv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
+    float acc[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
+    const float* pu = pnum + (((size_t)bh * NC + c) * M + (act ? m : 0)) * Dv;
+    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+        const int ds = min(kBSlab, Dv - d0);
+        __syncthreads();
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds);
+        __syncthreads();
+        gv_accumulate(gv, gs, vs, ds);
+        if (act) {
+            for (int d = 0; d < ds; d += 4) {
+                const float4 p = *reinterpret_cast<const float4*>(pu + d0 + d);
+#pragma unroll
+                for (int t = 0; t < kBT; ++t) {
+                    const float* gr = gs + t * kBP + d;
+                    acc[t] += gr[0] * p.x + gr[1] * p.y + gr[2] * p.z + gr[3] * p.w;
+                }
+            }
+        }
+    }
+    gv_store(gv, gvl);
+    __syncthreads();
+    if (!act) return;
+    const float pm = pmax[((size_t)bh * NC + c) * M + m];
+    float lt[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) {
+        lt[t] = t < nt ? L[rbase + (size_t)t * M + m] : 0.0f;
+        acc[t] = pm == kNegInf ? 0.0f : __expf(pm - lt[t]) * acc[t];
+    }
+    for (int tau = 0; tau < nt; ++tau) {
+        const float s = st[tau * M + m];
+#pragma unroll
+        for (int t = 0; t < kBT; ++t)
+            if (t >= tau && t < nt) acc[t] += gvl[t * kBP + tau] * __expf(s - lt[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < kBT; ++t)
+        if (t < nt) C[rbase + (size_t)t * M + m] = AL[rbase + (size_t)t * M + m] * acc[t];
+}
+
+// ---------------------------------------------------------------------------
+// bwd_gy: gy_t = dY_t . Y_t per (b, t, h); one wavefront per token row.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_gy_kernel(const T* __restrict__ dY, const T* __restrict__ Y, int N,
+                                                     int H, int Dv, int64_t rows, float* __restrict__ gy) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const T* a = dY + row * Dv;
+    const T* y = Y + row * Dv;
+    float sum = 0.0f;
+    for (int d = lane; d < Dv; d += 64) sum += to_f32(a[d]) * to_f32(y[d]);
+    sum = wave_sum(sum);
+    if (lane == 0) {
+        const int h = (int)(row % H);
+        const int64_t bt = row / H;
+        const int b = (int)(bt / N), t = (int)(bt % N);
+        gy[((int64_t)b * H + h) * N + t] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_summary: chunk c's own terms of the reverse scan, relative to
+// Lpre = L at the last token of chunk c-1 (chunk 0 has none):
+//   a_c,m = sum_{t in c} w_tm g_t,  b_c,m = sum_{t in c} w_tm gz_tm,
+//   w_tm = e^{Lpre_m - L_tm} alpha_tm  (c_tm = alpha_tm gz_tm is stored).
+// a overwrites the chunk's starting numerator, b its starting den.
+// Thread (col = tid % 64, rg = tid / 64) owns a[m = rg + 4 r][d0 + col].
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_summary_kernel(
+    const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ L,
+    const float* __restrict__ AL, const float* __restrict__ C, float* __restrict__ a_out,
+    float* __restrict__ b_out) {
+    __shared__ float wl[kBT * 256];
+    __shared__ float gs[kBT * kBP];
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    if (c == 0) return;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int t0 = c * kBT, nt = min(kBT, N - t0), d0 = blockIdx.z * kBSlab, ds = min(kBSlab, Dv - d0);
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    const float* lpre = L + rbase - M;
+    for (int e = tid; e < nt * M; e += kBNT) wl[e] = __expf(lpre[e % M] - L[rbase + e]) * AL[rbase + e];
+    stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
+    __syncthreads();
+    const size_t sbase = ((size_t)bh * NC + c) * M;
+    if (blockIdx.z == 0 && tid < M) {
+        float sum = 0.0f;
+        for (int t = 0; t < nt; ++t) {
+            const size_t o = rbase + (size_t)t * M + tid;
+            sum += __expf(lpre[tid] - L[o]) * C[o];
+        }
+        b_out[sbase + tid] = sum;
+    }
+    const int col = tid & 63, rg = tid >> 6, rows = M >> 2;
+    float acc[64];
+#pragma unroll
+    for (int r = 0; r < 64; ++r) acc[r] = 0.0f;
+    for (int t = 0; t < nt; ++t) {
+        const float gval = gs[t * kBP + col];
+        const float* wr = wl + t * M + rg;
+#pragma unroll
+        for (int r = 0; r < 64; ++r)
+            if (r < rows) acc[r] += wr[4 * r] * gval;
+    }
+    if (col < ds) {
+#pragma unroll
+        for (int r = 0; r < 64; ++r)
+            if (r < rows) a_out[(sbase + rg + 4 * r) * Dv + d0 + col] = acc[r];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_carry: reverse scan over chunks, in place.  Slot c of (a, b) receives
+// (X_c, Y_c); X_{NC-1} = 0 and X_{c-1} = a_c + e^{Lend_{c-1} - Lend_c} X_c.
+// Thread per (bh, m, four value columns); chunks are read kScanB at a time.
+// ---------------------------------------------------------------------------
+constexpr int kScanB = 8;
+
+__global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, float* __restrict__ bsum,
+                                                        const float* __restrict__ L, int N, int NC, int M,
+                                                        int Dv, int64_t rows) {
+    const int D4 = Dv >> 2;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * D4) return;
+    const int64_t row = gid / D4;
+    const int j = (int)(gid % D4);
+    const int64_t bh = row / M;
+    const int m = (int)(row % M);
+    float4* a4 = reinterpret_cast<float4*>(a);
+    auto lend = [&](int c) { return L[((size_t)bh * N + min(N, (c + 1) * kBT) - 1) * M + m]; };
+    float4 X = make_float4(0.f, 0.f, 0.f, 0.f);
+    float Y = 0.0f;
+    float lnext = lend(NC - 1);
+    for (int c1 = NC - 1; c1 >= 0; c1 -= kScanB) {
+        float4 av[kScanB];
+        float bv[kScanB], lv[kScanB];
+#pragma unroll
+        for (int i = 0; i < kScanB; ++i) {
+            const int c = c1 - i;
+            const size_t si = (size_t)bh * NC * M + (size_t)max(c, 0) * M + m;
+            av[i] = c > 0 ? a4[si * D4 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            bv[i] = c > 0 ? bsum[si] : 0.0f;
+            lv[i] = c > 0 ? lend(c - 1) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kScanB; ++i) {
+            const int c = c1 - i;
+            if (c < 0) break;
+            const size_t si = (size_t)bh * NC * M + (size_t)c * M + m;
+            a4[si * D4 + j] = X;
+            if (j == 0) bsum[si] = Y;
+            if (c > 0) {
+                const float f = __expf(lv[i] - lnext);
+                X.x = av[i].x + f * X.x;
+                X.y = av[i].y + f * X.y;
+                X.z = av[i].z + f * X.z;
+                X.w = av[i].w + f * X.w;
+                Y = bv[i] + f * Y;
+                lnext = lv[i];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_dv: dv_tau = sum_{t >= tau} G[tau][t] g_t + sum_m e^{s_tau m - Lend_m} X_m,
+// G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm.  G is built over latent slabs
+// of 64 by thread (tau = tid / 4, t = 16 (tid % 4) + j); the output by thread
+// (col, rg) owning dv[tau = rg + 4 r][d0 + col].
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
+    const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ S,
+    const float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ X, T* __restrict__ dV) {
+    __shared__ float ql[kBT * 256];       // slabs of s, L, alpha while G is built; then e^{s - Lend}
+    __shared__ float gl[kBT * kBP];       // G[tau][t]
+    __shared__ float gs[kBT * kBP];       // dY slab
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int t0 = c * kBT, nt = min(kBT, N - t0), d0 = blockIdx.z * kBSlab, ds = min(kBSlab, Dv - d0);
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    float* ss = ql;
+    float* ls = ql + kBT * kBP;
+    float* as = ql + 2 * kBT * kBP;
+    const int tau = tid >> 2, tq = (tid & 3) * 16;
+    float g[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) g[j] = 0.0f;
+    for (int m0 = 0; m0 < M; m0 += 64) {
+        const int mc = min(64, M - m0);
+        __syncthreads();
+        for (int e = tid; e < kBT * 64; e += kBNT) {
+            const int i = e >> 6, mm = e & 63;
+            const bool ok = i < nt && mm < mc;
+            const size_t o = rbase + (size_t)i * M + m0 + mm;
+            ss[i * kBP + mm] = ok ? S[o] : kNegInf;
+            ls[i * kBP + mm] = ok ? L[o] : 0.0f;
+            as[i * kBP + mm] = ok ? AL[o] : 0.0f;
+        }
+        __syncthreads();
+        for (int mm = 0; mm < mc; ++mm) {
+            const float s = ss[tau * kBP + mm];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int t = tq + j;
+                if (t >= tau) g[j] += __expf(s - ls[t * kBP + mm]) * as[t * kBP + mm];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) gl[tau * kBP + tq + j] = (tq + j >= tau && tq + j < nt) ? g[j] : 0.0f;
+    __syncthreads();
+    // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token
+    const float* lend = L + rbase + (size_t)(nt - 1) * M;
+    for (int e = tid; e < nt * M; e += kBNT) ql[e] = __expf(S[rbase + e] - lend[e % M]);
+    stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
+    __syncthreads();
+    const int col = tid & 63, rg = tid >> 6;
+    float acc[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int t = 0; t < nt; ++t) {
+        const float gval = gs[t * kBP + col];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += gl[(rg + 4 * r) * kBP + t] * gval;
+    }
+    if (c + 1 < NC && col < ds) {
+        const float* xr = X + ((size_t)bh * NC + c) * M * Dv + d0 + col;
+        for (int m = 0; m < M; ++m) {
+            const float xv = xr[(size_t)m * Dv];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] += ql[(rg + 4 * r) * M + m] * xv;
+        }
+    }
+    if (col < ds) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tk = rg + 4 * r;
+            if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d0 + col] = from_f32<T>(acc[r]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_ds: ds_tau m = e^{s - Lend}(v_tau . X_m - Y_m)
+//                  + sum_{t >= tau} e^{s_tau m - L_tm}(alpha_tm GV[t][tau] - c_tm),
+// written over s.  Thread m; the later-chunk term is accumulated first in
+// registers (one per token of the chunk) and parked in DS until the in-chunk
+// sum is added.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
+    const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv, float* __restrict__ S,
+    const float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ C,
+    const float* __restrict__ X, const float* __restrict__ Ysum) {
+    __shared__ float st[kBT * 256];
+    __shared__ float gvl[kBT * kBP];
+    __shared__ float gs[kBT * kBP];
+    __shared__ float vs[kBT * kBP];
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
+    const bool act = m < M;
+    const int t0 = c * kBT, nt = min(kBT, N - t0);
+    const bool carry = c + 1 < NC;
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    for (int e = tid; e < nt * M; e += kBNT) st[e] = S[rbase + e];
+    float gv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
+    float acc[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
+    const float* xr = X + (((size_t)bh * NC + c) * M + (act ? m : 0)) * Dv;
+    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+        const int ds = min(kBSlab, Dv - d0);
+        __syncthreads();
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds);
+        __syncthreads();
+        gv_accumulate(gv, gs, vs, ds);
+        if (act && carry) {
+            for (int d = 0; d < ds; d += 4) {
+                const float4 p = *reinterpret_cast<const float4*>(xr + d0 + d);
+#pragma unroll
+                for (int t = 0; t < kBT; ++t) {
+                    const float* vr = vs + t * kBP + d;
+                    acc[t] += vr[0] * p.x + vr[1] * p.y + vr[2] * p.z + vr[3] * p.w;
+                }
+            }
+        }
+    }
+    gv_store(gv, gvl);
+    __syncthreads();
+    if (!act) return;
+    if (carry) {
+        const float lend = L[rbase + (size_t)(nt - 1) * M + m];
+        const float ysum = Ysum[((size_t)bh * NC + c) * M + m];
+#pragma unroll
+        for (int t = 0; t < kBT; ++t)
+            if (t < nt) S[rbase + (size_t)t * M + m] = __expf(st[t * M + m] - lend) * (acc[t] - ysum);
+    }
+    float lt[kBT], at[kBT], ct[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) {
+        const bool ok = t < nt;
+        const size_t o = rbase + (size_t)t * M + m;
+        lt[t] = ok ? L[o] : 0.0f;
+        at[t] = ok ? AL[o] : 0.0f;
+        ct[t] = ok ? C[o] : 0.0f;
+    }
+    for (int tau = 0; tau < nt; ++tau) {
+        const float s = st[tau * M + m];
+        float sum = 0.0f;
+#pragma unroll
+        for (int t = 0; t < kBT; ++t)
+            if (t >= tau && t < nt) sum += __expf(s - lt[t]) * (at[t] * gvl[t * kBP + tau] - ct[t]);
+        const size_t o = rbase + (size_t)tau * M + m;
+        S[o] = (carry ? S[o] : 0.0f) + sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_dk: per token, dK_t = scale sum_m (ds_tm Q_m [+ da_tm Kd_m when Qd = K])
+// and dQd_t = scale sum_m da_tm Kd_m (separate Qd); da_tm = c_tm - alpha_tm gy_t.
+// Thread (col, tg) owns tokens tg + 4 r (r < 4) and columns col + 64 k.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
+    const T* __restrict__ Q, const T* __restrict__ Kd, int N, int H, int M, int Dk, float scale, bool sep_q,
+    const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
+    const float* __restrict__ gy, T* __restrict__ dK, T* __restrict__ dQd) {
+    __shared__ float dsl[kBTok * 256];
+    __shared__ float dal[kBTok * 256];
+    const int bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int t0 = blockIdx.x * kBTok, nt = min(kBTok, N - t0);
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    for (int e = tid; e < kBTok * M; e += kBNT) {
+        const int i = e / M;
+        const bool ok = i < nt;
+        dsl[e] = ok ? DS[rbase + e] : 0.0f;
+        dal[e] = ok ? C[rbase + e] - AL[rbase + e] * gy[(size_t)bh * N + t0 + i] : 0.0f;
+    }
+    __syncthreads();
+    const int col = tid & 63, tg = tid >> 6;
+    for (int d0 = 0; d0 < Dk; d0 += 64) {
+        const int d = d0 + col;
+        if (d >= Dk) break;
+        float ak[4] = {0.f, 0.f, 0.f, 0.f}, aq[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < M; ++m) {
+            const float qv = to_f32(Q[((size_t)h * M + m) * Dk + d]);
+            const float kv = to_f32(Kd[((size_t)h * M + m) * Dk + d]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = tg + 4 * r;
+                ak[r] += dsl[i * M + m] * qv;
+                aq[r] += dal[i * M + m] * kv;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = tg + 4 * r;
+            if (i >= nt) continue;
+            const size_t o = tok_index(b, t0 + i, h, N, H, Dk) + d;
+            if (sep_q) {
+                dK[o] = from_f32<T>(scale * ak[r]);
+                dQd[o] = from_f32<T>(scale * aq[r]);
+            } else {
+                dK[o] = from_f32<T>(scale * (ak[r] + aq[r]));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_dq: partial sums over a group of kBGroup tokens of
+//   P1_m = sum_t ds_tm k_t (+ da_tm qd_t when Kd = Q),  P2_m = sum_t da_tm qd_t.
+// grid (NG, BH, ceil(Dk/64)); thread (col, mg) owns m = mg + 4 r.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
+    const T* __restrict__ K, const T* __restrict__ Qd, int N, int H, int M, int Dk, bool sep_k,
+    const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
+    const float* __restrict__ gy, float* __restrict__ P1, float* __restrict__ P2) {
+    __shared__ float dsl[kBTok * 256];
+    __shared__ float dal[kBTok * 256];
+    __shared__ float kt[kBTok * 64];
+    __shared__ float qt[kBTok * 64];
+    const int g = blockIdx.x, NG = gridDim.x, bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int d0 = blockIdx.z * 64;
+    const int col = tid & 63, mg = tid >> 6, rows = M >> 2;
+    float a1[64], a2[64];
+#pragma unroll
+    for (int r = 0; r < 64; ++r) a1[r] = a2[r] = 0.0f;
+    const int tg0 = g * kBGroup, tg1 = min(N, tg0 + kBGroup);
+    for (int t0 = tg0; t0 < tg1; t0 += kBTok) {
+        const int nt = min(kBTok, tg1 - t0);
+        const size_t rbase = ((size_t)bh * N + t0) * M;
+        __syncthreads();
+        for (int e = tid; e < kBTok * M; e += kBNT) {
+            const int i = e / M;
+            const bool ok = i < nt;
+            dsl[e] = ok ? DS[rbase + e] : 0.0f;
+            dal[e] = ok ? C[rbase + e] - AL[rbase + e] * gy[(size_t)bh * N + t0 + i] : 0.0f;
+        }
+        for (int e = tid; e < kBTok * 64; e += kBNT) {
+            const int i = e >> 6, d = d0 + (e & 63);
+            const bool ok = i < nt && d < Dk;
+            const size_t o = tok_index(b, t0 + i, h, N, H, Dk) + d;
+            kt[e] = ok ? to_f32(K[o]) : 0.0f;
+            qt[e] = ok ? to_f32(Qd[o]) : 0.0f;
+        }
+        __syncthreads();
+        for (int i = 0; i < nt; ++i) {
+            const float kv = kt[i * 64 + col], qv = qt[i * 64 + col];
+            const float* dr = dsl + i * M + mg;
+            const float* ar = dal + i * M + mg;
+#pragma unroll
+            for (int r = 0; r < 64; ++r) {
+                if (r < rows) {
+                    a1[r] += dr[4 * r] * kv;
+                    a2[r] += ar[4 * r] * qv;
+                }
+            }
+        }
+    }
+    if (d0 + col >= Dk) return;
+#pragma unroll
+    for (int r = 0; r < 64; ++r) {
+        if (r >= rows) break;
+        const size_t o = (((size_t)bh * NG + g) * M + mg + 4 * r) * Dk + d0 + col;
+        if (sep_k) {
+            P1[o] = a1[r];
+            P2[o] = a2[r];
+        } else {
+            P1[o] = a1[r] + a2[r];
+        }
+    }
+}
+
+// out[h][m][d] = scale * sum over (b, group) of P[(b H + h)][group][m][d]
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict__ P, int B, int H, int NG,
+                                                         int MD, float scale, T* __restrict__ out) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (int64_t)H * MD) return;
+    const int h = (int)(gid / MD), e = (int)(gid % MD);
+    float sum = 0.0f;
+    for (int b = 0; b < B; ++b)
+        for (int g = 0; g < NG; ++g) sum += P[(((size_t)b * H + h) * NG + g) * MD + e];
+    out[gid] = from_f32<T>(scale * sum);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+struct BwdLayout {
+    int64_t NC, NG;
+    size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_c, off_gy, off_p1, off_p2, total;
+    BwdLayout(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
+        NC = (N + kBT - 1) / kBT;
+        NG = (N + kBGroup - 1) / kBGroup;
+        const size_t BH = (size_t)B * H;
+        size_t o = 0;
+        auto take = [&](size_t floats) {
+            const size_t at = o;
+            o += ((floats * sizeof(float) + 255) / 256) * 256;
+            return at;
+        };
+        off_pm = take(BH * NC * M);
+        off_pd = take(BH * NC * M);
+        off_pn = take(BH * NC * M * Dv);
+        off_s = take(BH * N * M);
+        off_l = take(BH * N * M);
+        off_al = take(BH * N * M);
+        off_c = take(BH * N * M);
+        off_gy = take(BH * N);
+        off_p1 = take(BH * NG * M * Dk);
+        off_p2 = take(BH * NG * M * Dk);
+        total = o + 256;
+    }
+};
+
+template <typename T>
+static int run_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
+                        int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                        const void* Yp, const void* dYp, void* dQ, void* dK, void* dV, void* dQd, void* dKd,
+                        char* ws, const BwdLayout& lay, hipStream_t st) {
+    const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
+    const bool shared = !sep_q && !sep_k;
+    float* pm = reinterpret_cast<float*>(ws + lay.off_pm);
+    float* pd = reinterpret_cast<float*>(ws + lay.off_pd);
+    float* pn = reinterpret_cast<float*>(ws + lay.off_pn);
+    float* S = reinterpret_cast<float*>(ws + lay.off_s);
+    float* L = reinterpret_cast<float*>(ws + lay.off_l);
+    float* AL = reinterpret_cast<float*>(ws + lay.off_al);
+    float* C = reinterpret_cast<float*>(ws + lay.off_c);
+    float* gy = reinterpret_cast<float*>(ws + lay.off_gy);
+    float* P1 = reinterpret_cast<float*>(ws + lay.off_p1);
+    float* P2 = reinterpret_cast<float*>(ws + lay.off_p2);
+    const int64_t NC = lay.NC, NG = lay.NG, BH = B * H;
+    const T* q = static_cast<const T*>(Q);
+    const T* k = static_cast<const T*>(K);
+    const T* v = static_cast<const T*>(V);
+    const T* qd = sep_q ? static_cast<const T*>(Qdec) : k;
+    const T* kd = sep_k ? static_cast<const T*>(Kdec) : q;
+    const T* y = static_cast<const T*>(Yp);
+    const T* dy = static_cast<const T*>(dYp);
+    int rc;
+    // chunk starting states at the backward's chunk length
+    if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, kBT, pm, pd, pn, st))) return rc;
+    if ((rc = launch_prefix_public(pm, pd, pn, BH, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                   nullptr, st)))
+        return rc;
+    const dim3 gc((unsigned)NC, (unsigned)BH);
+    hipLaunchKernelGGL(bwd_stats_kernel<T>, gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M, (int)Dk,
+                       scale, shared, pm, pd, S, L, AL);
+    if ((rc = check_launch("bwd_stats_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
+                       L, AL, C);
+    if ((rc = check_launch("bwd_gz_kernel"))) return rc;
+    const int64_t rows = B * N * H;
+    hipLaunchKernelGGL(bwd_gy_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, y, (int)N,
+                       (int)H, (int)Dv, rows, gy);
+    if ((rc = check_launch("bwd_gy_kernel"))) return rc;
+    const unsigned nslab = (unsigned)((Dv + kBSlab - 1) / kBSlab);
+    hipLaunchKernelGGL(bwd_summary_kernel<T>, dim3((unsigned)NC, (unsigned)BH, nslab), dim3(kBNT), 0, st, dy,
+                       (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
+    if ((rc = check_launch("bwd_summary_kernel"))) return rc;
+    const int64_t cthreads = BH * M * (Dv / 4);
+    hipLaunchKernelGGL(bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, st, pn, pd, L,
+                       (int)N, (int)NC, (int)M, (int)Dv, BH * M);
+    if ((rc = check_launch("bwd_carry_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_dv_kernel<T>, dim3((unsigned)NC, (unsigned)BH, nslab), dim3(kBNT), 0, st, dy, (int)N,
+                       (int)H, (int)M, (int)Dv, S, L, AL, pn, static_cast<T*>(dV));
+    if ((rc = check_launch("bwd_dv_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, AL,
+                       C, pn, pd);
+    if ((rc = check_launch("bwd_ds_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kBTok - 1) / kBTok), (unsigned)BH), dim3(kBNT), 0,
+                       st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, S, AL, C, gy,
+                       static_cast<T*>(dK), static_cast<T*>(dQd));
+    if ((rc = check_launch("bwd_dk_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
+                       dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, S, AL, C, gy, P1, P2);
+    if ((rc = check_launch("bwd_dq_kernel"))) return rc;
+    const int64_t red = H * M * Dk;
+    hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P1, (int)B,
+                       (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dQ));
+    if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
+    if (sep_k) {
+        hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P2,
+                           (int)B, (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dKd));
+        if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
+    }
+    return FLARE_OK;
+}
+
+}  // namespace flare
+
+using namespace flare;
+
+extern "C" {
+
+size_t flare_ar_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
+    return BwdLayout(B, N, H, M, Dk, Dv).total;
+}
+
+int flare_ar_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
+                      int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                      const void* Y, const void* dY, void* dQ, void* dK, void* dV, void* dQdec, void* dKdec,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+    FLARE_REQUIRE(Q && K && V && Y && dY && dQ && dK && dV, "flare_ar_backward: null tensor pointer");
+    FLARE_REQUIRE(dtype == FLARE_F32 || dtype == FLARE_BF16 || dtype == FLARE_F16,
+                  "flare_ar_backward: unknown dtype code %d", dtype);
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0, "flare_ar_backward: empty problem (B=%lld N=%lld H=%lld)",
+                  (long long)B, (long long)N, (long long)H);
+    FLARE_REQUIRE(M % 16 == 0 && M >= 16 && M <= 256,
+                  "flare_ar_backward: M=%lld must be a multiple of 16 in [16, 256]", (long long)M);
+    FLARE_REQUIRE(Dk % 16 == 0 && Dk >= 16 && Dk <= 256,
+                  "flare_ar_backward: D_score=%lld must be a multiple of 16 in [16, 256]", (long long)Dk);
+    FLARE_REQUIRE(Dv % 16 == 0 && Dv >= 16 && Dv <= 512,
+                  "flare_ar_backward: D_value=%lld must be a multiple of 16 in [16, 512]", (long long)Dv);
+    FLARE_REQUIRE(!Qdec || dQdec, "flare_ar_backward: Qdec given without dQdec");
+    FLARE_REQUIRE(!Kdec || dKdec, "flare_ar_backward: Kdec given without dKdec");
+    const BwdLayout lay(B, N, H, M, Dk, Dv);
+    FLARE_REQUIRE(workspace && workspace_bytes >= lay.total,
+                  "flare_ar_backward: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                  lay.total);
+    FLARE_REQUIRE((((uintptr_t)workspace) & 255) == 0, "flare_ar_backward: workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+#define FLARE_BWD(TY)                                                                                          \
+    return run_backward<TY>(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, Y, dY, dQ, dK, dV, dQdec, \
+                            dKdec, ws, lay, st)
+    if (dtype == FLARE_BF16) FLARE_BWD(__hip_bfloat16);
+    if (dtype == FLARE_F16) FLARE_BWD(__half);
+    FLARE_BWD(float);
+#undef FLARE_BWD
+}
+
+}  // extern "C"

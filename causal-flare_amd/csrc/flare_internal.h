@@ -56,6 +56,9 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
                             float* lse_dec, float* lse_enc, hipStream_t stream);
+int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
+                          int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
+                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);
 int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M, int64_t Dv,
                          const float* m0, const float* d0, const float* u0, float* m_fin, float* d_fin,
                          float* u_fin, hipStream_t stream);

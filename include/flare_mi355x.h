@@ -118,6 +118,24 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
 int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 
 /*
+ * Backward of the chunked forward (flare_ar_forward without initial state or
+ * mask): from the forward's inputs, its output Y and dY (all in `dtype`,
+ * Y and dY [B, N, H, Dv]) write dQ [H, M, Dk], dK [B, N, H, Dk], dV [B, N, H, Dv]
+ * and, when Qdec / Kdec are given, dQdec [B, N, H, Dk] / dKdec [H, M, Dk], all
+ * in `dtype`.  A NULL Qdec (Kdec) means the decoder uses K (Q) and its gradient
+ * is folded into dK (dQ).  Requires M, Dk, Dv multiples of 16 with M <= 256,
+ * Dk <= 256, Dv <= 512.  Replaces _chunked_flare_lse_backward_impl
+ * (training.py:4369-4918), the autograd backward of AutoRegressiveFLARE.
+ */
+size_t flare_ar_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk,
+                                        int64_t Dv);
+int flare_ar_backward(const void* Q, const void* K, const void* V, const void* Qdec,
+                      const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                      int64_t Dk, int64_t Dv, float scale, const void* Y, const void* dY, void* dQ,
+                      void* dK, void* dV, void* dQdec, void* dKdec, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * One recurrent decode step for every (b,h): K, V (and Qdec) are [B, H, D];
  * the fp32 state m/d/u is updated in place; y [B, H, Dv] is written in
  * `out_dtype`.  mask [B] (int32, nonzero = valid) may be NULL; an invalid

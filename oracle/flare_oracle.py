@@ -19,6 +19,9 @@ Two layers:
     - ``brute_ar_state``: the same definition continued from a cached state
       ``{m, d, u}`` (``inference.py:66-120``), with an optional token mask.
   They are the pins for the C restatement (see tests/test_oracle.py).
+* ``ar_grads``: fp64 torch autograd of ``ar_forward_torch64`` (the same
+  definition with cumulative sums), the ground truth of the backward; pinned
+  by ``brute_ar`` (forward values) and by central finite differences.
 
 Parity status: every C entry point is pinned by fp64 brute force, by
 invariants (chunk-size independence, prefill/decode continuation, state
@@ -301,3 +304,47 @@ def allclose_rel(a, b, dtype_name: str):
         return 0.0, 0.0
     d = np.abs(a - b)
     return float((d / (np.abs(b) + atol)).max()), float(d.max())
+
+
+# --------------------------------------------------------------------------
+# Gradients (fp64 autograd of the definition)
+# --------------------------------------------------------------------------
+
+def ar_forward_torch64(Q, K, V, scale=None, Q_dec=None, K_dec=None):
+    """The definition of reference.py:15-47 in fp64 torch ops, differentiable.
+
+    z_t = sum_{tau<=t} e^{s_tau} v_tau / sum_{tau<=t} e^{s_tau} is written with
+    cumulative sums relative to each latent's sequence-wide max (exact in fp64
+    for the score ranges the tests use); y_t = softmax_m(a_t) . z_t.  Inputs
+    must be fp64 torch tensors; returns Y [B, N, H, Dv].
+    """
+    import torch
+    H, M, Dk = Q.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = K if Q_dec is None else Q_dec
+    Kd = Q if K_dec is None else K_dec
+    S = scale * torch.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * torch.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    E = torch.exp(S - S.amax(dim=2, keepdim=True))                      # [B,H,N,M]
+    Vt = V.transpose(1, 2)                                              # [B,H,N,Dv]
+    num = torch.cumsum(E.unsqueeze(-1) * Vt.unsqueeze(3), dim=2)        # [B,H,N,M,Dv]
+    Z = num / torch.cumsum(E, dim=2).unsqueeze(-1)
+    Y = torch.einsum("bhnm,bhnmd->bhnd", torch.softmax(A, dim=-1), Z)
+    return Y.transpose(1, 2)
+
+
+def ar_grads(Q, K, V, dY, scale=None, Q_dec=None, K_dec=None):
+    """Gradients of sum(Y * dY) w.r.t. (Q, K, V, Q_dec, K_dec), fp64 autograd --
+    the ground truth of the reference's backward tests
+    (testing/autoregressive/test_flare.py:184-219, 370-427), which backpropagate
+    (y * grad_out).sum() through the torch reference.  Returns numpy arrays
+    (None for an absent decoder tensor)."""
+    import torch
+
+    def leaf(x):
+        return None if x is None else torch.as_tensor(_f64(x)).requires_grad_(True)
+
+    q, k, v, qd, kd = (leaf(x) for x in (Q, K, V, Q_dec, K_dec))
+    y = ar_forward_torch64(q, k, v, scale, qd, kd)
+    (y * torch.as_tensor(_f64(dY))).sum().backward()
+    return tuple(None if x is None else x.grad.numpy() for x in (q, k, v, qd, kd))

@@ -1,0 +1,154 @@
+"""GPU parity of the backward (flare_ar_backward through AutoRegressiveFLARE)
+against the fp64 autograd oracle (oracle/flare_oracle.py: ar_grads).
+
+Mirrors testing/autoregressive/test_flare.py:370-427 (decoder-flag backward
+against the torch reference) and widens it to multi-chunk, ragged, bf16 and
+sharp-score cases.
+
+Tolerances:
+  * the reference's own backward bar for fp32 inputs at its test shape,
+    torch.testing.assert_close(rtol=1e-2, atol=1e-3) (test_flare.py:421-427);
+  * elsewhere a scale-free bar: max |g - g_ref| <= tol * max(max |g_ref|, 1e-2)
+    per gradient tensor (the floor covers gradients that vanish exactly, such
+    as dQ and dK for a one-token sequence, where y_0 = v_0); tol = 1e-4 for
+    fp32 inputs (fp32 accumulation over up to a few thousand tokens) and 2e-2
+    for bf16 inputs (bf16 inputs and bf16 gradients, each rounded at 2^-8
+    relative).
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import flare_oracle as O
+from _util import to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _case(*args):
+    print("CASE", *args, flush=True)
+    sys.stdout.flush()
+
+
+def _inputs(seed, B, N, H, M, D, Dv, dtype, sep_q, sep_k, q_std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(s, generator=g)
+    Q = r(H, M, D) * q_std
+    K, V = r(B, N, H, D), r(B, N, H, Dv)
+    Qd = r(B, N, H, D) if sep_q else None
+    Kd = r(H, M, D) * q_std if sep_k else None
+    G = r(B, N, H, Dv)
+    cast = lambda t: None if t is None else t.to(dtype)
+    return tuple(cast(t) for t in (Q, K, V, Qd, Kd, G))
+
+
+def _run(Q, K, V, Qd, Kd, G, scale, chunk=None):
+    from causal_flare import flare_autoregressive_triton
+    leaves = [None if t is None else t.to(DEV).requires_grad_(True) for t in (Q, K, V, Qd, Kd)]
+    y = flare_autoregressive_triton(leaves[0], leaves[1], leaves[2], scale=scale, chunk_size=chunk,
+                                    Q_dec=leaves[3], K_dec=leaves[4])
+    (y.float() * G.to(DEV).float()).sum().backward()
+    return y, [None if t is None else t.grad for t in leaves]
+
+
+def _check(grads, ref, tol, what):
+    for name, g, r in zip(("dQ", "dK", "dV", "dQ_dec", "dK_dec"), grads, ref):
+        if r is None:
+            assert g is None, f"{what}: unexpected {name}"
+            continue
+        a = to_np(g).astype(np.float64)
+        assert a.shape == r.shape, (what, name, a.shape, r.shape)
+        assert np.isfinite(a).all(), f"{what}: non-finite {name}"
+        err = np.abs(a - r).max() / max(np.abs(r).max(), 1e-2)
+        assert err <= tol, f"{what}: {name} normalised max error {err:.3e} > {tol}"
+
+
+@pytest.mark.parametrize("d_score,d_value", [(16, 16), (64, 128)])
+def test_decoder_flags_backward_reference_shape(d_score, d_value):
+    """test_flare.py:370-427 at its shape and tolerance."""
+    B, N, H, M = 1, 16, 2, 16
+    scale = 1.0 / math.sqrt(d_score)
+    for sep_q in (False, True):
+        for sep_k in (False, True):
+            _case("bwd_ref_shape", d_score, d_value, sep_q, sep_k)
+            Q, K, V, Qd, Kd, G = _inputs(2029, B, N, H, M, d_score, d_value, torch.float32, sep_q, sep_k)
+            y, grads = _run(Q, K, V, Qd, Kd, G, scale, chunk=16)
+            ref = O.ar_grads(Q, K, V, G, scale, Qd, Kd)
+            for name, g, r in zip(("q", "k", "v", "q_dec", "k_dec"), grads, ref):
+                if r is None:
+                    continue
+                torch.testing.assert_close(g.cpu().double(), torch.as_tensor(r), rtol=1e-2, atol=1e-3,
+                                           msg=lambda m: f"{name} sep_q={sep_q} sep_k={sep_k}: {m}")
+
+
+@pytest.mark.parametrize("q_dec_mode", ["none", "k_enc", "rand"])
+@pytest.mark.parametrize("k_dec_mode", ["none", "q_enc", "rand"])
+def test_backward_aliasing_modes_fp32(q_dec_mode, k_dec_mode):
+    """The 3x3 decoder aliasing modes (test_flare.py:430-490): a decoder tensor
+    that is the encoder tensor itself gets its gradient folded into dK / dQ."""
+    from causal_flare import flare_autoregressive_triton
+    _case("bwd_alias", q_dec_mode, k_dec_mode)
+    B, N, H, M, D, Dv = 2, 150, 2, 32, 32, 48
+    Q, K, V, Qd, Kd, G = _inputs(11, B, N, H, M, D, Dv, torch.float32, True, True)
+    q, k, v = (t.to(DEV).requires_grad_(True) for t in (Q, K, V))
+    qd = {"none": None, "k_enc": k, "rand": Qd.to(DEV).requires_grad_(True)}[q_dec_mode]
+    kd = {"none": None, "q_enc": q, "rand": Kd.to(DEV).requires_grad_(True)}[k_dec_mode]
+    y = flare_autoregressive_triton(q, k, v, scale=0.2, Q_dec=qd, K_dec=kd)
+    (y * G.to(DEV)).sum().backward()
+    ref = O.ar_grads(Q, K, V, G, 0.2, Qd if q_dec_mode == "rand" else None, Kd if k_dec_mode == "rand" else None)
+    got = [q.grad, k.grad, v.grad, qd.grad if q_dec_mode == "rand" else None,
+           kd.grad if k_dec_mode == "rand" else None]
+    _check(got, ref, 1e-4, f"alias q_dec={q_dec_mode} k_dec={k_dec_mode}")
+
+
+@pytest.mark.parametrize("B,N,H,M,D,Dv", [(1, 1, 1, 16, 16, 16), (2, 63, 1, 16, 32, 16), (1, 65, 2, 48, 16, 80),
+                                          (2, 300, 2, 64, 64, 64), (1, 2100, 1, 32, 32, 32)])
+@pytest.mark.parametrize("sep", [(False, False), (True, True)])
+def test_backward_shapes_fp32(B, N, H, M, D, Dv, sep):
+    """Ragged final chunks, one-token sequences, many chunks (the reverse carry)."""
+    _case("bwd_fp32", B, N, H, M, D, Dv, sep)
+    Q, K, V, Qd, Kd, G = _inputs(5, B, N, H, M, D, Dv, torch.float32, *sep)
+    scale = 1.0 / math.sqrt(D)
+    _, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), 1e-4, f"fp32 {B, N, H, M, D, Dv, sep}")
+
+
+@pytest.mark.parametrize("q_std", [2.0, 4.0])
+def test_backward_sharp_scores_fp32(q_std):
+    """Large scores: running maxima move by tens within a chunk, so the factors
+    e^{s - L} span many orders of magnitude."""
+    _case("bwd_sharp", q_std)
+    Q, K, V, Qd, Kd, G = _inputs(8, 1, 400, 2, 32, 32, 32, torch.float32, False, False, q_std=q_std)
+    _, grads = _run(Q, K, V, Qd, Kd, G, 1.0)
+    _check(grads, O.ar_grads(Q, K, V, G, 1.0, Qd, Kd), 1e-4, f"sharp q_std={q_std}")
+
+
+@pytest.mark.parametrize("M,D,N", [(128, 64, 1000), (256, 128, 300)])
+@pytest.mark.parametrize("sep", [(False, False), (True, False), (False, True)])
+def test_backward_bf16(M, D, N, sep):
+    _case("bwd_bf16", M, D, N, sep)
+    Q, K, V, Qd, Kd, G = _inputs(9, 1, N, 2, M, D, D, torch.bfloat16, *sep)
+    Q = (Q.float() / math.sqrt(D)).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    y, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    assert y.dtype == torch.bfloat16 and all(g is None or g.dtype == torch.bfloat16 for g in grads)
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), 2e-2, f"bf16 M={M} D={D} N={N} sep={sep}")
+
+
+def test_backward_c_abi_rejects_bad_arguments():
+    from causal_flare import _lib
+    lib = _lib.lib()
+    B, N, H, M, D = 1, 16, 1, 16, 16
+    t = torch.zeros(64, device=DEV)
+    P = _lib.ptr
+    need = lib.flare_ar_backward_workspace_size(B, N, H, M, D, D)
+    rc = lib.flare_ar_backward(P(t), P(t), P(t), None, None, 0, B, N, H, M, D, D, 1.0, P(t), P(t), P(t), P(t),
+                               P(t), None, None, P(t), need - 1, None)
+    assert rc != 0 and b"workspace" in lib.flare_last_error()
+    rc = lib.flare_ar_backward(P(t), P(t), P(t), None, None, 0, B, N, H, 512, D, D, 1.0, P(t), P(t), P(t), P(t),
+                               P(t), None, None, P(t), need, None)
+    assert rc != 0 and b"M=512" in lib.flare_last_error()

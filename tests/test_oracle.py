@@ -188,3 +188,64 @@ def test_golden_fixtures():
             else:
                 y, _ = O.ar_recurrent(q, k, v, scale=float(z["scale"]))
             _close(y, z["y"], 3e-5)
+
+
+# --------------------------------------------------------------------------
+# Gradient oracle (ar_grads): pinned by the per-token definition (forward
+# values) and by central finite differences of that definition.
+# --------------------------------------------------------------------------
+def _grad_inputs(seed, B, N, H, M, D, Dv, sep_q, sep_k):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(s, generator=g, dtype=torch.float64)
+    Q, K, V = r(H, M, D), r(B, N, H, D), r(B, N, H, Dv)
+    Qd = r(B, N, H, D) if sep_q else None
+    Kd = r(H, M, D) if sep_k else None
+    return Q, K, V, Qd, Kd, r(B, N, H, Dv)
+
+
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, False), (False, True), (True, True)])
+def test_grad_oracle_forward_is_the_definition(sep_q, sep_k):
+    Q, K, V, Qd, Kd, _ = _grad_inputs(3, 2, 19, 2, 8, 8, 5, sep_q, sep_k)
+    y = O.ar_forward_torch64(Q, K, V, 0.6, Qd, Kd)
+    _close(y.numpy(), O.brute_ar(Q, K, V, 0.6, Qd, Kd), 1e-12)
+
+
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, False), (False, True), (True, True)])
+def test_grad_oracle_matches_finite_differences(sep_q, sep_k):
+    """Central differences of sum(brute_ar * dY) (the numpy per-token
+    definition, independent of the autograd graph) at every input entry."""
+    Q, K, V, Qd, Kd, G = _grad_inputs(5, 1, 6, 1, 4, 3, 2, sep_q, sep_k)
+    grads = O.ar_grads(Q, K, V, G, 0.8, Qd, Kd)
+    inputs = [Q, K, V, Qd, Kd]
+    Gn = G.numpy()
+    h = 1e-6
+    for idx, (x, gx) in enumerate(zip(inputs, grads)):
+        if x is None:
+            assert gx is None
+            continue
+        fd = np.zeros(x.shape)
+        for j in range(x.numel()):
+            vals = []
+            for sgn in (1.0, -1.0):
+                xs = [t.clone() if t is not None else None for t in inputs]
+                xs[idx].view(-1)[j] += sgn * h
+                vals.append(float((O.brute_ar(xs[0], xs[1], xs[2], 0.8, xs[3], xs[4]) * Gn).sum()))
+            fd.reshape(-1)[j] = (vals[0] - vals[1]) / (2 * h)
+        np.testing.assert_allclose(gx, fd, rtol=1e-6, atol=1e-8)
+
+
+def test_grad_oracle_single_latent_is_attention_backward():
+    """M = 1: alpha = 1 and y is causal softmax attention of the latent's
+    scores, whose gradient torch's SDPA backward gives independently."""
+    Q, K, V, _, _, G = _grad_inputs(7, 1, 9, 2, 1, 4, 3, False, False)
+    dQ, dK, dV, _, _ = O.ar_grads(Q, K, V, G, 0.5)
+    q, k, v = (t.clone().requires_grad_(True) for t in (Q, K, V))
+    # y_t = sum_{tau<=t} softmax_tau(0.5 k_tau . q) v_tau: attention with query q
+    # repeated per token, key k, causal mask -- but the decoder score also
+    # depends on k through alpha = softmax over one latent = 1 (no gradient).
+    qq = q[:, 0].unsqueeze(0).unsqueeze(2).expand(1, 2, 9, 4)            # [B,H,N,D]
+    y = F.scaled_dot_product_attention(qq, k.transpose(1, 2), v.transpose(1, 2), is_causal=True, scale=0.5)
+    (y.transpose(1, 2) * G).sum().backward()
+    _close(dV, v.grad.numpy(), 1e-10)
+    _close(dK, k.grad.numpy(), 1e-10)
+    _close(dQ, q.grad.numpy(), 1e-10)
