@@ -30,9 +30,9 @@
 //   bwd_stats    s, L, alpha per (t, m)                   grid (NC, BH)
 //   bwd_gz       c = alpha gz per (t, m)                  grid (NC, BH)
 //   bwd_gy       gy = dY . Y per token                    grid (tokens)
-//   bwd_summary  per-chunk terms of X, Y                  grid (NC, BH, Dv/64)
+//   bwd_summary  per-chunk terms of X, Y                  grid (NC, BH)
 //   bwd_carry    reverse scan over chunks -> X_c, Y_c     grid (BH M Dv/4)
-//   bwd_dv       dV                                        grid (NC, BH, Dv/64)
+//   bwd_dv       dV                                        grid (NC, BH)
 //   bwd_ds       ds (written over s)                      grid (NC, BH)
 //   bwd_dk       dK, dQ_dec per token                     grid (N/16, BH)
 //   bwd_dq       dQ, dK_dec partial sums per token group  grid (NG, BH, Dk/64)
@@ -55,9 +55,17 @@ __device__ __forceinline__ size_t tok_index(int b, int t, int h, int N, int H, i
     return (((size_t)b * N + t) * H + h) * D;
 }
 
+constexpr float kBLog2e = 1.4426950408889634f;
+constexpr int kGT = 68;        // pitch of the transposed GV tile and of 16-byte-read tiles
+
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+
 // ---------------------------------------------------------------------------
-// bwd_stats: per chunk, scores s (encoder), L = log of the running den from
-// the chunk's starting state, and the decoder weights alpha.
+// bwd_stats: per chunk, scores s2 = s log2(e) (encoder), L2 = log2 of the
+// running den from the chunk's starting state, and the decoder weights alpha.
+// S and L hold log2-domain values so that every later factor is one exp2.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
@@ -72,9 +80,9 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
-    float mx = kNegInf, dn = 0.0f;
+    float mx = kNegInf, dn = 0.0f;      // running max (log2 units) and den relative to it
     if (act) {
-        mx = pmax[((size_t)bh * NC + c) * M + m];
+        mx = pmax[((size_t)bh * NC + c) * M + m] * kBLog2e;
         dn = pden[((size_t)bh * NC + c) * M + m];
     }
     const T* qrow = Q + ((size_t)h * M + (act ? m : 0)) * Dk;
@@ -98,16 +106,16 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
                             q3 = to_f32(qrow[d + 3]);
 #pragma unroll
                 for (int i = 0; i < kBTok; ++i) {
-                    const float* kr = kt + i * Dk + d;
-                    as[i] += kr[0] * q0 + kr[1] * q1 + kr[2] * q2 + kr[3] * q3;
+                    const float4 kr = ld4(kt + i * Dk + d);
+                    as[i] += kr.x * q0 + kr.y * q1 + kr.z * q2 + kr.w * q3;
                 }
                 if (!shared) {
                     const float k0 = to_f32(kdrow[d]), k1 = to_f32(kdrow[d + 1]), k2 = to_f32(kdrow[d + 2]),
                                 k3 = to_f32(kdrow[d + 3]);
 #pragma unroll
                     for (int i = 0; i < kBTok; ++i) {
-                        const float* qr = qdt + i * Dk + d;
-                        aa[i] += qr[0] * k0 + qr[1] * k1 + qr[2] * k2 + qr[3] * k3;
+                        const float4 qr = ld4(qdt + i * Dk + d);
+                        aa[i] += qr.x * k0 + qr.y * k1 + qr.z * k2 + qr.w * k3;
                     }
                 }
             }
@@ -115,12 +123,13 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
             for (int i = 0; i < kBTok; ++i) {
                 if (i < ni) {
                     const float s = as[i] * scale;
-                    const MergeScales ts = token_scales(mx, s);
-                    dn = dn * ts.sa + ts.sb;
-                    mx = ts.m_new;
+                    const float s2 = s * kBLog2e;
+                    const float mn = fmaxf(mx, s2);
+                    dn = dn * ex2(mx - mn) + ex2(s2 - mn);     // mx = -inf before the first token: ex2 -> 0
+                    mx = mn;
                     const size_t o = ((size_t)bh * N + t0 + i0 + i) * M + m;
-                    S[o] = s;
-                    L[o] = mx + __logf(dn);
+                    S[o] = s2;
+                    L[o] = mx + __log2f(dn);
                     at[i * M + m] = shared ? s : aa[i] * scale;
                 }
             }
@@ -148,14 +157,16 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
 
 // ---------------------------------------------------------------------------
 // Shared by bwd_gz and bwd_ds: GV[t][tau] = g_t . v_tau over one chunk, from
-// column slabs staged in LDS.  Thread (t = tid / 4, tau = 16 (tid % 4) + j).
+// column slabs staged in LDS, kept transposed (gvt[tau][t], pitch kGT) so that
+// a row of t values is read 16 bytes at a time.  Thread (t = tid / 4,
+// tau = 16 (tid % 4) + j).
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void stage_slab(float* dst, const T* __restrict__ src, int b, int t0, int nt, int h,
-                                           int N, int H, int D, int d0, int ds) {
+                                           int N, int H, int D, int d0, int ds, int pitch) {
     for (int e = threadIdx.x; e < kBT * kBSlab; e += kBNT) {
         const int i = e / kBSlab, d = e % kBSlab;
-        dst[i * kBP + d] = (i < nt && d < ds) ? to_f32(src[tok_index(b, t0 + i, h, N, H, D) + d0 + d]) : 0.0f;
+        dst[i * pitch + d] = (i < nt && d < ds) ? to_f32(src[tok_index(b, t0 + i, h, N, H, D) + d0 + d]) : 0.0f;
     }
 }
 
@@ -168,24 +179,26 @@ __device__ __forceinline__ void gv_accumulate(float (&gv)[16], const float* gs, 
     }
 }
 
-__device__ __forceinline__ void gv_store(const float (&gv)[16], float* gvl) {
+__device__ __forceinline__ void gv_store(const float (&gv)[16], float* gvt) {
     const int t = threadIdx.x >> 2, tq = (threadIdx.x & 3) * 16;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gvl[t * kBP + tq + j] = gv[j];
+    for (int j = 0; j < 16; ++j) gvt[(tq + j) * kGT + t] = gv[j];
 }
 
 // ---------------------------------------------------------------------------
 // bwd_gz: c_tm = alpha_tm gz_tm with
 //   gz_tm = e^{pm_m - L_tm} (g_t . pu_m) + sum_{tau <= t} e^{s_tau m - L_tm} (g_t . v_tau)
 // (pm, pu: the chunk's starting max and numerator, pu relative to pm).
+// Thread m; the pair sum runs over 16-token blocks of t: blocks wholly after
+// tau need no causal test, the diagonal block selects t >= tau.  L of tokens
+// past the sequence end is +inf, which zeroes their factors.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv,
     const float* __restrict__ pmax, const float* __restrict__ pnum, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ AL, float* __restrict__ C) {
-    __shared__ float st[kBT * 256];
-    __shared__ float gvl[kBT * kBP];
+    __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     __shared__ float gs[kBT * kBP];
     __shared__ float vs[kBT * kBP];
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
@@ -193,7 +206,6 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const bool act = m < M;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    for (int e = tid; e < nt * M; e += kBNT) st[e] = S[rbase + e];
     float gv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
@@ -204,13 +216,13 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
-        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
-        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds);
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
         if (act) {
             for (int d = 0; d < ds; d += 4) {
-                const float4 p = *reinterpret_cast<const float4*>(pu + d0 + d);
+                const float4 p = ld4(pu + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
                     const float* gr = gs + t * kBP + d;
@@ -219,21 +231,49 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
             }
         }
     }
-    gv_store(gv, gvl);
+    gv_store(gv, gvt);
     __syncthreads();
     if (!act) return;
     const float pm = pmax[((size_t)bh * NC + c) * M + m];
+    const float pm2 = pm * kBLog2e;
     float lt[kBT];
 #pragma unroll
     for (int t = 0; t < kBT; ++t) {
-        lt[t] = t < nt ? L[rbase + (size_t)t * M + m] : 0.0f;
-        acc[t] = pm == kNegInf ? 0.0f : __expf(pm - lt[t]) * acc[t];
+        lt[t] = t < nt ? L[rbase + (size_t)t * M + m] : __builtin_huge_valf();
+        acc[t] = pm == kNegInf ? 0.0f : ex2(pm2 - lt[t]) * acc[t];
     }
-    for (int tau = 0; tau < nt; ++tau) {
-        const float s = st[tau * M + m];
+    const float* scol = S + rbase + m;
 #pragma unroll
-        for (int t = 0; t < kBT; ++t)
-            if (t >= tau && t < nt) acc[t] += gvl[t * kBP + tau] * __expf(s - lt[t]);
+    for (int tb = 0; tb < kBT / 16; ++tb) {
+        if (16 * tb >= nt) break;
+        // tau < 16 tb: every t of the block is >= tau
+        float sn = scol[0];
+        for (int tau = 0; tau < 16 * tb; ++tau) {
+            const float s = sn;
+            sn = scol[(size_t)(tau + 1) * M];
+            const float* gr = gvt + tau * kGT + 16 * tb;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 g4 = ld4(gr + 4 * q);
+                const int t = 16 * tb + 4 * q;
+                acc[t] += g4.x * ex2(s - lt[t]);
+                acc[t + 1] += g4.y * ex2(s - lt[t + 1]);
+                acc[t + 2] += g4.z * ex2(s - lt[t + 2]);
+                acc[t + 3] += g4.w * ex2(s - lt[t + 3]);
+            }
+        }
+        // the diagonal block: tau in [16 tb, min(nt, 16 tb + 16))
+        const int tend = min(nt, 16 * tb + 16);
+        for (int tau = 16 * tb; tau < tend; ++tau) {
+            const float s = scol[(size_t)tau * M];
+            const float* gr = gvt + tau * kGT + 16 * tb;
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int t = 16 * tb + u;
+                const float e = ex2(s - lt[t]) * gr[u];
+                acc[t] += t >= tau ? e : 0.0f;
+            }
+        }
     }
 #pragma unroll
     for (int t = 0; t < kBT; ++t)
@@ -263,53 +303,70 @@ __global__ __launch_bounds__(256) void bwd_gy_kernel(const T* __restrict__ dY, c
 }
 
 // ---------------------------------------------------------------------------
+// Register-blocked accumulation shared by bwd_summary and bwd_dq:
+// acc[i][j] += a[8 mi + i] * b[8 di + j] for one token row of each operand.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void outer8(float (&acc)[8][8], const float* a, const float* b) {
+    const float4 a0 = ld4(a), a1 = ld4(a + 4), b0 = ld4(b), b1 = ld4(b + 4);
+    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] += av[i] * bv[j];
+}
+
+// ---------------------------------------------------------------------------
 // bwd_summary: chunk c's own terms of the reverse scan, relative to
 // Lpre = L at the last token of chunk c-1 (chunk 0 has none):
 //   a_c,m = sum_{t in c} w_tm g_t,  b_c,m = sum_{t in c} w_tm gz_tm,
 //   w_tm = e^{Lpre_m - L_tm} alpha_tm  (c_tm = alpha_tm gz_tm is stored).
 // a overwrites the chunk's starting numerator, b its starting den.
-// Thread (col = tid % 64, rg = tid / 64) owns a[m = rg + 4 r][d0 + col].
+// Thread (mi = tid % 32, di = tid / 32) owns a[8 mi .. +8][d0 + 8 di .. +8].
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_summary_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ L,
     const float* __restrict__ AL, const float* __restrict__ C, float* __restrict__ a_out,
     float* __restrict__ b_out) {
-    __shared__ float wl[kBT * 256];
-    __shared__ float gs[kBT * kBP];
+    __shared__ __attribute__((aligned(16))) float wl[kBT * 256];
+    __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     if (c == 0) return;
     const int b = bh / H, h = bh % H, tid = threadIdx.x;
-    const int t0 = c * kBT, nt = min(kBT, N - t0), d0 = blockIdx.z * kBSlab, ds = min(kBSlab, Dv - d0);
+    const int t0 = c * kBT, nt = min(kBT, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
     const float* lpre = L + rbase - M;
-    for (int e = tid; e < nt * M; e += kBNT) wl[e] = __expf(lpre[e % M] - L[rbase + e]) * AL[rbase + e];
-    stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
-    __syncthreads();
+    for (int e = tid; e < nt * M; e += kBNT) wl[e] = ex2(lpre[e % M] - L[rbase + e]) * AL[rbase + e];
     const size_t sbase = ((size_t)bh * NC + c) * M;
-    if (blockIdx.z == 0 && tid < M) {
+    if (tid < M) {
         float sum = 0.0f;
         for (int t = 0; t < nt; ++t) {
             const size_t o = rbase + (size_t)t * M + tid;
-            sum += __expf(lpre[tid] - L[o]) * C[o];
+            sum += ex2(lpre[tid] - L[o]) * C[o];
         }
         b_out[sbase + tid] = sum;
     }
-    const int col = tid & 63, rg = tid >> 6, rows = M >> 2;
-    float acc[64];
+    const int mi = tid & 31, di = tid >> 5;
+    const bool act = 8 * mi < M;
+    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+        const int ds = min(kBSlab, Dv - d0);
+        __syncthreads();
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
+        __syncthreads();
+        if (!act || 8 * di >= ds) continue;
+        float acc[8][8];
 #pragma unroll
-    for (int r = 0; r < 64; ++r) acc[r] = 0.0f;
-    for (int t = 0; t < nt; ++t) {
-        const float gval = gs[t * kBP + col];
-        const float* wr = wl + t * M + rg;
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int r = 0; r < 64; ++r)
-            if (r < rows) acc[r] += wr[4 * r] * gval;
-    }
-    if (col < ds) {
+            for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+        for (int t = 0; t < nt; ++t) outer8(acc, wl + t * M + 8 * mi, gs + t * kGT + 8 * di);
 #pragma unroll
-        for (int r = 0; r < 64; ++r)
-            if (r < rows) a_out[(sbase + rg + 4 * r) * Dv + d0 + col] = acc[r];
+        for (int i = 0; i < 8; ++i) {
+            float* dst = a_out + (sbase + 8 * mi + i) * Dv + d0 + 8 * di;
+            *reinterpret_cast<float4*>(dst) = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+        }
     }
 }
 
@@ -354,7 +411,7 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, f
             a4[si * D4 + j] = X;
             if (j == 0) bsum[si] = Y;
             if (c > 0) {
-                const float f = __expf(lv[i] - lnext);
+                const float f = ex2(lv[i] - lnext);
                 X.x = av[i].x + f * X.x;
                 X.y = av[i].y + f * X.y;
                 X.z = av[i].z + f * X.z;
@@ -368,28 +425,35 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, f
 
 // ---------------------------------------------------------------------------
 // bwd_dv: dv_tau = sum_{t >= tau} G[tau][t] g_t + sum_m e^{s_tau m - Lend_m} X_m,
-// G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm.  G is built over latent slabs
-// of 64 by thread (tau = tid / 4, t = 16 (tid % 4) + j); the output by thread
-// (col, rg) owning dv[tau = rg + 4 r][d0 + col].
+// G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm.  G covers the ten 16 x 16
+// blocks (ib <= jb) of the chunk: thread (u = tid % 16, v = tid / 16) owns
+// pair (16 ib + u, 16 jb + v) of each, over latent slabs of 64 staged in LDS.
+// The output is built per value slab by thread (col, rg) owning
+// dv[tau = rg + 4 r][d0 + col].
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ X, T* __restrict__ dV) {
-    __shared__ float ql[kBT * 256];       // slabs of s, L, alpha while G is built; then e^{s - Lend}
-    __shared__ float gl[kBT * kBP];       // G[tau][t]
-    __shared__ float gs[kBT * kBP];       // dY slab
+    __shared__ __attribute__((aligned(16))) float ql[kBT * 256];   // latent slabs, then e^{s - Lend}
+    __shared__ float gl[kBT * kBP];                                // G[tau][t]
+    __shared__ float gs[kBT * kBP];                                // dY slab
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x;
-    const int t0 = c * kBT, nt = min(kBT, N - t0), d0 = blockIdx.z * kBSlab, ds = min(kBSlab, Dv - d0);
+    const int t0 = c * kBT, nt = min(kBT, N - t0);
+    const bool carry = c + 1 < NC;
     const size_t rbase = ((size_t)bh * N + t0) * M;
     float* ss = ql;
-    float* ls = ql + kBT * kBP;
-    float* as = ql + 2 * kBT * kBP;
-    const int tau = tid >> 2, tq = (tid & 3) * 16;
-    float g[16];
+    float* ls = ql + kBT * kGT;
+    float* as = ql + 2 * kBT * kGT;
+    constexpr int kNB = 10;
+    constexpr int kIb[kNB] = {0, 0, 0, 0, 1, 1, 1, 2, 2, 3};
+    constexpr int kJb[kNB] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
+    const int u = tid & 15, v = tid >> 4;
+    for (int e = tid; e < kBT * kBP; e += kBNT) gl[e] = 0.0f;
+    float g[kNB];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) g[j] = 0.0f;
+    for (int k = 0; k < kNB; ++k) g[k] = 0.0f;
     for (int m0 = 0; m0 < M; m0 += 64) {
         const int mc = min(64, M - m0);
         __syncthreads();
@@ -397,50 +461,70 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
             const int i = e >> 6, mm = e & 63;
             const bool ok = i < nt && mm < mc;
             const size_t o = rbase + (size_t)i * M + m0 + mm;
-            ss[i * kBP + mm] = ok ? S[o] : kNegInf;
-            ls[i * kBP + mm] = ok ? L[o] : 0.0f;
-            as[i * kBP + mm] = ok ? AL[o] : 0.0f;
+            ss[i * kGT + mm] = ok ? S[o] : kNegInf;
+            ls[i * kGT + mm] = ok ? L[o] : __builtin_huge_valf();
+            as[i * kGT + mm] = ok ? AL[o] : 0.0f;
         }
         __syncthreads();
-        for (int mm = 0; mm < mc; ++mm) {
-            const float s = ss[tau * kBP + mm];
+        for (int mm = 0; mm < mc; mm += 4) {
+            float4 s4[4], l4[4], a4[4];
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const int t = tq + j;
-                if (t >= tau) g[j] += __expf(s - ls[t * kBP + mm]) * as[t * kBP + mm];
+            for (int q = 0; q < 4; ++q) {
+                s4[q] = ld4(ss + (16 * q + u) * kGT + mm);
+                l4[q] = ld4(ls + (16 * q + v) * kGT + mm);
+                a4[q] = ld4(as + (16 * q + v) * kGT + mm);
+            }
+#pragma unroll
+            for (int k = 0; k < kNB; ++k) {
+                const float4 sv = s4[kIb[k]], lv = l4[kJb[k]], av = a4[kJb[k]];
+                g[k] += ex2(sv.x - lv.x) * av.x + ex2(sv.y - lv.y) * av.y + ex2(sv.z - lv.z) * av.z +
+                        ex2(sv.w - lv.w) * av.w;
             }
         }
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gl[tau * kBP + tq + j] = (tq + j >= tau && tq + j < nt) ? g[j] : 0.0f;
+    for (int k = 0; k < kNB; ++k) {
+        const int tau = 16 * kIb[k] + u, t = 16 * kJb[k] + v;
+        gl[tau * kBP + t] = (t >= tau) ? g[k] : 0.0f;
+    }
     __syncthreads();
     // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token
-    const float* lend = L + rbase + (size_t)(nt - 1) * M;
-    for (int e = tid; e < nt * M; e += kBNT) ql[e] = __expf(S[rbase + e] - lend[e % M]);
-    stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
-    __syncthreads();
+    if (carry) {
+        const float* lend = L + rbase + (size_t)(nt - 1) * M;
+        for (int e = tid; e < nt * M; e += kBNT) ql[e] = ex2(S[rbase + e] - lend[e % M]);
+    }
     const int col = tid & 63, rg = tid >> 6;
-    float acc[16];
+    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+        const int ds = min(kBSlab, Dv - d0);
+        __syncthreads();
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
+        __syncthreads();
+        float acc[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    for (int t = 0; t < nt; ++t) {
-        const float gval = gs[t * kBP + col];
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        for (int t = 0; t < nt; ++t) {
+            const float gval = gs[t * kBP + col];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] += gl[(rg + 4 * r) * kBP + t] * gval;
-    }
-    if (c + 1 < NC && col < ds) {
-        const float* xr = X + ((size_t)bh * NC + c) * M * Dv + d0 + col;
-        for (int m = 0; m < M; ++m) {
-            const float xv = xr[(size_t)m * Dv];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += ql[(rg + 4 * r) * M + m] * xv;
+            for (int r = 0; r < 16; ++r) acc[r] += gl[(rg + 4 * r) * kBP + t] * gval;
         }
-    }
-    if (col < ds) {
+        if (carry && col < ds) {
+            const float* xr = X + ((size_t)bh * NC + c) * M * Dv + d0 + col;
+            for (int m = 0; m < M; m += 4) {
+                const float x0 = xr[(size_t)m * Dv], x1 = xr[(size_t)(m + 1) * Dv], x2 = xr[(size_t)(m + 2) * Dv],
+                            x3 = xr[(size_t)(m + 3) * Dv];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int tk = rg + 4 * r;
-            if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d0 + col] = from_f32<T>(acc[r]);
+                for (int r = 0; r < 16; ++r) {
+                    const float4 q4 = ld4(ql + (rg + 4 * r) * M + m);
+                    acc[r] += q4.x * x0 + q4.y * x1 + q4.z * x2 + q4.w * x3;
+                }
+            }
+        }
+        if (col < ds) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int tk = rg + 4 * r;
+                if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d0 + col] = from_f32<T>(acc[r]);
+            }
         }
     }
 }
@@ -448,17 +532,16 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 // ---------------------------------------------------------------------------
 // bwd_ds: ds_tau m = e^{s - Lend}(v_tau . X_m - Y_m)
 //                  + sum_{t >= tau} e^{s_tau m - L_tm}(alpha_tm GV[t][tau] - c_tm),
-// written over s.  Thread m; the later-chunk term is accumulated first in
-// registers (one per token of the chunk) and parked in DS until the in-chunk
-// sum is added.
+// written over s.  Thread m.  The later-chunk term is accumulated first and
+// parked in the chunk's L slots (L is held in registers from then on); the
+// pair sum runs per tau over 16-token blocks of t as in bwd_gz.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv, float* __restrict__ S,
-    const float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ C,
+    float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ C,
     const float* __restrict__ X, const float* __restrict__ Ysum) {
-    __shared__ float st[kBT * 256];
-    __shared__ float gvl[kBT * kBP];
+    __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     __shared__ float gs[kBT * kBP];
     __shared__ float vs[kBT * kBP];
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
@@ -467,7 +550,6 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const bool carry = c + 1 < NC;
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    for (int e = tid; e < nt * M; e += kBNT) st[e] = S[rbase + e];
     float gv[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
@@ -478,13 +560,13 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
-        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds);
-        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds);
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
         if (act && carry) {
             for (int d = 0; d < ds; d += 4) {
-                const float4 p = *reinterpret_cast<const float4*>(xr + d0 + d);
+                const float4 p = ld4(xr + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
                     const float* vr = vs + t * kBP + d;
@@ -493,33 +575,57 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
             }
         }
     }
-    gv_store(gv, gvl);
+    gv_store(gv, gvt);
     __syncthreads();
     if (!act) return;
+    float* scol = S + rbase + m;
+    float* lcol = L + rbase + m;
+    float lt[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) lt[t] = t < nt ? lcol[(size_t)t * M] : __builtin_huge_valf();
     if (carry) {
-        const float lend = L[rbase + (size_t)(nt - 1) * M + m];
+        const float lend = lcol[(size_t)(nt - 1) * M];
         const float ysum = Ysum[((size_t)bh * NC + c) * M + m];
 #pragma unroll
         for (int t = 0; t < kBT; ++t)
-            if (t < nt) S[rbase + (size_t)t * M + m] = __expf(st[t * M + m] - lend) * (acc[t] - ysum);
+            if (t < nt) lcol[(size_t)t * M] = ex2(scol[(size_t)t * M] - lend) * (acc[t] - ysum);
     }
-    float lt[kBT], at[kBT], ct[kBT];
+    float at[kBT], ct[kBT];
 #pragma unroll
     for (int t = 0; t < kBT; ++t) {
         const bool ok = t < nt;
-        const size_t o = rbase + (size_t)t * M + m;
-        lt[t] = ok ? L[o] : 0.0f;
-        at[t] = ok ? AL[o] : 0.0f;
-        ct[t] = ok ? C[o] : 0.0f;
+        at[t] = ok ? AL[rbase + (size_t)t * M + m] : 0.0f;
+        ct[t] = ok ? C[rbase + (size_t)t * M + m] : 0.0f;
     }
+    float sn = scol[0];
     for (int tau = 0; tau < nt; ++tau) {
-        const float s = st[tau * M + m];
+        const float s = sn;
+        if (tau + 1 < nt) sn = scol[(size_t)(tau + 1) * M];
+        const float* gr = gvt + tau * kGT;
+        const int tb0 = tau >> 4;
         float sum = 0.0f;
 #pragma unroll
-        for (int t = 0; t < kBT; ++t)
-            if (t >= tau && t < nt) sum += __expf(s - lt[t]) * (at[t] * gvl[t * kBP + tau] - ct[t]);
-        const size_t o = rbase + (size_t)tau * M + m;
-        S[o] = (carry ? S[o] : 0.0f) + sum;
+        for (int tb = 0; tb < kBT / 16; ++tb) {
+            if (tb == tb0) {
+#pragma unroll
+                for (int uu = 0; uu < 16; ++uu) {
+                    const int t = 16 * tb + uu;
+                    const float e = ex2(s - lt[t]) * (at[t] * gr[t] - ct[t]);
+                    sum += t >= tau ? e : 0.0f;
+                }
+            } else if (tb > tb0) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int t = 16 * tb + 4 * q;
+                    const float4 g4 = ld4(gr + t);
+                    sum += ex2(s - lt[t]) * (at[t] * g4.x - ct[t]) + ex2(s - lt[t + 1]) * (at[t + 1] * g4.y - ct[t + 1]) +
+                           ex2(s - lt[t + 2]) * (at[t + 2] * g4.z - ct[t + 2]) +
+                           ex2(s - lt[t + 3]) * (at[t + 3] * g4.w - ct[t + 3]);
+                }
+            }
+        }
+        const size_t o = (size_t)tau * M;
+        scol[o] = (carry ? lcol[o] : 0.0f) + sum;
     }
 }
 
@@ -578,23 +684,27 @@ __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
 // ---------------------------------------------------------------------------
 // bwd_dq: partial sums over a group of kBGroup tokens of
 //   P1_m = sum_t ds_tm k_t (+ da_tm qd_t when Kd = Q),  P2_m = sum_t da_tm qd_t.
-// grid (NG, BH, ceil(Dk/64)); thread (col, mg) owns m = mg + 4 r.
+// grid (NG, BH, ceil(Dk/64)); thread (mi = tid % 32, di = tid / 32) owns the
+// 8 x 8 tile m = 8 mi .., d = d0 + 8 di ..
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
     const T* __restrict__ K, const T* __restrict__ Qd, int N, int H, int M, int Dk, bool sep_k,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
     const float* __restrict__ gy, float* __restrict__ P1, float* __restrict__ P2) {
-    __shared__ float dsl[kBTok * 256];
-    __shared__ float dal[kBTok * 256];
-    __shared__ float kt[kBTok * 64];
-    __shared__ float qt[kBTok * 64];
+    __shared__ __attribute__((aligned(16))) float dsl[kBTok * 256];
+    __shared__ __attribute__((aligned(16))) float dal[kBTok * 256];
+    __shared__ __attribute__((aligned(16))) float kt[kBTok * kGT];
+    __shared__ __attribute__((aligned(16))) float qt[kBTok * kGT];
     const int g = blockIdx.x, NG = gridDim.x, bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
     const int d0 = blockIdx.z * 64;
-    const int col = tid & 63, mg = tid >> 6, rows = M >> 2;
-    float a1[64], a2[64];
+    const int mi = tid & 31, di = tid >> 5;
+    const bool act = 8 * mi < M && d0 + 8 * di < Dk;
+    float a1[8][8], a2[8][8];
 #pragma unroll
-    for (int r = 0; r < 64; ++r) a1[r] = a2[r] = 0.0f;
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a1[i][j] = a2[i][j] = 0.0f;
     const int tg0 = g * kBGroup, tg1 = min(N, tg0 + kBGroup);
     for (int t0 = tg0; t0 < tg1; t0 += kBTok) {
         const int nt = min(kBTok, tg1 - t0);
@@ -607,36 +717,32 @@ __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
             dal[e] = ok ? C[rbase + e] - AL[rbase + e] * gy[(size_t)bh * N + t0 + i] : 0.0f;
         }
         for (int e = tid; e < kBTok * 64; e += kBNT) {
-            const int i = e >> 6, d = d0 + (e & 63);
+            const int i = e >> 6, dd = e & 63, d = d0 + dd;
             const bool ok = i < nt && d < Dk;
             const size_t o = tok_index(b, t0 + i, h, N, H, Dk) + d;
-            kt[e] = ok ? to_f32(K[o]) : 0.0f;
-            qt[e] = ok ? to_f32(Qd[o]) : 0.0f;
+            kt[i * kGT + dd] = ok ? to_f32(K[o]) : 0.0f;
+            qt[i * kGT + dd] = ok ? to_f32(Qd[o]) : 0.0f;
         }
         __syncthreads();
-        for (int i = 0; i < nt; ++i) {
-            const float kv = kt[i * 64 + col], qv = qt[i * 64 + col];
-            const float* dr = dsl + i * M + mg;
-            const float* ar = dal + i * M + mg;
-#pragma unroll
-            for (int r = 0; r < 64; ++r) {
-                if (r < rows) {
-                    a1[r] += dr[4 * r] * kv;
-                    a2[r] += ar[4 * r] * qv;
-                }
+        if (act) {
+            for (int i = 0; i < nt; ++i) {
+                outer8(a1, dsl + i * M + 8 * mi, kt + i * kGT + 8 * di);
+                outer8(a2, dal + i * M + 8 * mi, qt + i * kGT + 8 * di);
             }
         }
     }
-    if (d0 + col >= Dk) return;
+    if (!act) return;
 #pragma unroll
-    for (int r = 0; r < 64; ++r) {
-        if (r >= rows) break;
-        const size_t o = (((size_t)bh * NG + g) * M + mg + 4 * r) * Dk + d0 + col;
-        if (sep_k) {
-            P1[o] = a1[r];
-            P2[o] = a2[r];
-        } else {
-            P1[o] = a1[r] + a2[r];
+    for (int i = 0; i < 8; ++i) {
+        const size_t o = (((size_t)bh * NG + g) * M + 8 * mi + i) * Dk + d0 + 8 * di;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (sep_k) {
+                P1[o + j] = a1[i][j];
+                P2[o + j] = a2[i][j];
+            } else {
+                P1[o + j] = a1[i][j] + a2[i][j];
+            }
         }
     }
 }
@@ -726,15 +832,14 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_gy_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, y, (int)N,
                        (int)H, (int)Dv, rows, gy);
     if ((rc = check_launch("bwd_gy_kernel"))) return rc;
-    const unsigned nslab = (unsigned)((Dv + kBSlab - 1) / kBSlab);
-    hipLaunchKernelGGL(bwd_summary_kernel<T>, dim3((unsigned)NC, (unsigned)BH, nslab), dim3(kBNT), 0, st, dy,
+    hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
                        (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
     if ((rc = check_launch("bwd_summary_kernel"))) return rc;
     const int64_t cthreads = BH * M * (Dv / 4);
     hipLaunchKernelGGL(bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, st, pn, pd, L,
                        (int)N, (int)NC, (int)M, (int)Dv, BH * M);
     if ((rc = check_launch("bwd_carry_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_dv_kernel<T>, dim3((unsigned)NC, (unsigned)BH, nslab), dim3(kBNT), 0, st, dy, (int)N,
+    hipLaunchKernelGGL(bwd_dv_kernel<T>, gc, dim3(kBNT), 0, st, dy, (int)N,
                        (int)H, (int)M, (int)Dv, S, L, AL, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, AL,
