@@ -184,6 +184,16 @@ def bench_others(torch, flare):
     dt = timed(lambda: flare.flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=64))
     out["config5_semi_ar"] = {"ms": dt * 1e3, "tok_s": 2 * 8192 / dt,
                               "tflops_alg": 6 * 128 * 64 * 2 * 8192 * 16 / dt / 1e12}
+    # backward (autograd through flare_autoregressive_triton) on configs 2 and 3
+    for name, shape, reps in (("config2_backward", (4, 4096, 16, 128, 64), 5),
+                              ("config3_backward", (1, 65536, 16, 256, 128), 3)):
+        q, k, v = (t.requires_grad_(True) for t in inputs(7, *shape))
+        y = flare.flare_autoregressive_triton(q, k, v)
+        dy = torch.randn_like(y)
+        dt = timed(lambda: y.backward(dy, retain_graph=True), reps)
+        B, N = shape[0], shape[1]
+        out[name] = {"ms": dt * 1e3, "tok_s": B * N / dt}
+        del q, k, v, y, dy
     return out
 
 

@@ -64,14 +64,16 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 
 // ---------------------------------------------------------------------------
 // bwd_stats: per chunk, scores s2 = s log2(e) (encoder), L2 = log2 of the
-// running den from the chunk's starting state, and the decoder weights alpha.
-// S and L hold log2-domain values so that every later factor is one exp2.
+// running den from the chunk's starting state, the decoder weights alpha and
+// LA = L2 - log2(alpha), so that e^{s_tau - L_t} alpha_t = exp2(s2_tau - LA_t).
+// S, L and LA hold log2-domain values: every later factor is one exp2.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ Qd, const T* __restrict__ Kd,
     int N, int H, int M, int Dk, float scale, bool shared, const float* __restrict__ pmax,
-    const float* __restrict__ pden, float* __restrict__ S, float* __restrict__ L, float* __restrict__ AL) {
+    const float* __restrict__ pden, float* __restrict__ S, float* __restrict__ L, float* __restrict__ AL,
+    float* __restrict__ LA) {
     __shared__ float kt[kBTok * 256];
     __shared__ float qdt[kBTok * 256];
     __shared__ float at[kBTok * 256];
@@ -97,6 +99,7 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
             if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
         }
         __syncthreads();
+        float lv[kBTok];
         if (act) {
             float as[kBTok], aa[kBTok];
 #pragma unroll
@@ -129,7 +132,8 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
                     mx = mn;
                     const size_t o = ((size_t)bh * N + t0 + i0 + i) * M + m;
                     S[o] = s2;
-                    L[o] = mx + __log2f(dn);
+                    lv[i] = mx + __log2f(dn);
+                    L[o] = lv[i];
                     at[i * M + m] = shared ? s : aa[i] * scale;
                 }
             }
@@ -149,8 +153,15 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
         }
         __syncthreads();
         if (act) {
-            for (int i = 0; i < ni; ++i)
-                AL[((size_t)bh * N + t0 + i0 + i) * M + m] = __expf(at[i * M + m] - lse[i]);
+#pragma unroll
+            for (int i = 0; i < kBTok; ++i) {
+                if (i < ni) {
+                    const size_t o = ((size_t)bh * N + t0 + i0 + i) * M + m;
+                    const float la = at[i * M + m] - lse[i];     // log alpha
+                    AL[o] = __expf(la);
+                    LA[o] = lv[i] - la * kBLog2e;
+                }
+            }
         }
     }
 }
@@ -425,27 +436,29 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, f
 
 // ---------------------------------------------------------------------------
 // bwd_dv: dv_tau = sum_{t >= tau} G[tau][t] g_t + sum_m e^{s_tau m - Lend_m} X_m,
-// G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm.  G covers the ten 16 x 16
-// blocks (ib <= jb) of the chunk: thread (u = tid % 16, v = tid / 16) owns
-// pair (16 ib + u, 16 jb + v) of each, over latent slabs of 64 staged in LDS.
-// The output is built per value slab by thread (col, rg) owning
-// dv[tau = rg + 4 r][d0 + col].
+// G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm = sum_m exp2(s2_tau m - LA_tm).
+// G covers the ten 16 x 16 blocks (ib <= jb) of the chunk: thread
+// (u = tid % 16, v = tid / 16) owns pair (16 ib + u, 16 jb + v) of each, over
+// latent slabs of 64 staged in LDS.  The output, for value slabs of 64
+// (Dv <= 512), is accumulated by thread (col, rg) owning
+// dv[tau = rg + 4 r][64 sl + col]; the X term runs over latent slabs of 64.
 // ---------------------------------------------------------------------------
+constexpr int kMaxVSlab = 8;
+
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ S,
-    const float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ X, T* __restrict__ dV) {
-    __shared__ __attribute__((aligned(16))) float ql[kBT * 256];   // latent slabs, then e^{s - Lend}
-    __shared__ float gl[kBT * kBP];                                // G[tau][t]
-    __shared__ float gs[kBT * kBP];                                // dY slab
+    const float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ X, T* __restrict__ dV) {
+    __shared__ __attribute__((aligned(16))) float uni[2 * kBT * kGT];   // s / LA latent slabs, then e^{s - Lend}
+    __shared__ float gl[kBT * kBP];                                      // G[tau][t]
+    __shared__ float gs[kBT * kBP];                                      // dY slab
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const bool carry = c + 1 < NC;
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    float* ss = ql;
-    float* ls = ql + kBT * kGT;
-    float* as = ql + 2 * kBT * kGT;
+    float* ss = uni;
+    float* ls = uni + kBT * kGT;
     constexpr int kNB = 10;
     constexpr int kIb[kNB] = {0, 0, 0, 0, 1, 1, 1, 2, 2, 3};
     constexpr int kJb[kNB] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
@@ -462,23 +475,20 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
             const bool ok = i < nt && mm < mc;
             const size_t o = rbase + (size_t)i * M + m0 + mm;
             ss[i * kGT + mm] = ok ? S[o] : kNegInf;
-            ls[i * kGT + mm] = ok ? L[o] : __builtin_huge_valf();
-            as[i * kGT + mm] = ok ? AL[o] : 0.0f;
+            ls[i * kGT + mm] = ok ? LA[o] : __builtin_huge_valf();
         }
         __syncthreads();
         for (int mm = 0; mm < mc; mm += 4) {
-            float4 s4[4], l4[4], a4[4];
+            float4 s4[4], l4[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 s4[q] = ld4(ss + (16 * q + u) * kGT + mm);
                 l4[q] = ld4(ls + (16 * q + v) * kGT + mm);
-                a4[q] = ld4(as + (16 * q + v) * kGT + mm);
             }
 #pragma unroll
             for (int k = 0; k < kNB; ++k) {
-                const float4 sv = s4[kIb[k]], lv = l4[kJb[k]], av = a4[kJb[k]];
-                g[k] += ex2(sv.x - lv.x) * av.x + ex2(sv.y - lv.y) * av.y + ex2(sv.z - lv.z) * av.z +
-                        ex2(sv.w - lv.w) * av.w;
+                const float4 sv = s4[kIb[k]], lv = l4[kJb[k]];
+                g[k] += ex2(sv.x - lv.x) + ex2(sv.y - lv.y) + ex2(sv.z - lv.z) + ex2(sv.w - lv.w);
             }
         }
     }
@@ -487,59 +497,80 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         const int tau = 16 * kIb[k] + u, t = 16 * kJb[k] + v;
         gl[tau * kBP + t] = (t >= tau) ? g[k] : 0.0f;
     }
-    __syncthreads();
-    // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token
-    if (carry) {
-        const float* lend = L + rbase + (size_t)(nt - 1) * M;
-        for (int e = tid; e < nt * M; e += kBNT) ql[e] = ex2(S[rbase + e] - lend[e % M]);
-    }
     const int col = tid & 63, rg = tid >> 6;
-    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
-        const int ds = min(kBSlab, Dv - d0);
-        __syncthreads();
-        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
-        __syncthreads();
-        float acc[16];
+    float acc[kMaxVSlab][16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int sl = 0; sl < kMaxVSlab; ++sl)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[sl][r] = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < kMaxVSlab; ++sl) {
+        if (sl * kBSlab >= Dv) break;
+        __syncthreads();
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, sl * kBSlab, min(kBSlab, Dv - sl * kBSlab), kBP);
+        __syncthreads();
         for (int t = 0; t < nt; ++t) {
             const float gval = gs[t * kBP + col];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += gl[(rg + 4 * r) * kBP + t] * gval;
+            for (int r = 0; r < 16; ++r) acc[sl][r] += gl[(rg + 4 * r) * kBP + t] * gval;
         }
-        if (carry && col < ds) {
-            const float* xr = X + ((size_t)bh * NC + c) * M * Dv + d0 + col;
-            for (int m = 0; m < M; m += 4) {
-                const float x0 = xr[(size_t)m * Dv], x1 = xr[(size_t)(m + 1) * Dv], x2 = xr[(size_t)(m + 2) * Dv],
-                            x3 = xr[(size_t)(m + 3) * Dv];
+    }
+    if (carry) {
+        // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token, per latent slab
+        const float* lend = L + rbase + (size_t)(nt - 1) * M;
+        const float* xb = X + ((size_t)bh * NC + c) * M * Dv;
+        for (int m0 = 0; m0 < M; m0 += 64) {
+            const int mc = min(64, M - m0);
+            __syncthreads();
+            for (int e = tid; e < kBT * 64; e += kBNT) {
+                const int i = e >> 6, mm = e & 63;
+                uni[i * kGT + mm] = (i < nt && mm < mc) ? ex2(S[rbase + (size_t)i * M + m0 + mm] - lend[m0 + mm]) : 0.0f;
+            }
+            __syncthreads();
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const float4 q4 = ld4(ql + (rg + 4 * r) * M + m);
-                    acc[r] += q4.x * x0 + q4.y * x1 + q4.z * x2 + q4.w * x3;
+            for (int sl = 0; sl < kMaxVSlab; ++sl) {
+                if (sl * kBSlab >= Dv) break;
+                if (sl * kBSlab + col >= Dv) continue;
+                const float* xr = xb + (size_t)m0 * Dv + sl * kBSlab + col;
+                for (int mm = 0; mm < mc; mm += 4) {
+                    const float x0 = xr[(size_t)mm * Dv], x1 = xr[(size_t)(mm + 1) * Dv],
+                                x2 = xr[(size_t)(mm + 2) * Dv], x3 = xr[(size_t)(mm + 3) * Dv];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const float4 q4 = ld4(uni + (rg + 4 * r) * kGT + mm);
+                        acc[sl][r] += q4.x * x0 + q4.y * x1 + q4.z * x2 + q4.w * x3;
+                    }
                 }
             }
         }
-        if (col < ds) {
+    }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int tk = rg + 4 * r;
-                if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d0 + col] = from_f32<T>(acc[r]);
-            }
+    for (int sl = 0; sl < kMaxVSlab; ++sl) {
+        if (sl * kBSlab >= Dv) break;
+        const int d = sl * kBSlab + col;
+        if (d >= Dv) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int tk = rg + 4 * r;
+            if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d] = from_f32<T>(acc[sl][r]);
         }
     }
 }
 
 // ---------------------------------------------------------------------------
 // bwd_ds: ds_tau m = e^{s - Lend}(v_tau . X_m - Y_m)
-//                  + sum_{t >= tau} e^{s_tau m - L_tm}(alpha_tm GV[t][tau] - c_tm),
-// written over s.  Thread m.  The later-chunk term is accumulated first and
-// parked in the chunk's L slots (L is held in registers from then on); the
-// pair sum runs per tau over 16-token blocks of t as in bwd_gz.
+//                  + sum_{t >= tau} e^{s_tau m - L_tm} alpha_tm GV[t][tau]
+//                  - e^{s_tau m - L_tau m} R_tau m,
+// R_tau = sum_{t >= tau} e^{L_tau - L_t} c_t = c_tau + e^{L_tau - L_tau+1} R_tau+1,
+// written over s.  Thread m.  The first and last terms are formed in one
+// reverse pass over the chunk and parked in the chunk's L slots (L is not
+// needed after this kernel); the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
+// runs per tau over 16-token blocks of t as in bwd_gz.
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv, float* __restrict__ S,
-    float* __restrict__ L, const float* __restrict__ AL, const float* __restrict__ C,
+    float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ C,
     const float* __restrict__ X, const float* __restrict__ Ysum) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     __shared__ float gs[kBT * kBP];
@@ -580,23 +611,25 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     if (!act) return;
     float* scol = S + rbase + m;
     float* lcol = L + rbase + m;
-    float lt[kBT];
+    const float* ccol = C + rbase + m;
+    const float lend = lcol[(size_t)(nt - 1) * M];
+    const float ysum = carry ? Ysum[((size_t)bh * NC + c) * M + m] : 0.0f;
+    float R = 0.0f, lnext = 0.0f;
 #pragma unroll
-    for (int t = 0; t < kBT; ++t) lt[t] = t < nt ? lcol[(size_t)t * M] : __builtin_huge_valf();
-    if (carry) {
-        const float lend = lcol[(size_t)(nt - 1) * M];
-        const float ysum = Ysum[((size_t)bh * NC + c) * M + m];
-#pragma unroll
-        for (int t = 0; t < kBT; ++t)
-            if (t < nt) lcol[(size_t)t * M] = ex2(scol[(size_t)t * M] - lend) * (acc[t] - ysum);
+    for (int t = kBT - 1; t >= 0; --t) {
+        if (t < nt) {
+            const size_t o = (size_t)t * M;
+            const float l = lcol[o], s = scol[o];
+            R = ccol[o] + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
+            lnext = l;
+            float park = -ex2(s - l) * R;
+            if (carry) park += ex2(s - lend) * (acc[t] - ysum);
+            lcol[o] = park;
+        }
     }
-    float at[kBT], ct[kBT];
+    float la[kBT];
 #pragma unroll
-    for (int t = 0; t < kBT; ++t) {
-        const bool ok = t < nt;
-        at[t] = ok ? AL[rbase + (size_t)t * M + m] : 0.0f;
-        ct[t] = ok ? C[rbase + (size_t)t * M + m] : 0.0f;
-    }
+    for (int t = 0; t < kBT; ++t) la[t] = t < nt ? LA[rbase + (size_t)t * M + m] : __builtin_huge_valf();
     float sn = scol[0];
     for (int tau = 0; tau < nt; ++tau) {
         const float s = sn;
@@ -610,7 +643,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 #pragma unroll
                 for (int uu = 0; uu < 16; ++uu) {
                     const int t = 16 * tb + uu;
-                    const float e = ex2(s - lt[t]) * (at[t] * gr[t] - ct[t]);
+                    const float e = ex2(s - la[t]) * gr[t];
                     sum += t >= tau ? e : 0.0f;
                 }
             } else if (tb > tb0) {
@@ -618,14 +651,13 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
                 for (int q = 0; q < 4; ++q) {
                     const int t = 16 * tb + 4 * q;
                     const float4 g4 = ld4(gr + t);
-                    sum += ex2(s - lt[t]) * (at[t] * g4.x - ct[t]) + ex2(s - lt[t + 1]) * (at[t + 1] * g4.y - ct[t + 1]) +
-                           ex2(s - lt[t + 2]) * (at[t + 2] * g4.z - ct[t + 2]) +
-                           ex2(s - lt[t + 3]) * (at[t + 3] * g4.w - ct[t + 3]);
+                    sum += ex2(s - la[t]) * g4.x + ex2(s - la[t + 1]) * g4.y + ex2(s - la[t + 2]) * g4.z +
+                           ex2(s - la[t + 3]) * g4.w;
                 }
             }
         }
         const size_t o = (size_t)tau * M;
-        scol[o] = (carry ? lcol[o] : 0.0f) + sum;
+        scol[o] = lcol[o] + sum;
     }
 }
 
@@ -765,7 +797,7 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 struct BwdLayout {
     int64_t NC, NG;
-    size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_c, off_gy, off_p1, off_p2, total;
+    size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_la, off_c, off_gy, off_p1, off_p2, total;
     BwdLayout(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
         NC = (N + kBT - 1) / kBT;
         NG = (N + kBGroup - 1) / kBGroup;
@@ -782,6 +814,7 @@ struct BwdLayout {
         off_s = take(BH * N * M);
         off_l = take(BH * N * M);
         off_al = take(BH * N * M);
+        off_la = take(BH * N * M);
         off_c = take(BH * N * M);
         off_gy = take(BH * N);
         off_p1 = take(BH * NG * M * Dk);
@@ -803,6 +836,7 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     float* S = reinterpret_cast<float*>(ws + lay.off_s);
     float* L = reinterpret_cast<float*>(ws + lay.off_l);
     float* AL = reinterpret_cast<float*>(ws + lay.off_al);
+    float* LA = reinterpret_cast<float*>(ws + lay.off_la);
     float* C = reinterpret_cast<float*>(ws + lay.off_c);
     float* gy = reinterpret_cast<float*>(ws + lay.off_gy);
     float* P1 = reinterpret_cast<float*>(ws + lay.off_p1);
@@ -823,7 +857,7 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
         return rc;
     const dim3 gc((unsigned)NC, (unsigned)BH);
     hipLaunchKernelGGL(bwd_stats_kernel<T>, gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M, (int)Dk,
-                       scale, shared, pm, pd, S, L, AL);
+                       scale, shared, pm, pd, S, L, AL, LA);
     if ((rc = check_launch("bwd_stats_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
                        L, AL, C);
@@ -840,9 +874,9 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
                        (int)N, (int)NC, (int)M, (int)Dv, BH * M);
     if ((rc = check_launch("bwd_carry_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_dv_kernel<T>, gc, dim3(kBNT), 0, st, dy, (int)N,
-                       (int)H, (int)M, (int)Dv, S, L, AL, pn, static_cast<T*>(dV));
+                       (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, AL,
+    hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kBTok - 1) / kBTok), (unsigned)BH), dim3(kBNT), 0,
