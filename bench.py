@@ -166,8 +166,9 @@ def bench_others(torch, flare):
         q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16).cuda()
         return q, torch.randn(B, N, H, D).to(torch.bfloat16).cuda(), torch.randn(B, N, H, D).to(torch.bfloat16).cuda()
 
-    def timed(fn, reps=20):
-        fn()
+    def timed(fn, reps=20, warm=1):
+        for _ in range(warm):
+            fn()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(reps):
@@ -190,7 +191,7 @@ def bench_others(torch, flare):
         q, k, v = (t.requires_grad_(True) for t in inputs(7, *shape))
         y = flare.flare_autoregressive_triton(q, k, v)
         dy = torch.randn_like(y)
-        dt = timed(lambda: y.backward(dy, retain_graph=True), reps)
+        dt = timed(lambda: y.backward(dy, retain_graph=True), reps, warm=2)
         B, N = shape[0], shape[1]
         out[name] = {"ms": dt * 1e3, "tok_s": B * N / dt}
         del q, k, v, y, dy
