@@ -21,6 +21,7 @@ HEADER_FUNCTIONS = (
     "flare_chunk_prefix",
     "flare_chunk_output",
     "flare_ar_forward_workspace_size",
+    "flare_ar_forward_workspace_size_sep",
     "flare_ar_forward",
     "flare_ar_forward_masked",
     "flare_ar_default_chunk",
@@ -56,6 +57,8 @@ def _declare(lib):
     lib.flare_chunk_output.argtypes = [_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 3 + [_vp, _i, _vp, _vp]
     lib.flare_ar_forward_workspace_size.restype = _sz
     lib.flare_ar_forward_workspace_size.argtypes = [_i64] * 6
+    lib.flare_ar_forward_workspace_size_sep.restype = _sz
+    lib.flare_ar_forward_workspace_size_sep.argtypes = [_i64] * 6
     lib.flare_ar_default_chunk.restype = _i64
     lib.flare_ar_default_chunk.argtypes = [_i64] * 5
     lib.flare_ar_forward_masked.restype = _i

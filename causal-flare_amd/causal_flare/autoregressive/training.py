@@ -95,7 +95,9 @@ def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
     fin_ptrs = (P(fin["m"]), P(fin["d"]), P(fin["u"])) if fin else (None, None, None)
     NC = (N + chunk - 1) // chunk
     if timings is None or token_mask is not None:
-        nbytes = lib.flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk)
+        size_fn = (lib.flare_ar_forward_workspace_size if qd is None and kd is None
+                   else lib.flare_ar_forward_workspace_size_sep)
+        nbytes = size_fn(B, N, H, M, Dv, chunk)
         ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
         if token_mask is None:
             rc = lib.flare_ar_forward(P(q), P(k), P(v), P(qd), P(kd), code, B, N, H, M, Dk, Dv,

@@ -383,12 +383,24 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
                          int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
                          const float* pden, const float* pnum, void* Y, int out_dtype,
-                         float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr) {
+                         float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr,
+                         void* alpha_ws = nullptr) {
     const bool shared = Qdec == nullptr && Kdec == nullptr;
-    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr &&
-        mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled()))
-        return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
-                                  tmask, stream);
+    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr) {
+        if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled()))
+            return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
+                                      tmask, stream);
+        // separate decoder tensors: the decoder softmax first (alpha_ws, [B*H, N, M] fp16),
+        // then the producer/consumer kernel reading it
+        if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
+            mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
+            const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, tmask,
+                                                alpha_ws, stream);
+            if (rc) return rc;
+            return launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask,
+                                    alpha_ws, stream);
+        }
+    }
     const int DT = pick_dt(M, Dv);
     FLARE_REQUIRE(DT > 0, "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
                   (long long)M, (long long)Dv);
@@ -503,12 +515,25 @@ int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64
     return default_chunk(B, N, H, M, Dv);
 }
 
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bytes of the chunk summaries (max, den, num), each 256-byte aligned.
+static size_t summary_bytes(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t chunk) {
+    const int64_t NC = (N + chunk - 1) / chunk;
+    const size_t per = (size_t)B * H * NC * M;
+    return 2 * align256(per * sizeof(float)) + align256(per * Dv * sizeof(float));
+}
+
 size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                        int64_t chunk) {
     if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
-    const int64_t NC = (N + chunk - 1) / chunk;
-    const size_t per = (size_t)B * H * NC * M;
-    return sizeof(float) * (per * 2 + per * Dv) + 3 * 256;
+    return summary_bytes(B, N, H, M, Dv, chunk);
+}
+
+size_t flare_ar_forward_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                           int64_t chunk) {
+    if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
+    return summary_bytes(B, N, H, M, Dv, chunk) + align256((size_t)B * H * N * M * 2);
 }
 
 int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
@@ -535,6 +560,10 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
         set_error("ar_forward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
         return FLARE_ERR_WORKSPACE;
     }
+    // room for the decoder softmax of separate decoder tensors (MFMA path)
+    void* alpha_ws = nullptr;
+    if ((Qdec || Kdec) && workspace_bytes >= flare_ar_forward_workspace_size_sep(B, N, H, M, Dv, chunk))
+        alpha_ws = (char*)workspace + summary_bytes(B, N, H, M, Dv, chunk);
     const int64_t NC = (N + chunk - 1) / chunk;
     const size_t per = (size_t)B * H * NC * M;
     char* ws = (char*)workspace;
@@ -548,7 +577,7 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
     rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
-                         cnum, Y, out_dtype, nullptr, s, token_mask);
+                         cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws);
 }
 
 }  // extern "C"

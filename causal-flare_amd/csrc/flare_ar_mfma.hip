@@ -796,7 +796,8 @@ int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, i
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
                        hipStream_t stream) {
     if (output_pc_enabled())
-        return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, stream);
+        return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, nullptr,
+                                stream);
     FLARE_REQUIRE(tmask == nullptr, "chunk_output_mfma: token masks need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);
     const int64_t NC = (N + chunk - 1) / chunk;

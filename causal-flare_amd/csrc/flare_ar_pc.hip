@@ -64,11 +64,15 @@ struct PCLayout {
     static_assert(DC % 16 == 0, "value columns per consumer must be a multiple of 16");
 };
 
-template <int M, int D, int NPW>
+// SEP: separate decoder weights.  alpha [B*H, N, M] (fp16) then holds the
+// decoder softmax, written by decoder_alpha_mfma; the producers read it in place
+// of the token softmax of the shared scores (no meeting, no factorised p).
+template <int M, int D, int NPW, bool SEP>
 __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
-    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, const int32_t* __restrict__ tmask) {
+    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, const int32_t* __restrict__ tmask,
+    const f16* __restrict__ alpha) {
     using L = PCLayout<M, D, NPW>;
     // K rows of the even / odd subtiles (swizzled); two arrays rather than one so
     // that reads of one never wait on the DMA that fills the other
@@ -185,6 +189,20 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                         keep[ti] = t >= t_end || tmask[(size_t)b * N + t] != 0;
                     }
                 }
+                // decoder weights of this lane's tokens and latents (separate decoder only),
+                // issued before the DMA for the same reason as the mask
+                f16x4 af[L::MTP][2];
+                if constexpr (SEP) {
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        const int t = t0 + 16 * ti + c;
+                        const bool ok = t < t_end;
+                        const f16* arow = alpha + ((size_t)bh * N + (ok ? t : t0)) * M + mp0 + 4 * g;
+#pragma unroll
+                        for (int mi = 0; mi < L::MTP; ++mi)
+                            af[mi][ti] = ok ? load4<f16x4>(arow + 16 * mi) : f16x4{0, 0, 0, 0};
+                    }
+                }
                 if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
                 // ---- raw scores A = Q K^T for this wave's latents (S = scale2 A):
                 //      acc[mi][ti][r] = A[t = 16 ti + c][m = 16 mi + 4 g + r], -inf for invalid tokens
@@ -236,14 +254,16 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                         dnbig |= R[mi][r] == kNegInf;   // no reference yet (fully masked so far): general path
                     }
                 // token max over this wave's latents (log2 units; -inf for invalid tokens)
-                float lm[2];
+                float lm[2] = {0.0f, 0.0f};
+                if constexpr (!SEP) {
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    float mx = kNegInf;
+                    for (int ti = 0; ti < 2; ++ti) {
+                        float mx = kNegInf;
 #pragma unroll
-                    for (int mi = 0; mi < L::MTP; ++mi)
-                        mx = fmaxf(mx, fmaxf(fmaxf(acc[mi][ti][0], acc[mi][ti][1]), fmaxf(acc[mi][ti][2], acc[mi][ti][3])));
-                    lm[ti] = rows_max4(mx) * scale2;
+                        for (int mi = 0; mi < L::MTP; ++mi)
+                            mx = fmaxf(mx, fmaxf(fmaxf(acc[mi][ti][0], acc[mi][ti][1]), fmaxf(acc[mi][ti][2], acc[mi][ti][3])));
+                        lm[ti] = rows_max4(mx) * scale2;
+                    }
                 }
                 const bool moved = __any((emax > L::kLazyE) | dnbig);
                 if (moved) {
@@ -282,61 +302,63 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                 }
                 // The factorised decoder weight p = E 2^(R - Rmax) 2^(Rmax - lm) needs
                 // Rmax - lm in the fp32 range; else (extreme spreads) p = 2^(S - lm) directly.
-                const bool slow = moved || __any((lm[0] > kNegInf) & (Rmax - lm[0] > L::kFactorMax)) ||
-                                  __any((lm[1] > kNegInf) & (Rmax - lm[1] > L::kFactorMax));
-                float bt[2];
+                const bool slow = SEP ? moved
+                                      : moved || __any((lm[0] > kNegInf) & (Rmax - lm[0] > L::kFactorMax)) ||
+                                            __any((lm[1] > kNegInf) & (Rmax - lm[1] > L::kFactorMax));
+                float bt[2] = {0.0f, 0.0f}, fw[2] = {0.0f, 0.0f};
+                if constexpr (!SEP) {
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti) bt[ti] = lm[ti] == kNegInf ? 0.0f : exp2f_fast(Rmax - lm[ti]);
-                // ---- the token softmax over all M latents: each producer publishes (lm_w, sum_m p)
-                //      per token, the four meet at an LDS counter, and each folds
-                //      f_w(t) = 2^(lm_w - lse_t) into its own weights (alpha = p f_w)
-                {
-                    float lsum[2] = {0.0f, 0.0f};
-                    if (!slow) {
+                    for (int ti = 0; ti < 2; ++ti) bt[ti] = lm[ti] == kNegInf ? 0.0f : exp2f_fast(Rmax - lm[ti]);
+                    // ---- the token softmax over all M latents: each producer publishes (lm_w, sum_m p)
+                    //      per token, the four meet at an LDS counter, and each folds
+                    //      f_w(t) = 2^(lm_w - lse_t) into its own weights (alpha = p f_w)
+                    {
+                        float lsum[2] = {0.0f, 0.0f};
+                        if (!slow) {
 #pragma unroll
-                        for (int mi = 0; mi < L::MTP; ++mi) {
-                            const f32x4 ar = *reinterpret_cast<const f32x4*>(arl + mp0 + 16 * mi + 4 * g);
+                            for (int mi = 0; mi < L::MTP; ++mi) {
+                                const f32x4 ar = *reinterpret_cast<const f32x4*>(arl + mp0 + 16 * mi + 4 * g);
 #pragma unroll
-                            for (int ti = 0; ti < 2; ++ti)
+                                for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                                for (int r = 0; r < 4; ++r) lsum[ti] = fmaf(e[mi][ti][r], ar[r], lsum[ti]);
-                        }
-                        lsum[0] *= bt[0];
-                        lsum[1] *= bt[1];
-                    } else {
-#pragma unroll
-                        for (int mi = 0; mi < L::MTP; ++mi)
-#pragma unroll
-                            for (int ti = 0; ti < 2; ++ti) {
-                                const f32x4 sc = scores(mi, ti);
-#pragma unroll
-                                for (int r = 0; r < 4; ++r)
-                                    lsum[ti] += lm[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[r], scale2, -lm[ti]));
+                                    for (int r = 0; r < 4; ++r) lsum[ti] = fmaf(e[mi][ti][r], ar[r], lsum[ti]);
                             }
+                            lsum[0] *= bt[0];
+                            lsum[1] *= bt[1];
+                        } else {
+#pragma unroll
+                            for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                                for (int ti = 0; ti < 2; ++ti) {
+                                    const f32x4 sc = scores(mi, ti);
+#pragma unroll
+                                    for (int r = 0; r < 4; ++r)
+                                        lsum[ti] += lm[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[r], scale2, -lm[ti]));
+                                }
+                        }
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) {
+                            const float l = rows_sum4(lsum[ti]);
+                            if (g == 0) lsep[buf][w * T + 16 * ti + c] = float2{lm[ti], l};
+                        }
                     }
+                    meet(j + 1);
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
-                        const float l = rows_sum4(lsum[ti]);
-                        if (g == 0) lsep[buf][w * T + 16 * ti + c] = float2{lm[ti], l};
+                        const int t = 16 * ti + c;
+                        float2 pr[L::NP];
+                        float mm = kNegInf;
+#pragma unroll
+                        for (int w2 = 0; w2 < L::NP; ++w2) {
+                            pr[w2] = lsep[buf][w2 * T + t];
+                            mm = fmaxf(mm, pr[w2].x);
+                        }
+                        float ss = 0.0f;
+#pragma unroll
+                        for (int w2 = 0; w2 < L::NP; ++w2) ss += pr[w2].y * exp2f_fast(pr[w2].x - mm);
+                        fw[ti] = (lm[ti] == kNegInf) ? 0.0f : exp2f_fast(lm[ti] - mm) * __builtin_amdgcn_rcpf(ss);
+                        bt[ti] *= fw[ti];
                     }
-                }
-                meet(j + 1);
-                float fw[2];
-#pragma unroll
-                for (int ti = 0; ti < 2; ++ti) {
-                    const int t = 16 * ti + c;
-                    float2 pr[L::NP];
-                    float mm = kNegInf;
-#pragma unroll
-                    for (int w2 = 0; w2 < L::NP; ++w2) {
-                        pr[w2] = lsep[buf][w2 * T + t];
-                        mm = fmaxf(mm, pr[w2].x);
-                    }
-                    float ss = 0.0f;
-#pragma unroll
-                    for (int w2 = 0; w2 < L::NP; ++w2) ss += pr[w2].y * exp2f_fast(pr[w2].x - mm);
-                    fw[ti] = (lm[ti] == kNegInf) ? 0.0f : exp2f_fast(lm[ti] - mm) * __builtin_amdgcn_rcpf(ss);
-                    bt[ti] *= fw[ti];
                 }
                 f16* et = etl[buf];
                 f16* wq = wl[buf];
@@ -378,7 +400,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                                 float q[4];
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) {
-                                    const float p = e[mi][ti][r] * (ar[r] * bt[ti]);     // alpha
+                                    const float p = SEP ? (float)af[mi][ti][r] : e[mi][ti][r] * (ar[r] * bt[ti]);   // alpha
                                     q[r] = p * __builtin_amdgcn_rcpf(dcum[ti][r]);
                                 }
                                 split_f16x4(q, whi[jb][ti], wlo[jb][ti]);
@@ -433,7 +455,8 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) {
                                     const float dt = dn[mi][r] + dcum[ti][r];
-                                    const float p = lm[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[ti][r], scale2, -lm[ti])) * fw[ti];
+                                    const float p = SEP ? (float)af[mi][ti][r]
+                                                        : lm[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[ti][r], scale2, -lm[ti])) * fw[ti];
                                     q[r] = dt > 0.0f ? p / dt : 0.0f;
                                     w1[r] = (f16)(moved ? q[r] * dn[mi][r] : q[r]);
                                 }
@@ -927,23 +950,118 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decoder weights for separate decoder tensors (reference flare_chunk_decoder_lse,
+// training.py:1106-1188, and the exp(a - lse) of flare_chunk_fwd):
+//   alpha[bh][t][m] = softmax over m of scale qd_t . kd_m   (fp16; 0 for a masked token).
+// grid (ceil(N / 128), B*H), 4 waves; wave w takes tokens 32 w .. 32 w + 31 of the
+// block, with Kd rows as the A operand and the token rows as B.
+// ---------------------------------------------------------------------------
+template <int M, int D>
+__global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict__ Qd, const bf16* __restrict__ Kd,
+                                                          int N, int H, float scale2,
+                                                          const int32_t* __restrict__ tmask, f16* __restrict__ alpha) {
+    constexpr int MT = M / 16, KS = D / 32;
+    const int bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 15, g = lane >> 4;
+    const int tb = blockIdx.x * 128 + 32 * w;
+    bf16x8 bq[2][KS];
+    bool valid[2];
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        const int t = tb + 16 * ti + c;
+        valid[ti] = t < N && (tmask == nullptr || tmask[(size_t)b * N + t] != 0);
+        const bf16* row = Qd + (((size_t)b * N + min(t, N - 1)) * H + h) * D;
+#pragma unroll
+        for (int kq = 0; kq < KS; ++kq) bq[ti][kq] = t < N ? load8<bf16x8>(row + 32 * kq + 8 * g) : zero8();
+    }
+    f32x4 acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        acc[mt][0] = acc[mt][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kq = 0; kq < KS; ++kq) {
+            const bf16x8 a = load8<bf16x8>(Kd + ((size_t)h * M + 16 * mt + c) * D + 32 * kq + 8 * g);
+            acc[mt][0] = mma(a, bq[0][kq], acc[mt][0]);
+            acc[mt][1] = mma(a, bq[1][kq], acc[mt][1]);
+        }
+    }
+    // acc[mt][ti][r] = a[m = 16 mt + 4 g + r][t = tb + 16 ti + c]
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[mt][ti][r] *= scale2;
+                mx = fmaxf(mx, acc[mt][ti][r]);
+            }
+        mx = rows_max4(mx);
+        float sum = 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[mt][ti][r] = exp2f_fast(acc[mt][ti][r] - mx);
+                sum += acc[mt][ti][r];
+            }
+        sum = rows_sum4(sum);
+        const float inv = valid[ti] ? 1.0f / sum : 0.0f;
+        const int t = tb + 16 * ti + c;
+        if (t < N) {
+            f16* dst = alpha + ((size_t)bh * N + t) * M + 4 * g;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                f16x4 o;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[r] = (f16)(acc[mt][ti][r] * inv);
+                *reinterpret_cast<f16x4*>(dst + 16 * mt) = o;
+            }
+        }
+    }
+}
+
 }  // namespace mfma
 
 using namespace mfma;
 
+int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
+                         float scale, const int32_t* tmask, void* alpha, hipStream_t stream) {
+    FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
+                  "decoder_alpha_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * H));
+    const float s2 = scale * kLog2e;
+#define FLARE_DEC_ALPHA(MM, DD)                                                                          \
+    hipLaunchKernelGGL((decoder_alpha_mfma<MM, DD>), grid, dim3(256), 0, stream, (const bf16*)Qd,         \
+                       (const bf16*)Kd, (int)N, (int)H, s2, tmask, (f16*)alpha)
+    if (M == 128 && D == 64) FLARE_DEC_ALPHA(128, 64);
+    else if (M == 128 && D == 128) FLARE_DEC_ALPHA(128, 128);
+    else if (M == 256 && D == 64) FLARE_DEC_ALPHA(256, 64);
+    else FLARE_DEC_ALPHA(256, 128);
+#undef FLARE_DEC_ALPHA
+    return check_launch("decoder_alpha_mfma");
+}
+
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
-                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, hipStream_t stream) {
+                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
+                     hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_OUT_PC(MM, DD, NW)                                                                         \
-    hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
-                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y, \
-                       out_dtype, tmask)
+#define FLARE_OUT_PC_SEP(MM, DD, NW, SP)                                                                     \
+    hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW, SP>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
+                       (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y,    \
+                       out_dtype, tmask, (const f16*)alpha)
+#define FLARE_OUT_PC(MM, DD, NW)                   \
+    do {                                           \
+        if (alpha) FLARE_OUT_PC_SEP(MM, DD, NW, true);  \
+        else FLARE_OUT_PC_SEP(MM, DD, NW, false);       \
+    } while (0)
     // The 128 x 64 bank runs 2 + 2 waves (72 KiB of LDS: two workgroups share a CU);
     // the larger banks 4 + 4 (one workgroup fills a CU).
     if (M == 128 && D == 64) FLARE_OUT_PC(128, 64, 2);
@@ -951,6 +1069,7 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
     else if (M == 256 && D == 64) FLARE_OUT_PC(256, 64, 4);
     else FLARE_OUT_PC(256, 128, 4);
 #undef FLARE_OUT_PC
+#undef FLARE_OUT_PC_SEP
     return check_launch("chunk_output_pc");
 }
 

@@ -45,9 +45,14 @@ inline bool output_pc_enabled() {
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, hipStream_t stream);
+// alpha: NULL for shared decoder weights; else the decoder softmax [B*H, N, M]
+// (fp16) written by launch_decoder_alpha, for separate Qdec / Kdec.
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
-                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, hipStream_t stream);
+                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
+                     hipStream_t stream);
+int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
+                         float scale, const int32_t* tmask, void* alpha, hipStream_t stream);
 }  // namespace flare
 
 namespace flare {

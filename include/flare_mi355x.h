@@ -85,6 +85,16 @@ int flare_chunk_output(const void* Q, const void* K, const void* V, const void* 
 /* Bytes of fp32 workspace flare_ar_forward needs (chunk summaries). */
 size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                        int64_t chunk);
+/*
+ * Workspace for separate decoder tensors (Qdec / Kdec given): the chunk
+ * summaries plus the decoder softmax [B*H, N, M] (fp16), which the bf16 MFMA
+ * path computes first, as the reference's flare_chunk_decoder_lse does
+ * (training.py:1106-1188).  Given a smaller workspace (at least
+ * flare_ar_forward_workspace_size), flare_ar_forward runs separate decoder
+ * tensors on the scalar-fp32 kernels.
+ */
+size_t flare_ar_forward_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                           int64_t chunk);
 
 /*
  * Whole chunked forward / prefill: phases 1-3 on one stream.  `chunk` <= 0

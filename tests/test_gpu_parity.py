@@ -351,6 +351,47 @@ def test_mfma_shapes_bf16(M, D, N, chunk):
     assert_parity(y, ref, torch.bfloat16, f"mfma M={M} D={D} N={N} chunk={chunk}")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (128, 128), (256, 64), (256, 128)])
+@pytest.mark.parametrize("mode", ["sep_q", "sep_k", "both"])
+def test_mfma_separate_decoder_bf16(M, D, mode):
+    """Separate decoder tensors on the MFMA path: the decoder softmax from its own
+    MFMA pass, read by the producer waves (ragged N, several chunks)."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_sep_decoder", M, D, mode)
+    B, N, H = 2, 1000, 2
+    q, k, v = seeded(41 + M + D, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(M + D)
+    qd = torch.randn(B, N, H, D, generator=g).bfloat16() if mode in ("sep_q", "both") else None
+    kd = (torch.randn(H, M, D, generator=g) * D ** -0.5).bfloat16() if mode in ("sep_k", "both") else None
+    dev = lambda t: None if t is None else t.to(DEV)
+    for chunk in (None, 64):
+        y = flare_autoregressive_triton(dev(q), dev(k), dev(v), chunk_size=chunk, Q_dec=dev(qd), K_dec=dev(kd))
+        ref = O.ar_chunked(q, k, v, Q_dec=qd, K_dec=kd, nthreads=16)
+        assert_parity(y, ref, torch.bfloat16, f"mfma sep decoder M={M} D={D} {mode} chunk={chunk}")
+
+
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_masked_prefill_separate_decoder_bf16(M, D):
+    """Masked prefill with separate decoder tensors (MFMA path): masked tokens get
+    decoder weights 0 and y = 0, and leave the state unchanged."""
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("masked_prefill_sep", M, D)
+    B, T, H = 2, 700, 2
+    q, k, v = seeded(13 + M, B, T, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(3)
+    qd = torch.randn(B, T, H, D, generator=g).bfloat16()
+    kd = (torch.randn(H, M, D, generator=g) * D ** -0.5).bfloat16()
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[:, :40] = 0
+    mask[1, 300:333] = 0
+    y, st = flare_autoregressive_prefill_triton(q.to(DEV), k.to(DEV), v.to(DEV), attention_mask=mask.to(DEV),
+                                                Q_dec=qd.to(DEV), K_dec=kd.to(DEV))
+    y_ref, st_ref = O.ar_recurrent(q, k, v, attention_mask=mask, Q_dec=qd, K_dec=kd, nthreads=16)
+    assert torch.all(y[mask == 0].float() == 0), "masked tokens must give y = 0"
+    assert_parity(y, y_ref, torch.bfloat16, f"masked prefill sep decoder M={M} D={D}")
+    assert_state_parity(st, st_ref, torch.bfloat16, "masked prefill sep decoder")
+
+
 @pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
 def test_mfma_large_values_bf16(M, D):
     """Values far outside fp16 (|v| up to 1e5, also at a chunk start) on the MFMA
