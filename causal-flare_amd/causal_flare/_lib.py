@@ -29,6 +29,7 @@ HEADER_FUNCTIONS = (
     "flare_ar_backward",
     "flare_decode_step",
     "flare_semi_ar_workspace_size",
+    "flare_semi_ar_workspace_size_sep",
     "flare_semi_ar_forward",
 )
 
@@ -75,6 +76,8 @@ def _declare(lib):
     lib.flare_decode_step.argtypes = [_vp] * 6 + [_i] + [_i64] * 5 + [_f] + [_vp] * 3 + [_vp, _i, _vp]
     lib.flare_semi_ar_workspace_size.restype = _sz
     lib.flare_semi_ar_workspace_size.argtypes = [_i64] * 6
+    lib.flare_semi_ar_workspace_size_sep.restype = _sz
+    lib.flare_semi_ar_workspace_size_sep.argtypes = [_i64] * 6
     lib.flare_semi_ar_forward.restype = _i
     lib.flare_semi_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp, _i, _vp, _vp]
                                           + [_vp, _sz, _vp])

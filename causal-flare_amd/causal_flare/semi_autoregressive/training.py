@@ -79,7 +79,9 @@ def _semi_autoregressive_forward(Q, K, V, *, block_size, chunk_size, scale=None,
     lse_dec = torch.empty((B, H, N), device=device, dtype=torch.float32)
     lse_enc = torch.empty((B, H, NB, M), device=device, dtype=torch.float32)
     lib = _lib.lib()
-    nbytes = lib.flare_semi_ar_workspace_size(B, N, H, M, D_value, block_size)
+    size_fn = (lib.flare_semi_ar_workspace_size if qd is None and kd is None
+               else lib.flare_semi_ar_workspace_size_sep)
+    nbytes = size_fn(B, N, H, M, D_value, block_size)
     ws = torch.empty(max(nbytes, 1), device=device, dtype=torch.uint8)
     P = _lib.ptr
     launch = lambda: lib.flare_semi_ar_forward(

@@ -395,7 +395,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
         if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
             mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
             const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, tmask,
-                                                alpha_ws, stream);
+                                                alpha_ws, nullptr, stream);
             if (rc) return rc;
             return launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask,
                                     alpha_ws, stream);

@@ -953,14 +953,16 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 // ---------------------------------------------------------------------------
 // Decoder weights for separate decoder tensors (reference flare_chunk_decoder_lse,
 // training.py:1106-1188, and the exp(a - lse) of flare_chunk_fwd):
-//   alpha[bh][t][m] = softmax over m of scale qd_t . kd_m   (fp16; 0 for a masked token).
+//   alpha[bh][t][m] = softmax over m of scale qd_t . kd_m   (fp16; 0 for a masked token),
+// and, when lse is given, LSE_dec[bh][t] = log sum_m exp(scale qd_t . kd_m).
 // grid (ceil(N / 128), B*H), 4 waves; wave w takes tokens 32 w .. 32 w + 31 of the
 // block, with Kd rows as the A operand and the token rows as B.
 // ---------------------------------------------------------------------------
 template <int M, int D>
 __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict__ Qd, const bf16* __restrict__ Kd,
                                                           int N, int H, float scale2,
-                                                          const int32_t* __restrict__ tmask, f16* __restrict__ alpha) {
+                                                          const int32_t* __restrict__ tmask, f16* __restrict__ alpha,
+                                                          float* __restrict__ lse) {
     constexpr int MT = M / 16, KS = D / 32;
     const int bh = blockIdx.y, b = bh / H, h = bh % H;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, c = lane & 15, g = lane >> 4;
@@ -1009,6 +1011,7 @@ __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict
         sum = rows_sum4(sum);
         const float inv = valid[ti] ? 1.0f / sum : 0.0f;
         const int t = tb + 16 * ti + c;
+        if (lse != nullptr && g == 0 && t < N) lse[(size_t)bh * N + t] = valid[ti] ? (mx + __log2f(sum)) * kLn2 : kNegInf;
         if (t < N) {
             f16* dst = alpha + ((size_t)bh * N + t) * M + 4 * g;
 #pragma unroll
@@ -1027,14 +1030,14 @@ __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict
 using namespace mfma;
 
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
-                         float scale, const int32_t* tmask, void* alpha, hipStream_t stream) {
+                         float scale, const int32_t* tmask, void* alpha, float* lse, hipStream_t stream) {
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "decoder_alpha_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * H));
     const float s2 = scale * kLog2e;
 #define FLARE_DEC_ALPHA(MM, DD)                                                                          \
     hipLaunchKernelGGL((decoder_alpha_mfma<MM, DD>), grid, dim3(256), 0, stream, (const bf16*)Qd,         \
-                       (const bf16*)Kd, (int)N, (int)H, s2, tmask, (f16*)alpha)
+                       (const bf16*)Kd, (int)N, (int)H, s2, tmask, (f16*)alpha, lse)
     if (M == 128 && D == 64) FLARE_DEC_ALPHA(128, 64);
     else if (M == 128 && D == 128) FLARE_DEC_ALPHA(128, 128);
     else if (M == 256 && D == 64) FLARE_DEC_ALPHA(256, 64);

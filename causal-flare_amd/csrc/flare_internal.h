@@ -52,7 +52,7 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
                      hipStream_t stream);
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
-                         float scale, const int32_t* tmask, void* alpha, hipStream_t stream);
+                         float scale, const int32_t* tmask, void* alpha, float* lse, hipStream_t stream);
 }  // namespace flare
 
 namespace flare {
@@ -60,7 +60,7 @@ bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, hipStream_t stream);
+                            float* lse_dec, float* lse_enc, const void* alpha, hipStream_t stream);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);

@@ -133,6 +133,13 @@ size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, 
     return sizeof(float) * (per * 2 + per * Dv) + 3 * 256;
 }
 
+size_t flare_semi_ar_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                        int64_t block) {
+    if (block <= 0) return 0;
+    const size_t base = (flare_semi_ar_workspace_size(B, N, H, M, Dv, block) + 255) & ~(size_t)255;
+    return base + (((size_t)B * H * N * M * 2 + 255) & ~(size_t)255);
+}
+
 int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
                           const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H,
                           int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,
@@ -158,8 +165,18 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
     float* bnum = (float*)(ws + 2 * align(per * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
     const bool shared = Qdec == nullptr && Kdec == nullptr;
-    if ((mfma_phase_mask() & 3) == 3 && mfma_semi_supported(dtype, out_dtype, shared, M, Dk, Dv, block) &&
-        mfma_prepare_supported(dtype, M, Dk, Dv)) {
+    // separate decoder tensors take the MFMA path when the workspace has room for
+    // their softmax (flare_semi_ar_workspace_size_sep)
+    void* alpha_ws = nullptr;
+    if (!shared && workspace_bytes >= flare_semi_ar_workspace_size_sep(B, N, H, M, Dv, block))
+        alpha_ws = ws + ((need + 255) & ~(size_t)255);
+    if ((mfma_phase_mask() & 3) == 3 && (shared || alpha_ws) &&
+        mfma_semi_supported(dtype, out_dtype, true, M, Dk, Dv, block) && mfma_prepare_supported(dtype, M, Dk, Dv)) {
+        if (alpha_ws) {
+            const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, nullptr,
+                                                alpha_ws, lse_dec, s);
+            if (rc) return rc;
+        }
         // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
         // block-causal MFMA readout.  The summaries fit in the workspace since
         // chunks are never shorter than blocks.
@@ -176,7 +193,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                                   nullptr, nullptr, s);
         if (rc) return rc;
         return launch_semi_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, block, bmax, bden, bnum, Y,
-                                       out_dtype, lse_dec, lse_enc, s);
+                                       out_dtype, lse_dec, lse_enc, alpha_ws, s);
     }
     int rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, block, bmax, bden, bnum, s);
     if (rc) return rc;

@@ -41,12 +41,14 @@ struct SemiLayout {
     static_assert(MT % 2 == 0 && DW % 16 == 0, "unsupported wave split");
 };
 
-template <int M, int D, int NW, int NSUB>
+// SEP: separate decoder tensors; alpha [B*H, N, M] (fp16, from decoder_alpha_mfma,
+// which also writes LSE_dec) replaces the softmax of the shared scores.
+template <int M, int D, int NW, int NSUB, bool SEP>
 __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, float* __restrict__ lse_dec,
-    float* __restrict__ lse_enc) {
+    float* __restrict__ lse_enc, const f16* __restrict__ alpha) {
     using L = SemiLayout<M, D, NW, NSUB>;
     __shared__ __attribute__((aligned(16))) f16 al[NSUB * T * L::AP];   // alpha[t][m] of the block
     __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];         // E^T[m][tau]
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
             if (lane == 0) moved[w] = wave_moved ? 1 : 0;
             // ---- decoder log-sum-exp partials per token
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti) {
+            for (int ti = 0; ti < (SEP ? 0 : 2); ++ti) {
                 float lm = kNegInf;
 #pragma unroll
                 for (int mi = 0; mi < L::MT; ++mi)
@@ -180,9 +182,21 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                 }
             }
             __syncthreads();   // S1: lse partials, E^T, rescale factors, moved flags visible
-            // ---- alpha = softmax over the bank (fp16 -> LDS), LSE_dec
+            // ---- alpha = softmax over the bank (fp16 -> LDS), LSE_dec; separate decoder
+            //      tensors: alpha copied from the decoder pass
+            if constexpr (SEP) {
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti) {
+                for (int ti = 0; ti < 2; ++ti) {
+                    const int t = 16 * ti + c;
+                    const f16* arow = alpha + ((size_t)bh * N + t0 + t) * M + mw0 + 4 * g;
+#pragma unroll
+                    for (int mi = 0; mi < L::MT; ++mi)
+                        *reinterpret_cast<f16x4*>(al + (j * T + t) * L::AP + mw0 + 16 * mi + 4 * g) =
+                            load4<f16x4>(arow + 16 * mi);
+                }
+            }
+#pragma unroll
+            for (int ti = 0; ti < (SEP ? 0 : 2); ++ti) {
                 const int t = 16 * ti + c;
                 float mm = kNegInf;
 #pragma unroll
@@ -336,6 +350,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 
 using namespace mfma;
 
+// shared: true also for separate decoder tensors served through decoder_alpha_mfma
 bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv,
                          int64_t block) {
     if (!(dtype == FLARE_BF16 && shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256) &&
@@ -347,15 +362,20 @@ bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, hipStream_t stream) {
+                            float* lse_dec, float* lse_enc, const void* alpha, hipStream_t stream) {
     FLARE_REQUIRE(chunk % block == 0 && N % block == 0, "semi_output_mfma: chunk and N must be whole blocks");
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_SEMI_MFMA(MM, DD, NWW, NS)                                                                   \
-    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS>), grid, dim3(64 * NWW), 0, stream,              \
+#define FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, SP)                                                           \
+    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS, SP>), grid, dim3(64 * NWW), 0, stream,          \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk,     \
-                       pmax, pden, pnum, Y, out_dtype, lse_dec, lse_enc)
+                       pmax, pden, pnum, Y, out_dtype, lse_dec, lse_enc, (const f16*)alpha)
+#define FLARE_SEMI_MFMA(MM, DD, NWW, NS)                              \
+    do {                                                             \
+        if (alpha) FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, true);       \
+        else FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, false);            \
+    } while (0)
 #define FLARE_SEMI_BLOCKS(MM, DD, NWW)                       \
     if (block == 32) FLARE_SEMI_MFMA(MM, DD, NWW, 1);        \
     else FLARE_SEMI_MFMA(MM, DD, NWW, 2);
@@ -372,6 +392,7 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
     }
 #undef FLARE_SEMI_BLOCKS
 #undef FLARE_SEMI_MFMA
+#undef FLARE_SEMI_MFMA_SEP
     return check_launch("semi_output_mfma");
 }
 

@@ -168,6 +168,10 @@ int flare_decode_step(const void* Q, const void* K, const void* V, const void* Q
  */
 size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                     int64_t block);
+/* As flare_ar_forward_workspace_size_sep: room for the decoder softmax of separate
+ * decoder tensors, which then run on the bf16 MFMA path. */
+size_t flare_semi_ar_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
+                                        int64_t block);
 int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
                           const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H,
                           int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,

@@ -314,6 +314,27 @@ def test_semi_ar_decoder_variants_bf16():
             assert_parity(aux["LSE_enc"], lse_enc, torch.bfloat16, "semi LSE_enc")
 
 
+@pytest.mark.parametrize("M,D,block", [(128, 64, 64), (256, 128, 32)])
+@pytest.mark.parametrize("mode", ["sep_q", "sep_k", "both"])
+def test_semi_ar_separate_decoder_mfma_bf16(M, D, block, mode):
+    """Separate decoder tensors on the block-causal MFMA readout (decoder softmax
+    and LSE_dec from the decoder pass)."""
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_sep_mfma", M, D, block, mode)
+    B, N, H = 2, 1024, 2
+    q, k, v = seeded(61 + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(D)
+    qd = torch.randn(B, N, H, D, generator=g).bfloat16() if mode in ("sep_q", "both") else None
+    kd = (torch.randn(H, M, D, generator=g) * D ** -0.5).bfloat16() if mode in ("sep_k", "both") else None
+    dev = lambda t: None if t is None else t.to(DEV)
+    y, aux = flare_semi_autoregressive_trition(dev(q), dev(k), dev(v), block_size=block, chunk_size=block,
+                                               Q_dec=dev(qd), K_dec=dev(kd))
+    y_ref, lse_dec, lse_enc = O.semi_ar(q, k, v, block, block, Q_dec=qd, K_dec=kd)
+    assert_parity(y, y_ref, torch.bfloat16, f"semi sep M={M} D={D} {mode}")
+    assert_parity(aux["LSE_dec"], lse_dec, torch.bfloat16, "semi sep LSE_dec")
+    assert_parity(aux["LSE_enc"], lse_enc, torch.bfloat16, "semi sep LSE_enc")
+
+
 def test_cfg5_semi_ar_bf16():
     """B=2, N=8192, H=16, M=128, D=64, block 64, bf16, seed 4."""
     from causal_flare import flare_semi_autoregressive_trition
