@@ -44,7 +44,7 @@
 
 namespace flare {
 
-constexpr int kBT = 64;        // tokens per backward chunk
+constexpr int kBT = 32;        // tokens per backward chunk
 constexpr int kBNT = 256;      // threads per workgroup; thread m owns latent m (M <= 256)
 constexpr int kBSlab = 64;     // value / key columns per LDS slab
 constexpr int kBP = 65;        // padded pitch of [64][64] LDS tiles
@@ -169,8 +169,8 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
 // ---------------------------------------------------------------------------
 // Shared by bwd_gz and bwd_ds: GV[t][tau] = g_t . v_tau over one chunk, from
 // column slabs staged in LDS, kept transposed (gvt[tau][t], pitch kGT) so that
-// a row of t values is read 16 bytes at a time.  Thread (t = tid / 4,
-// tau = 16 (tid % 4) + j).
+// a row of t values is read 16 bytes at a time.  Thread (t = tid / kGVQ,
+// tau = kGVJ (tid % kGVQ) + j) owns kGVJ entries.
 // ---------------------------------------------------------------------------
 template <typename T>
 __device__ __forceinline__ void stage_slab(float* dst, const T* __restrict__ src, int b, int t0, int nt, int h,
@@ -181,19 +181,22 @@ __device__ __forceinline__ void stage_slab(float* dst, const T* __restrict__ src
     }
 }
 
-__device__ __forceinline__ void gv_accumulate(float (&gv)[16], const float* gs, const float* vs, int ds) {
-    const int t = threadIdx.x >> 2, tq = (threadIdx.x & 3) * 16;
+constexpr int kGVJ = kBT * kBT / kBNT;   // GV entries per thread
+constexpr int kGVQ = kBT / kGVJ;         // threads per GV row
+
+__device__ __forceinline__ void gv_accumulate(float (&gv)[kGVJ], const float* gs, const float* vs, int ds) {
+    const int t = threadIdx.x / kGVQ, tq = (threadIdx.x % kGVQ) * kGVJ;
     for (int d = 0; d < ds; ++d) {
         const float gval = gs[t * kBP + d];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) gv[j] += gval * vs[(tq + j) * kBP + d];
+        for (int j = 0; j < kGVJ; ++j) gv[j] += gval * vs[(tq + j) * kBP + d];
     }
 }
 
-__device__ __forceinline__ void gv_store(const float (&gv)[16], float* gvt) {
-    const int t = threadIdx.x >> 2, tq = (threadIdx.x & 3) * 16;
+__device__ __forceinline__ void gv_store(const float (&gv)[kGVJ], float* gvt) {
+    const int t = threadIdx.x / kGVQ, tq = (threadIdx.x % kGVQ) * kGVJ;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gvt[(tq + j) * kGT + t] = gv[j];
+    for (int j = 0; j < kGVJ; ++j) gvt[(tq + j) * kGT + t] = gv[j];
 }
 
 // ---------------------------------------------------------------------------
@@ -217,9 +220,9 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const bool act = m < M;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    float gv[16];
+    float gv[kGVJ];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
+    for (int j = 0; j < kGVJ; ++j) gv[j] = 0.0f;
     float acc[kBT];
 #pragma unroll
     for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
@@ -437,13 +440,30 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, f
 // ---------------------------------------------------------------------------
 // bwd_dv: dv_tau = sum_{t >= tau} G[tau][t] g_t + sum_m e^{s_tau m - Lend_m} X_m,
 // G[tau][t] = sum_m e^{s_tau m - L_tm} alpha_tm = sum_m exp2(s2_tau m - LA_tm).
-// G covers the ten 16 x 16 blocks (ib <= jb) of the chunk: thread
+// G covers the causal 16 x 16 blocks (ib <= jb) of the chunk: thread
 // (u = tid % 16, v = tid / 16) owns pair (16 ib + u, 16 jb + v) of each, over
 // latent slabs of 64 staged in LDS.  The output, for value slabs of 64
 // (Dv <= 512), is accumulated by thread (col, rg) owning
 // dv[tau = rg + 4 r][64 sl + col]; the X term runs over latent slabs of 64.
 // ---------------------------------------------------------------------------
 constexpr int kMaxVSlab = 8;
+constexpr int kTB = kBT / 16;                         // 16-token blocks per chunk
+constexpr int kBlockPairs = kTB * (kTB + 1) / 2;      // causal block pairs (ib <= jb)
+constexpr int kRT = kBT / 4;                          // output tokens per thread
+struct BlockPairs {
+    int ib[kBlockPairs], jb[kBlockPairs];
+};
+constexpr BlockPairs block_pairs() {
+    BlockPairs p{};
+    int k = 0;
+    for (int i = 0; i < kTB; ++i)
+        for (int j = i; j < kTB; ++j) {
+            p.ib[k] = i;
+            p.jb[k] = j;
+            ++k;
+        }
+    return p;
+}
 
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
@@ -459,9 +479,8 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     const size_t rbase = ((size_t)bh * N + t0) * M;
     float* ss = uni;
     float* ls = uni + kBT * kGT;
-    constexpr int kNB = 10;
-    constexpr int kIb[kNB] = {0, 0, 0, 0, 1, 1, 1, 2, 2, 3};
-    constexpr int kJb[kNB] = {0, 1, 2, 3, 1, 2, 3, 2, 3, 3};
+    constexpr BlockPairs kP = block_pairs();
+    constexpr int kNB = kBlockPairs;
     const int u = tid & 15, v = tid >> 4;
     for (int e = tid; e < kBT * kBP; e += kBNT) gl[e] = 0.0f;
     float g[kNB];
@@ -479,30 +498,30 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         }
         __syncthreads();
         for (int mm = 0; mm < mc; mm += 4) {
-            float4 s4[4], l4[4];
+            float4 s4[kTB], l4[kTB];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kTB; ++q) {
                 s4[q] = ld4(ss + (16 * q + u) * kGT + mm);
                 l4[q] = ld4(ls + (16 * q + v) * kGT + mm);
             }
 #pragma unroll
             for (int k = 0; k < kNB; ++k) {
-                const float4 sv = s4[kIb[k]], lv = l4[kJb[k]];
+                const float4 sv = s4[kP.ib[k]], lv = l4[kP.jb[k]];
                 g[k] += ex2(sv.x - lv.x) + ex2(sv.y - lv.y) + ex2(sv.z - lv.z) + ex2(sv.w - lv.w);
             }
         }
     }
 #pragma unroll
     for (int k = 0; k < kNB; ++k) {
-        const int tau = 16 * kIb[k] + u, t = 16 * kJb[k] + v;
+        const int tau = 16 * kP.ib[k] + u, t = 16 * kP.jb[k] + v;
         gl[tau * kBP + t] = (t >= tau) ? g[k] : 0.0f;
     }
     const int col = tid & 63, rg = tid >> 6;
-    float acc[kMaxVSlab][16];
+    float acc[kMaxVSlab][kRT];
 #pragma unroll
     for (int sl = 0; sl < kMaxVSlab; ++sl)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[sl][r] = 0.0f;
+        for (int r = 0; r < kRT; ++r) acc[sl][r] = 0.0f;
 #pragma unroll
     for (int sl = 0; sl < kMaxVSlab; ++sl) {
         if (sl * kBSlab >= Dv) break;
@@ -512,7 +531,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         for (int t = 0; t < nt; ++t) {
             const float gval = gs[t * kBP + col];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[sl][r] += gl[(rg + 4 * r) * kBP + t] * gval;
+            for (int r = 0; r < kRT; ++r) acc[sl][r] += gl[(rg + 4 * r) * kBP + t] * gval;
         }
     }
     if (carry) {
@@ -536,7 +555,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
                     const float x0 = xr[(size_t)mm * Dv], x1 = xr[(size_t)(mm + 1) * Dv],
                                 x2 = xr[(size_t)(mm + 2) * Dv], x3 = xr[(size_t)(mm + 3) * Dv];
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
+                    for (int r = 0; r < kRT; ++r) {
                         const float4 q4 = ld4(uni + (rg + 4 * r) * kGT + mm);
                         acc[sl][r] += q4.x * x0 + q4.y * x1 + q4.z * x2 + q4.w * x3;
                     }
@@ -550,7 +569,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         const int d = sl * kBSlab + col;
         if (d >= Dv) continue;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < kRT; ++r) {
             const int tk = rg + 4 * r;
             if (tk < nt) dV[tok_index(b, t0 + tk, h, N, H, Dv) + d] = from_f32<T>(acc[sl][r]);
         }
@@ -581,9 +600,9 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const bool carry = c + 1 < NC;
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    float gv[16];
+    float gv[kGVJ];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) gv[j] = 0.0f;
+    for (int j = 0; j < kGVJ; ++j) gv[j] = 0.0f;
     float acc[kBT];
 #pragma unroll
     for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
