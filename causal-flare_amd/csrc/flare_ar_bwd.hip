@@ -186,10 +186,13 @@ constexpr int kGVQ = kBT / kGVJ;         // threads per GV row
 
 __device__ __forceinline__ void gv_accumulate(float (&gv)[kGVJ], const float* gs, const float* vs, int ds) {
     const int t = threadIdx.x / kGVQ, tq = (threadIdx.x % kGVQ) * kGVJ;
-    for (int d = 0; d < ds; ++d) {
-        const float gval = gs[t * kBP + d];
+    for (int d = 0; d < ds; d += 4) {
+        const float4 g4 = ld4(gs + t * kGT + d);
 #pragma unroll
-        for (int j = 0; j < kGVJ; ++j) gv[j] += gval * vs[(tq + j) * kBP + d];
+        for (int j = 0; j < kGVJ; ++j) {
+            const float4 v4 = ld4(vs + (tq + j) * kGT + d);
+            gv[j] += g4.x * v4.x + g4.y * v4.y + g4.z * v4.z + g4.w * v4.w;
+        }
     }
 }
 
@@ -213,8 +216,8 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const float* __restrict__ pmax, const float* __restrict__ pnum, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ AL, float* __restrict__ C) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
-    __shared__ float gs[kBT * kBP];
-    __shared__ float vs[kBT * kBP];
+    __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
+    __shared__ __attribute__((aligned(16))) float vs[kBT * kGT];
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
@@ -230,8 +233,8 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
-        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
-        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
         if (act) {
@@ -239,8 +242,8 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
                 const float4 p = ld4(pu + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
-                    const float* gr = gs + t * kBP + d;
-                    acc[t] += gr[0] * p.x + gr[1] * p.y + gr[2] * p.z + gr[3] * p.w;
+                    const float4 g4 = ld4(gs + t * kGT + d);
+                    acc[t] += g4.x * p.x + g4.y * p.y + g4.z * p.z + g4.w * p.w;
                 }
             }
         }
@@ -470,7 +473,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ X, T* __restrict__ dV) {
     __shared__ __attribute__((aligned(16))) float uni[2 * kBT * kGT];   // s / LA latent slabs, then e^{s - Lend}
-    __shared__ float gl[kBT * kBP];                                      // G[tau][t]
+    __shared__ __attribute__((aligned(16))) float gl[kBT * kGT];        // G[tau][t]
     __shared__ float gs[kBT * kBP];                                      // dY slab
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x;
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     constexpr BlockPairs kP = block_pairs();
     constexpr int kNB = kBlockPairs;
     const int u = tid & 15, v = tid >> 4;
-    for (int e = tid; e < kBT * kBP; e += kBNT) gl[e] = 0.0f;
+    for (int e = tid; e < kBT * kGT; e += kBNT) gl[e] = 0.0f;
     float g[kNB];
 #pragma unroll
     for (int k = 0; k < kNB; ++k) g[k] = 0.0f;
@@ -514,7 +517,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 #pragma unroll
     for (int k = 0; k < kNB; ++k) {
         const int tau = 16 * kP.ib[k] + u, t = 16 * kP.jb[k] + v;
-        gl[tau * kBP + t] = (t >= tau) ? g[k] : 0.0f;
+        gl[tau * kGT + t] = (t >= tau) ? g[k] : 0.0f;
     }
     const int col = tid & 63, rg = tid >> 6;
     float acc[kMaxVSlab][kRT];
@@ -528,10 +531,15 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         __syncthreads();
         stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, sl * kBSlab, min(kBSlab, Dv - sl * kBSlab), kBP);
         __syncthreads();
-        for (int t = 0; t < nt; ++t) {
-            const float gval = gs[t * kBP + col];
+        // G rows are zero past nt and gs rows are zero-filled, so whole groups of 4 tokens are safe
+        for (int t = 0; t < nt; t += 4) {
+            const float g0 = gs[t * kBP + col], g1 = gs[(t + 1) * kBP + col], g2 = gs[(t + 2) * kBP + col],
+                        g3 = gs[(t + 3) * kBP + col];
 #pragma unroll
-            for (int r = 0; r < kRT; ++r) acc[sl][r] += gl[(rg + 4 * r) * kBP + t] * gval;
+            for (int r = 0; r < kRT; ++r) {
+                const float4 q4 = ld4(gl + (rg + 4 * r) * kGT + t);
+                acc[sl][r] += q4.x * g0 + q4.y * g1 + q4.z * g2 + q4.w * g3;
+            }
         }
     }
     if (carry) {
@@ -592,8 +600,8 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ C,
     const float* __restrict__ X, const float* __restrict__ Ysum) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
-    __shared__ float gs[kBT * kBP];
-    __shared__ float vs[kBT * kBP];
+    __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
+    __shared__ __attribute__((aligned(16))) float vs[kBT * kGT];
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
@@ -610,8 +618,8 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
-        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
-        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kBP);
+        stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
+        stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
         if (act && carry) {
@@ -619,8 +627,8 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
                 const float4 p = ld4(xr + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
-                    const float* vr = vs + t * kBP + d;
-                    acc[t] += vr[0] * p.x + vr[1] * p.y + vr[2] * p.z + vr[3] * p.w;
+                    const float4 v4 = ld4(vs + t * kGT + d);
+                    acc[t] += v4.x * p.x + v4.y * p.y + v4.z * p.z + v4.w * p.w;
                 }
             }
         }
