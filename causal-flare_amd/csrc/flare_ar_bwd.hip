@@ -34,7 +34,7 @@
 //   bwd_carry    reverse scan over chunks -> X_c, Y_c     grid (BH M Dv/4)
 //   bwd_dv       dV                                        grid (NC, BH)
 //   bwd_ds       ds (written over s)                      grid (NC, BH)
-//   bwd_dk       dK, dQ_dec per token                     grid (N/16, BH)
+//   bwd_dk       dK, dQ_dec per token                     grid (N/32, BH)
 //   bwd_dq       dQ, dK_dec partial sums per token group  grid (NG, BH, Dk/64)
 //   bwd_reduce   sum of the partials over (b, group)
 #include <stdio.h>
@@ -691,19 +691,21 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 // ---------------------------------------------------------------------------
 // bwd_dk: per token, dK_t = scale sum_m (ds_tm Q_m [+ da_tm Kd_m when Qd = K])
 // and dQd_t = scale sum_m da_tm Kd_m (separate Qd); da_tm = c_tm - alpha_tm gy_t.
-// Thread (col, tg) owns tokens tg + 4 r (r < 4) and columns col + 64 k.
+// Thread (col, tg) owns tokens tg + 4 r (r < kDkTok / 4) and columns col + 64 k.
 // ---------------------------------------------------------------------------
+constexpr int kDkTok = 32;     // tokens per bwd_dk workgroup
+
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
     const T* __restrict__ Q, const T* __restrict__ Kd, int N, int H, int M, int Dk, float scale, bool sep_q,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
     const float* __restrict__ gy, T* __restrict__ dK, T* __restrict__ dQd) {
-    __shared__ float dsl[kBTok * 256];
-    __shared__ float dal[kBTok * 256];
+    __shared__ __attribute__((aligned(16))) float dsl[kDkTok * 256];
+    __shared__ __attribute__((aligned(16))) float dal[kDkTok * 256];
     const int bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
-    const int t0 = blockIdx.x * kBTok, nt = min(kBTok, N - t0);
+    const int t0 = blockIdx.x * kDkTok, nt = min(kDkTok, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
-    for (int e = tid; e < kBTok * M; e += kBNT) {
+    for (int e = tid; e < kDkTok * M; e += kBNT) {
         const int i = e / M;
         const bool ok = i < nt;
         dsl[e] = ok ? DS[rbase + e] : 0.0f;
@@ -711,22 +713,30 @@ __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
     }
     __syncthreads();
     const int col = tid & 63, tg = tid >> 6;
+    constexpr int R = kDkTok / 4;
     for (int d0 = 0; d0 < Dk; d0 += 64) {
         const int d = d0 + col;
         if (d >= Dk) break;
-        float ak[4] = {0.f, 0.f, 0.f, 0.f}, aq[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int m = 0; m < M; ++m) {
-            const float qv = to_f32(Q[((size_t)h * M + m) * Dk + d]);
-            const float kv = to_f32(Kd[((size_t)h * M + m) * Dk + d]);
+        float ak[R], aq[R];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < R; ++r) ak[r] = aq[r] = 0.0f;
+        const T* qc = Q + (size_t)h * M * Dk + d;
+        const T* kc = Kd + (size_t)h * M * Dk + d;
+        for (int m = 0; m < M; m += 4) {
+            const float q0 = to_f32(qc[(size_t)m * Dk]), q1 = to_f32(qc[(size_t)(m + 1) * Dk]),
+                        q2 = to_f32(qc[(size_t)(m + 2) * Dk]), q3 = to_f32(qc[(size_t)(m + 3) * Dk]);
+            const float k0 = to_f32(kc[(size_t)m * Dk]), k1 = to_f32(kc[(size_t)(m + 1) * Dk]),
+                        k2 = to_f32(kc[(size_t)(m + 2) * Dk]), k3 = to_f32(kc[(size_t)(m + 3) * Dk]);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
                 const int i = tg + 4 * r;
-                ak[r] += dsl[i * M + m] * qv;
-                aq[r] += dal[i * M + m] * kv;
+                const float4 s4 = ld4(dsl + i * M + m), a4 = ld4(dal + i * M + m);
+                ak[r] += s4.x * q0 + s4.y * q1 + s4.z * q2 + s4.w * q3;
+                aq[r] += a4.x * k0 + a4.y * k1 + a4.z * k2 + a4.w * k3;
             }
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < R; ++r) {
             const int i = tg + 4 * r;
             if (i >= nt) continue;
             const size_t o = tok_index(b, t0 + i, h, N, H, Dk) + d;
@@ -906,7 +916,7 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kBTok - 1) / kBTok), (unsigned)BH), dim3(kBNT), 0,
+    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT), 0,
                        st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, S, AL, C, gy,
                        static_cast<T*>(dK), static_cast<T*>(dQd));
     if ((rc = check_launch("bwd_dk_kernel"))) return rc;
