@@ -3,11 +3,12 @@
 Same public names as the reference package (``causal_flare/__init__.py:1-27``).
 Every compute call runs hand-written HIP kernels for gfx950 from
 ``_lib/libflare_mi355x.so``; there is no CPU fallback.  Out of scope here and
-raising ``NotImplementedError``: backward passes, ``flare_recurrent_triton``
-and the semi-autoregressive prefill/decode stubs (stubs in the reference too).
+raising ``NotImplementedError``: the semi-autoregressive prefill/decode stubs
+(stubs in the reference too).
 """
 from . import autoregressive, semi_autoregressive
 from .autoregressive.training import flare_autoregressive_triton
+from .autoregressive.recurrent import flare_recurrent_triton
 from .autoregressive.inference import (
     flare_autoregressive_decode_triton,
     flare_autoregressive_prefill_triton,
@@ -19,11 +20,6 @@ from .semi_autoregressive.inference import (
 )
 
 __version__ = "0.0.1+mi355x"
-
-
-def flare_recurrent_triton(*args, **kwargs):
-    """The experimental token-recurrent variant (reference recurrent.py:1191) is not part of this build."""
-    raise NotImplementedError("flare_recurrent_triton is not part of the MI355X causal FLARE build.")
 
 
 __all__ = [

@@ -93,7 +93,29 @@ def test_semi_ar_stubs_raise():
         causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v)
     with pytest.raises(NotImplementedError):
         causal_flare.flare_semi_autoregressive_decode_trition(q, k, v)
-    with pytest.raises(NotImplementedError):
+
+
+def test_recurrent_validation_messages():
+    """flare_recurrent_triton validates as RecurrentFLARE.forward and the tile helpers
+    (recurrent.py:60-116, 291-312) before it needs a GPU."""
+    q, k, v = torch.randn(2, 16, 16), torch.randn(1, 8, 2, 16), torch.randn(1, 8, 2, 16)
+    with pytest.raises(ValueError, match="Recurrent FLARE expects Q"):
+        causal_flare.flare_recurrent_triton(q[0], k, v)
+    with pytest.raises(ValueError, match="K and V must have the same shape"):
+        causal_flare.flare_recurrent_triton(q, k, torch.randn(1, 8, 2, 32))
+    with pytest.raises(ValueError, match="matching H,D"):
+        causal_flare.flare_recurrent_triton(torch.randn(3, 16, 16), k, v)
+    with pytest.raises(ValueError, match="multiples of 16"):
+        causal_flare.flare_recurrent_triton(torch.randn(2, 8, 16), k, v)
+    with pytest.raises(ValueError, match="BLOCK_T must be 1 or a multiple of 16"):
+        causal_flare.flare_recurrent_triton(q, k, v, block_t=8)
+    with pytest.raises(ValueError, match="BLOCK_T currently supports"):
+        causal_flare.flare_recurrent_triton(q, k, v, block_t=48)
+    with pytest.raises(ValueError, match="BLOCK_M must be a multiple of 16"):
+        causal_flare.flare_recurrent_triton(q, k, v, block_m=8)
+    with pytest.raises(ValueError, match="BLOCK_D must be a multiple of 16"):
+        causal_flare.flare_recurrent_triton(q, k, v, block_d=8)
+    with pytest.raises(RuntimeError, match="GPU"):
         causal_flare.flare_recurrent_triton(q, k, v)
 
 

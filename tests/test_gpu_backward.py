@@ -152,3 +152,51 @@ def test_backward_c_abi_rejects_bad_arguments():
     rc = lib.flare_ar_backward(P(t), P(t), P(t), None, None, 0, B, N, H, 512, D, D, 1.0, P(t), P(t), P(t), P(t),
                                P(t), None, None, P(t), need, None)
     assert rc != 0 and b"M=512" in lib.flare_last_error()
+
+
+# --------------------------------------------------------------------------
+# flare_recurrent_triton (served by the chunked kernels; Y [B, H, T, D])
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("block_t", [1, 16])
+def test_recurrent_decoder_variants_backward_reference_shape(block_t):
+    """test_flare.py:222-281: 3x3 decoder modes, forward at rtol 1e-4 / atol 1e-5,
+    gradients at rtol 1e-2 / atol 1e-3, against the fp64 definition."""
+    from causal_flare import flare_recurrent_triton
+    B, N, H, M, D = 1, 16, 2, 16, 16
+    scale = 1.0 / math.sqrt(D)
+    g = torch.Generator().manual_seed(321)
+    r = lambda *s: torch.randn(s, generator=g)
+    Q, K, V, Qd, Kd = r(H, M, D), r(B, N, H, D), r(B, N, H, D), r(B, N, H, D), r(H, M, D)
+    G = r(B, H, N, D)
+    for qm in ("none", "k_enc", "rand"):
+        for km in ("none", "q_enc", "rand"):
+            _case("recurrent_ref_shape", block_t, qm, km)
+            q, k, v = (t.to(DEV).requires_grad_(True) for t in (Q, K, V))
+            qd = {"none": None, "k_enc": k, "rand": Qd.to(DEV).requires_grad_(True)}[qm]
+            kd = {"none": None, "q_enc": q, "rand": Kd.to(DEV).requires_grad_(True)}[km]
+            y = flare_recurrent_triton(q, k, v, scale=scale, Q_dec=qd, K_dec=kd, block_t=block_t)
+            assert y.shape == (B, H, N, D) and y.dtype == torch.float32
+            (y * G.to(DEV)).sum().backward()
+            qd_o = Qd if qm == "rand" else None
+            kd_o = Kd if km == "rand" else None
+            y_ref = O.brute_ar(Q, K, V, scale, qd_o, kd_o).transpose(0, 2, 1, 3)
+            torch.testing.assert_close(y.detach().cpu().double(), torch.as_tensor(y_ref), rtol=1e-4, atol=1e-5)
+            ref = O.ar_grads(Q, K, V, G.permute(0, 2, 1, 3), scale, qd_o, kd_o)
+            got = [q.grad, k.grad, v.grad, qd.grad if qm == "rand" else None, kd.grad if km == "rand" else None]
+            for name, a, b in zip(("q", "k", "v", "q_dec", "k_dec"), got, ref):
+                if b is None:
+                    continue
+                torch.testing.assert_close(a.cpu().double(), torch.as_tensor(b), rtol=1e-2, atol=1e-3,
+                                           msg=lambda m: f"recurrent {name} q_dec={qm} k_dec={km}: {m}")
+
+
+def test_recurrent_bf16_matches_chunked():
+    """bf16, MFMA shapes: the recurrent entry point equals the chunked one in [B, H, T, D]."""
+    from causal_flare import flare_autoregressive_triton, flare_recurrent_triton
+    _case("recurrent_bf16")
+    B, N, H, M, D = 2, 700, 2, 128, 64
+    q, k, v, _, _, _ = _inputs(17, B, N, H, M, D, D, torch.bfloat16, False, False, q_std=D ** -0.5)
+    y = flare_recurrent_triton(q.to(DEV), k.to(DEV), v.to(DEV))
+    y2 = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV))
+    assert y.dtype == torch.bfloat16 and y.shape == (B, H, N, D)
+    assert torch.equal(y, y2.permute(0, 2, 1, 3))
