@@ -126,6 +126,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
         // reference starts at the prefix's log-sum-exp: den = 1, U = z
         float R[L::MTP][4], dn[L::MTP][4];
         bool dnbig = false;
+        bool rinf = false;   // some latent of this lane has no reference yet (R = -inf)
 #pragma unroll
         for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
@@ -134,6 +135,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                 const float pd = pden[pbase + m];
                 R[mi][r] = pd > 0.0f ? pmax[pbase + m] * kLog2e + __log2f(pd) : kNegInf;
                 dn[mi][r] = pd > 0.0f ? 1.0f : 0.0f;
+                rinf |= R[mi][r] == kNegInf;
             }
         // Rmax = max_m R over the wave's latents, ar = 2^(R - Rmax); refreshed when a reference moves
         float Rmax;
@@ -251,7 +253,6 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                         e[mi][0][r] = exp2f_fast(fmaf(acc[mi][0][r], scale2, -R[mi][r]));
                         e[mi][1][r] = exp2f_fast(fmaf(acc[mi][1][r], scale2, -R[mi][r]));
                         emax = fmaxf(emax, fmaxf(e[mi][0][r], e[mi][1][r]));
-                        dnbig |= R[mi][r] == kNegInf;   // no reference yet (fully masked so far): general path
                     }
                 // token max over this wave's latents (log2 units; -inf for invalid tokens)
                 float lm[2] = {0.0f, 0.0f};
@@ -261,10 +262,11 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                         float mx = kNegInf;
 #pragma unroll
                         for (int mi = 0; mi < L::MTP; ++mi)
-                            mx = fmaxf(mx, fmaxf(fmaxf(acc[mi][ti][0], acc[mi][ti][1]), fmaxf(acc[mi][ti][2], acc[mi][ti][3])));
+                            mx = max3_raw(mx, max3_raw(acc[mi][ti][0], acc[mi][ti][1], acc[mi][ti][2]), acc[mi][ti][3]);
                         lm[ti] = rows_max4(mx) * scale2;
                     }
                 }
+                dnbig |= rinf;   // some latent has no reference yet (fully masked so far): general path
                 const bool moved = __any((emax > L::kLazyE) | dnbig);
                 if (moved) {
                     float gam[L::MTP][4];
@@ -285,6 +287,11 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                             dn[mi][r] *= gam[mi][r];     // E is recomputed on the general path
                         }
                     refresh_ar();
+                    rinf = false;
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) rinf |= R[mi][r] == kNegInf;
                     // rescale factor and den at the subtile start: lanes c = 0..3 store rows r = c
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi) {

@@ -81,7 +81,9 @@ __device__ __forceinline__ void split_f16x4(const float q[4], f16x4& hi, f16x4& 
 // DPP moves inside a 16-lane row.  Lanes whose source is outside the row read 0.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+    // bound_ctrl: a lane whose source is out of its row reads 0 (every pattern used here
+    // either has a source for every lane or wants 0 there), so no old value is needed
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 constexpr int kQuadXor1 = 0xB1;       // quad_perm(1,0,3,2)
 constexpr int kQuadXor2 = 0x4E;       // quad_perm(2,3,0,1)
@@ -113,6 +115,13 @@ __device__ __forceinline__ float row_scan16(float x) {
 }
 // Lane 15 of each 16-lane row, broadcast over the row (DPP row_newbcast:15).
 __device__ __forceinline__ float row_bcast15(float x) { return dpp<0x15F>(x); }
+// max of three floats as one v_max3_f32, for operands that are never NaN (fmaxf would
+// first canonicalise every operand that is not the result of an arithmetic op)
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
 // max / sum over the four 16-lane rows (lanes c, c+16, c+32, c+48)
 __device__ __forceinline__ float rows_max4(float x) {
     x = fmaxf(x, __shfl_xor(x, 16, 64));
