@@ -47,7 +47,7 @@ namespace flare {
 constexpr int kBT = 32;        // tokens per backward chunk
 constexpr int kBNT = 256;      // threads per workgroup; thread m owns latent m (M <= 256)
 constexpr int kBSlab = 64;     // value / key columns per LDS slab
-constexpr int kBP = 65;        // padded pitch of [64][64] LDS tiles
+constexpr int kBP = 65;        // padded pitch of [kBT][64] LDS tiles read as scalars
 constexpr int kBTok = 16;      // tokens per tile in the token-row kernels
 constexpr int kBGroup = 512;   // tokens per partial sum of dQ / dK_dec
 
