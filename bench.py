@@ -195,6 +195,11 @@ def bench_others(torch, flare):
         B, N = shape[0], shape[1]
         out[name] = {"ms": dt * 1e3, "tok_s": B * N / dt}
         del q, k, v, y, dy
+    q, k, v = (t.requires_grad_(True) for t in inputs(4, 2, 8192, 16, 128, 64))
+    y, _ = flare.flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=64)
+    dy = torch.randn_like(y)
+    dt = timed(lambda: y.backward(dy, retain_graph=True), 5, warm=2)
+    out["config5_semi_ar_backward"] = {"ms": dt * 1e3, "tok_s": 2 * 8192 / dt}
     return out
 
 

@@ -31,6 +31,8 @@ HEADER_FUNCTIONS = (
     "flare_semi_ar_workspace_size",
     "flare_semi_ar_workspace_size_sep",
     "flare_semi_ar_forward",
+    "flare_semi_ar_backward_workspace_size",
+    "flare_semi_ar_backward",
 )
 
 F32, BF16, F16 = 0, 1, 2
@@ -78,6 +80,10 @@ def _declare(lib):
     lib.flare_semi_ar_workspace_size.argtypes = [_i64] * 6
     lib.flare_semi_ar_workspace_size_sep.restype = _sz
     lib.flare_semi_ar_workspace_size_sep.argtypes = [_i64] * 6
+    lib.flare_semi_ar_backward_workspace_size.restype = _sz
+    lib.flare_semi_ar_backward_workspace_size.argtypes = [_i64] * 7
+    lib.flare_semi_ar_backward.restype = _i
+    lib.flare_semi_ar_backward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 7 + [_vp, _sz, _vp])
     lib.flare_semi_ar_forward.restype = _i
     lib.flare_semi_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp, _i, _vp, _vp]
                                           + [_vp, _sz, _vp])

@@ -5,7 +5,9 @@ Drop-in for ``flare_semi_autoregressive_trition`` / ``SemiAutoRegressiveFLARE``
 g attends to every token of blocks <= g.  Returns ``(Y, {"LSE_dec": [B,H,N],
 "LSE_enc": [B,H,NB,M]})`` and, with ``profile=True``, a third timings dict.
 Validation (``semi_autoregressive/reference.py:17-51``) runs before the device
-check, so its errors are raised for CPU tensors too.  Forward only.
+check, so its errors are raised for CPU tensors too.  The backward
+(reference ``_semi_autoregressive_backward_impl``, training.py:3768-3988) runs
+as HIP kernels through ``flare_semi_ar_backward``.
 """
 from __future__ import annotations
 
@@ -58,7 +60,8 @@ def _validate_block_causal_config(*, N: int, block_size, chunk_size, name: str):
 
 
 def _semi_autoregressive_forward(Q, K, V, *, block_size, chunk_size, scale=None, input_precision=None,
-                                 profile=False, Q_dec=None, K_dec=None):
+                                 profile=False, Q_dec=None, K_dec=None, saved=None):
+    """Forward launch; when ``saved`` is a dict it receives what the backward needs."""
     name = "SemiAutoRegressiveFLARE"
     B, N, H, M, D_score, D_value = validate_flare_qkv_layouts(Q, K, V, name=name)
     block_size, chunk_size, NB, _, _ = _validate_block_causal_config(
@@ -92,10 +95,45 @@ def _semi_autoregressive_forward(Q, K, V, *, block_size, chunk_size, scale=None,
     rc = _PhaseTimer(device, profile_data["forward"] if profile else None)("semi_ar_forward", launch)
     _lib.check(rc, "flare_semi_ar_forward")
     aux = {"LSE_dec": lse_dec, "LSE_enc": lse_enc}
+    if saved is not None:
+        saved.update(qd=qd, kd=kd, Y=Y, scale=scale, block=block_size)
     if profile:
         _refresh_profile_totals(profile_data)
         return Y, aux, profile_data
     return Y, aux
+
+
+def run_semi_backward(Q, K, V, qd, kd, Y, dY, *, scale, block):
+    """Launch flare_semi_ar_backward; returns (dQ, dK, dV, dQ_dec, dK_dec) in the
+    inputs' dtypes (None for a decoder tensor that was not separate)."""
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    if dY is None:
+        return None, None, None, None, None
+    if N == 0:
+        return tuple(None if t is None else torch.zeros_like(t) for t in (Q, K, V, qd, kd))
+    if M > 256 or Dk > 256 or Dv > 512:
+        raise NotImplementedError(
+            f"The MI355X semi-autoregressive FLARE backward supports M <= 256, D_score <= 256 and D_value <= 512; "
+            f"got M={M}, D_score={Dk}, D_value={Dv}."
+        )
+    device = K.device
+    cdt = _compute_dtype(Q, K, V, qd, kd)
+    prep = lambda t: None if t is None else t.to(cdt).contiguous()
+    q, k, v, qdc, kdc, y, dy = (prep(t) for t in (Q, K, V, qd, kd, Y, dY))
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqd = torch.empty_like(qdc) if qdc is not None else None
+    dkd = torch.empty_like(kdc) if kdc is not None else None
+    lib = _lib.lib()
+    nbytes = lib.flare_semi_ar_backward_workspace_size(B, N, H, M, Dk, Dv, block)
+    ws = torch.empty(nbytes, device=device, dtype=torch.uint8)
+    P = _lib.ptr
+    rc = lib.flare_semi_ar_backward(P(q), P(k), P(v), P(qdc), P(kdc), _lib.dtype_code(cdt), B, N, H, M, Dk, Dv,
+                                    float(scale), block, P(y), P(dy), P(dq), P(dk), P(dv), P(dqd), P(dkd), P(ws),
+                                    nbytes, _lib.stream_of(device))
+    _lib.check(rc, "flare_semi_ar_backward")
+    cast = lambda g, ref: None if g is None else g.to(ref.dtype)
+    return cast(dq, Q), cast(dk, K), cast(dv, V), cast(dqd, qd), cast(dkd, kd)
 
 
 class SemiAutoRegressiveFLARE(autograd.Function):
@@ -104,15 +142,22 @@ class SemiAutoRegressiveFLARE(autograd.Function):
     @staticmethod
     def forward(ctx, Q, K, V, scale=None, block_size=None, chunk_size=None, input_precision=None,
                 profile=False, Q_dec=None, K_dec=None):
-        return _semi_autoregressive_forward(Q, K, V, block_size=block_size, chunk_size=chunk_size, scale=scale,
-                                            input_precision=input_precision, profile=profile, Q_dec=Q_dec,
-                                            K_dec=K_dec)
+        saved = {}
+        out = _semi_autoregressive_forward(Q, K, V, block_size=block_size, chunk_size=chunk_size, scale=scale,
+                                           input_precision=input_precision, profile=profile, Q_dec=Q_dec,
+                                           K_dec=K_dec, saved=saved)
+        ctx.scale = saved.get("scale")
+        ctx.block = saved.get("block")
+        ctx.save_for_backward(Q, K, V, saved.get("qd"), saved.get("kd"), saved.get("Y"))
+        return out
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError(
-            "The MI355X semi-autoregressive FLARE build implements the forward pass only; backward is not available."
-        )
+    def backward(ctx, dY, *unused):
+        """Gradients of Q, K, V (and Q_dec, K_dec when separate): reference
+        _semi_autoregressive_backward_impl (semi training.py:3768-3988)."""
+        Q, K, V, qd, kd, Y = ctx.saved_tensors
+        dq, dk, dv, dqd, dkd = run_semi_backward(Q, K, V, qd, kd, Y, dY, scale=ctx.scale, block=ctx.block)
+        return dq, dk, dv, None, None, None, None, None, dqd, dkd
 
 
 def flare_semi_autoregressive_trition(Q, K, V, *, block_size, chunk_size, scale=None, input_precision=None,

@@ -832,6 +832,68 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// dQ, dK, dQ_dec, dK_dec from the score gradients (ds in DS; da = C - AL gy):
+// shared by the token-causal and the block-causal backward.
+template <typename T>
+static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, bool sep_q, bool sep_k, int64_t B,
+                           int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
+                           const float* C, const float* gy, void* dQ, void* dK, void* dQd, void* dKd, float* P1,
+                           float* P2, hipStream_t st) {
+    const int64_t BH = B * H, NG = (N + kBGroup - 1) / kBGroup;
+    int rc;
+    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT), 0,
+                       st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
+                       static_cast<T*>(dK), static_cast<T*>(dQd));
+    if ((rc = check_launch("bwd_dk_kernel"))) return rc;
+    hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
+                       dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
+    if ((rc = check_launch("bwd_dq_kernel"))) return rc;
+    const int64_t red = H * M * Dk;
+    hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P1, (int)B,
+                       (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dQ));
+    if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
+    if (sep_k) {
+        hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P2,
+                           (int)B, (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dKd));
+        if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
+    }
+    return FLARE_OK;
+}
+
+template <typename T>
+static int launch_gy(const T* dy, const T* y, int64_t B, int64_t N, int64_t H, int64_t Dv, float* gy, hipStream_t st) {
+    const int64_t rows = B * N * H;
+    hipLaunchKernelGGL(bwd_gy_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, y, (int)N, (int)H,
+                       (int)Dv, rows, gy);
+    return check_launch("bwd_gy_kernel");
+}
+
+size_t bwd_partial_floats(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk) {
+    return (size_t)B * H * ((N + kBGroup - 1) / kBGroup) * M * Dk;
+}
+
+int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N, int64_t H, int64_t Dv, float* gy,
+                  hipStream_t st) {
+    if (dtype == FLARE_BF16)
+        return launch_gy((const __hip_bfloat16*)dY, (const __hip_bfloat16*)Y, B, N, H, Dv, gy, st);
+    if (dtype == FLARE_F16) return launch_gy((const __half*)dY, (const __half*)Y, B, N, H, Dv, gy, st);
+    return launch_gy((const float*)dY, (const float*)Y, B, N, H, Dv, gy, st);
+}
+
+int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
+                        int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
+                        const float* C, const float* gy, void* dQ, void* dK, void* dQdec, void* dKdec, float* P1,
+                        float* P2, hipStream_t st) {
+    const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
+#define FLARE_CONTRACT(TY)                                                                                       \
+    return launch_contract((const TY*)Q, (const TY*)K, (const TY*)(sep_q ? Qdec : K), (const TY*)(sep_k ? Kdec : Q), \
+                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dQ, dK, dQdec, dKdec, P1, P2, st)
+    if (dtype == FLARE_BF16) FLARE_CONTRACT(__hip_bfloat16);
+    if (dtype == FLARE_F16) FLARE_CONTRACT(__half);
+    FLARE_CONTRACT(float);
+#undef FLARE_CONTRACT
+}
+
 struct BwdLayout {
     int64_t NC, NG;
     size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_la, off_c, off_gy, off_p1, off_p2, total;
@@ -899,10 +961,7 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
                        L, AL, C);
     if ((rc = check_launch("bwd_gz_kernel"))) return rc;
-    const int64_t rows = B * N * H;
-    hipLaunchKernelGGL(bwd_gy_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, y, (int)N,
-                       (int)H, (int)Dv, rows, gy);
-    if ((rc = check_launch("bwd_gy_kernel"))) return rc;
+    if ((rc = launch_gy(dy, y, B, N, H, Dv, gy, st))) return rc;
     hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
                        (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
     if ((rc = check_launch("bwd_summary_kernel"))) return rc;
@@ -916,23 +975,8 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT), 0,
-                       st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, S, AL, C, gy,
-                       static_cast<T*>(dK), static_cast<T*>(dQd));
-    if ((rc = check_launch("bwd_dk_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
-                       dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, S, AL, C, gy, P1, P2);
-    if ((rc = check_launch("bwd_dq_kernel"))) return rc;
-    const int64_t red = H * M * Dk;
-    hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P1, (int)B,
-                       (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dQ));
-    if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
-    if (sep_k) {
-        hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P2,
-                           (int)B, (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dKd));
-        if ((rc = check_launch("bwd_reduce_kernel"))) return rc;
-    }
-    return FLARE_OK;
+    return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, dQ, dK, dQd, dKd, P1,
+                           P2, st);
 }
 
 }  // namespace flare

@@ -68,3 +68,14 @@ int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int6
                          const float* m0, const float* d0, const float* u0, float* m_fin, float* d_fin,
                          float* u_fin, hipStream_t stream);
 }  // namespace flare
+
+namespace flare {
+// Shared by the token-causal and block-causal backward (flare_ar_bwd.hip).
+size_t bwd_partial_floats(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk);
+int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N, int64_t H, int64_t Dv, float* gy,
+                  hipStream_t stream);
+int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
+                        int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
+                        const float* C, const float* gy, void* dQ, void* dK, void* dQdec, void* dKdec, float* P1,
+                        float* P2, hipStream_t stream);
+}  // namespace flare

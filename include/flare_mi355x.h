@@ -168,6 +168,22 @@ int flare_decode_step(const void* Q, const void* K, const void* V, const void* Q
  */
 size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                     int64_t block);
+/*
+ * Backward of flare_semi_ar_forward: from the inputs, Y and dY (all in `dtype`)
+ * write dQ, dK, dV and, when Qdec / Kdec are given, dQdec / dKdec, as
+ * flare_ar_backward does.  Requires block % 16 == 0, N % block == 0 and M, Dk,
+ * Dv multiples of 16 with M <= 256, Dk <= 256, Dv <= 512.  Replaces
+ * _semi_autoregressive_backward_impl (causal_flare/semi_autoregressive/
+ * training.py:3768-3988), the autograd backward of SemiAutoRegressiveFLARE.
+ */
+size_t flare_semi_ar_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk,
+                                             int64_t Dv, int64_t block);
+int flare_semi_ar_backward(const void* Q, const void* K, const void* V, const void* Qdec,
+                           const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                           int64_t Dk, int64_t Dv, float scale, int64_t block, const void* Y,
+                           const void* dY, void* dQ, void* dK, void* dV, void* dQdec, void* dKdec,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 /* As flare_ar_forward_workspace_size_sep: room for the decoder softmax of separate
  * decoder tensors, which then run on the bf16 MFMA path. */
 size_t flare_semi_ar_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,

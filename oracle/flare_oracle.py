@@ -21,7 +21,9 @@ Two layers:
   They are the pins for the C restatement (see tests/test_oracle.py).
 * ``ar_grads``: fp64 torch autograd of ``ar_forward_torch64`` (the same
   definition with cumulative sums), the ground truth of the backward; pinned
-  by ``brute_ar`` (forward values) and by central finite differences.
+  by ``brute_ar`` (forward values) and by central finite differences;
+  ``semi_grads`` likewise for the block-causal forward (pinned by
+  ``brute_semi_ar`` and finite differences).
 
 Parity status: every C entry point is pinned by fp64 brute force, by
 invariants (chunk-size independence, prefill/decode continuation, state
@@ -346,5 +348,41 @@ def ar_grads(Q, K, V, dY, scale=None, Q_dec=None, K_dec=None):
 
     q, k, v, qd, kd = (leaf(x) for x in (Q, K, V, Q_dec, K_dec))
     y = ar_forward_torch64(q, k, v, scale, qd, kd)
+    (y * torch.as_tensor(_f64(dY))).sum().backward()
+    return tuple(None if x is None else x.grad.numpy() for x in (q, k, v, qd, kd))
+
+
+def semi_forward_torch64(Q, K, V, block_size, scale=None, Q_dec=None, K_dec=None):
+    """Block-causal definition (semi_autoregressive/reference.py:560-597: token t of
+    block g attends to every token of blocks <= g) in fp64 torch ops: the
+    cumulative sums of ar_forward_torch64 read at each block's last token."""
+    import torch
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = K if Q_dec is None else Q_dec
+    Kd = Q if K_dec is None else K_dec
+    S = scale * torch.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * torch.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    E = torch.exp(S - S.amax(dim=2, keepdim=True))
+    Vt = V.transpose(1, 2)
+    num = torch.cumsum(E.unsqueeze(-1) * Vt.unsqueeze(3), dim=2)
+    Z = num / torch.cumsum(E, dim=2).unsqueeze(-1)                      # [B,H,N,M,Dv]
+    ends = (torch.arange(N) // block_size + 1) * block_size - 1         # each token's block end
+    Y = torch.einsum("bhnm,bhnmd->bhnd", torch.softmax(A, dim=-1), Z[:, :, ends])
+    return Y.transpose(1, 2)
+
+
+def semi_grads(Q, K, V, dY, block_size, scale=None, Q_dec=None, K_dec=None):
+    """Gradients of sum(Y * dY) for the block-causal forward, fp64 autograd --
+    the ground truth of the reference's block-causal backward tests
+    (testing/semi_autoregressive/test_block_causal.py:346-578)."""
+    import torch
+
+    def leaf(x):
+        return None if x is None else torch.as_tensor(_f64(x)).requires_grad_(True)
+
+    q, k, v, qd, kd = (leaf(x) for x in (Q, K, V, Q_dec, K_dec))
+    y = semi_forward_torch64(q, k, v, block_size, scale, qd, kd)
     (y * torch.as_tensor(_f64(dY))).sum().backward()
     return tuple(None if x is None else x.grad.numpy() for x in (q, k, v, qd, kd))

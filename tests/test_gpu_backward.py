@@ -200,3 +200,56 @@ def test_recurrent_bf16_matches_chunked():
     y2 = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV))
     assert y.dtype == torch.bfloat16 and y.shape == (B, H, N, D)
     assert torch.equal(y, y2.permute(0, 2, 1, 3))
+
+
+# --------------------------------------------------------------------------
+# Block-causal (semi-autoregressive) backward
+# --------------------------------------------------------------------------
+def _run_semi(Q, K, V, Qd, Kd, G, block, scale):
+    from causal_flare import flare_semi_autoregressive_trition
+    leaves = [None if t is None else t.to(DEV).requires_grad_(True) for t in (Q, K, V, Qd, Kd)]
+    y, aux = flare_semi_autoregressive_trition(leaves[0], leaves[1], leaves[2], block_size=block,
+                                               chunk_size=min(block, 64), scale=scale, Q_dec=leaves[3],
+                                               K_dec=leaves[4])
+    (y.float() * G.to(DEV).float()).sum().backward()
+    return y, [None if t is None else t.grad for t in leaves]
+
+
+@pytest.mark.parametrize("sep", [(False, False), (True, True)])
+def test_semi_backward_reference_shape_bf16(sep):
+    """test_block_causal.py:433-530: B=1, N=64, H=2, M=16, D=16, block 32, bf16,
+    rtol = atol = 2e-2."""
+    _case("semi_bwd_ref_shape", sep)
+    Q, K, V, Qd, Kd, G = _inputs(6, 1, 64, 2, 16, 16, 16, torch.bfloat16, *sep)
+    scale = 16 ** -0.5
+    _, grads = _run_semi(Q, K, V, Qd, Kd, G, 32, scale)
+    ref = O.semi_grads(Q, K, V, G, 32, scale, Qd, Kd)
+    for name, g, r in zip(("q", "k", "v", "q_dec", "k_dec"), grads, ref):
+        if r is None:
+            continue
+        torch.testing.assert_close(g.cpu().double(), torch.as_tensor(r), rtol=2e-2, atol=2e-2,
+                                   msg=lambda m: f"semi {name}: {m}")
+
+
+@pytest.mark.parametrize("block", [16, 64])
+@pytest.mark.parametrize("sep", [(False, False), (True, False), (False, True)])
+def test_semi_backward_fp32(block, sep):
+    _case("semi_bwd_fp32", block, sep)
+    Q, K, V, Qd, Kd, G = _inputs(12, 2, 256, 2, 32, 32, 48, torch.float32, *sep)
+    scale = 32 ** -0.5
+    _, grads = _run_semi(Q, K, V, Qd, Kd, G, block, scale)
+    _check(grads, O.semi_grads(Q, K, V, G, block, scale, Qd, Kd), 1e-4, f"semi fp32 block={block} sep={sep}")
+
+
+def test_semi_backward_large_bf16():
+    """test_block_causal.py:536-580 (B=4, M=64, D=32, block 256; N halved to keep the
+    fp64 oracle small), rtol = atol = 3e-2, and the scale-free bar."""
+    _case("semi_bwd_large")
+    Q, K, V, Qd, Kd, G = _inputs(8, 4, 4096, 2, 64, 32, 32, torch.bfloat16, False, False)
+    scale = 32 ** -0.5
+    _, grads = _run_semi(Q, K, V, Qd, Kd, G, 256, scale)
+    ref = O.semi_grads(Q, K, V, G, 256, scale)
+    for name, g, r in zip(("q", "k", "v"), grads, ref):
+        torch.testing.assert_close(g.cpu().double(), torch.as_tensor(r), rtol=3e-2, atol=3e-2,
+                                   msg=lambda m: f"semi large {name}: {m}")
+    _check(grads, ref, 2e-2, "semi large bf16")

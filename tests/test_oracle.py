@@ -249,3 +249,33 @@ def test_grad_oracle_single_latent_is_attention_backward():
     _close(dV, v.grad.numpy(), 1e-10)
     _close(dK, k.grad.numpy(), 1e-10)
     _close(dQ, q.grad.numpy(), 1e-10)
+
+
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, True)])
+@pytest.mark.parametrize("block", [4, 8])
+def test_semi_grad_oracle_forward_is_the_definition(sep_q, sep_k, block):
+    Q, K, V, Qd, Kd, _ = _grad_inputs(4, 2, 16, 2, 8, 8, 5, sep_q, sep_k)
+    y = O.semi_forward_torch64(Q, K, V, block, 0.6, Qd, Kd)
+    _close(y.numpy(), O.brute_semi_ar(Q, K, V, block, 0.6, Qd, Kd), 1e-12)
+
+
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, False), (False, True), (True, True)])
+def test_semi_grad_oracle_matches_finite_differences(sep_q, sep_k):
+    Q, K, V, Qd, Kd, G = _grad_inputs(6, 1, 6, 1, 4, 3, 2, sep_q, sep_k)
+    grads = O.semi_grads(Q, K, V, G, 2, 0.8, Qd, Kd)
+    inputs = [Q, K, V, Qd, Kd]
+    Gn = G.numpy()
+    h = 1e-6
+    for idx, (x, gx) in enumerate(zip(inputs, grads)):
+        if x is None:
+            assert gx is None
+            continue
+        fd = np.zeros(x.shape)
+        for j in range(x.numel()):
+            vals = []
+            for sgn in (1.0, -1.0):
+                xs = [t.clone() if t is not None else None for t in inputs]
+                xs[idx].view(-1)[j] += sgn * h
+                vals.append(float((O.brute_semi_ar(xs[0], xs[1], xs[2], 2, 0.8, xs[3], xs[4]) * Gn).sum()))
+            fd.reshape(-1)[j] = (vals[0] - vals[1]) / (2 * h)
+        np.testing.assert_allclose(gx, fd, rtol=1e-6, atol=1e-8)
