@@ -814,9 +814,11 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
                 bool need = false;
 #pragma unroll
                 for (int mt = 0; mt < L::MTP; ++mt) {
-                    mx[mt] = fmaxf(fmaxf(fmaxf(acc[mt][0][0], acc[mt][0][1]), fmaxf(acc[mt][0][2], acc[mt][0][3])),
-                                   fmaxf(fmaxf(acc[mt][1][0], acc[mt][1][1]), fmaxf(acc[mt][1][2], acc[mt][1][3]))) * scale2;
-                    rt[mt] = fmaxf(rt[mt], mx[mt]);
+                    float x = max3_raw(acc[mt][0][0], acc[mt][0][1], acc[mt][0][2]);
+                    x = max3_raw(x, acc[mt][0][3], acc[mt][1][0]);
+                    x = max3_raw(x, acc[mt][1][1], acc[mt][1][2]);
+                    mx[mt] = fmaxf(x, acc[mt][1][3]) * scale2;
+                    rt[mt] = max3_raw(rt[mt], mx[mt], mx[mt]);
                     need |= mx[mt] > R[mt] + kLazy;
                 }
                 const bool moved = __any(need);
@@ -846,7 +848,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             e[r] = exp2f_fast(fmaf(acc[mt][ti][r], scale2, nR));
-                            es += e[r];
+                            es = (ti == 0 && r == 0) ? e[r] : es + e[r];   // e >= 0: 0 + e = e
                         }
                         *reinterpret_cast<f16x4*>(et + (mp0 + 16 * mt + c) * L::EP + 16 * ti + 4 * g) =
                             __builtin_convertvector(e, f16x4);
