@@ -91,11 +91,18 @@ constexpr int kRowHalfMirror = 0x141;
 constexpr int kRowMirror = 0x140;
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
 
+// max of two floats as one v_max_f32, for operands that are never NaN (fmaxf would
+// first canonicalise an operand that arrives through a bit cast, as DPP results do)
+__device__ __forceinline__ float max_raw(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 __device__ __forceinline__ float row_max16(float x) {
-    x = fmaxf(x, dpp<kQuadXor1>(x));
-    x = fmaxf(x, dpp<kQuadXor2>(x));
-    x = fmaxf(x, dpp<kRowHalfMirror>(x));
-    x = fmaxf(x, dpp<kRowMirror>(x));
+    x = max_raw(x, dpp<kQuadXor1>(x));
+    x = max_raw(x, dpp<kQuadXor2>(x));
+    x = max_raw(x, dpp<kRowHalfMirror>(x));
+    x = max_raw(x, dpp<kRowMirror>(x));
     return x;
 }
 __device__ __forceinline__ float row_sum16(float x) {
@@ -124,8 +131,8 @@ __device__ __forceinline__ float max3_raw(float a, float b, float c) {
 }
 // max / sum over the four 16-lane rows (lanes c, c+16, c+32, c+48)
 __device__ __forceinline__ float rows_max4(float x) {
-    x = fmaxf(x, __shfl_xor(x, 16, 64));
-    return fmaxf(x, __shfl_xor(x, 32, 64));
+    x = max_raw(x, __shfl_xor(x, 16, 64));
+    return max_raw(x, __shfl_xor(x, 32, 64));
 }
 __device__ __forceinline__ float rows_sum4(float x) {
     x += __shfl_xor(x, 16, 64);
