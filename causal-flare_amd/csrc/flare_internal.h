@@ -60,7 +60,10 @@ bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, const void* alpha, hipStream_t stream);
+                            float* lse_dec, float* lse_enc, void* alpha, bool sep, hipStream_t stream);
+// true when the semi MFMA readout keeps a block's decoder softmax in LDS; otherwise
+// it needs a [B*H, N, M] fp16 alpha buffer in the workspace
+bool semi_alpha_in_lds(int64_t M, int64_t block);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);

@@ -123,21 +123,34 @@ __global__ __launch_bounds__(kSemiNT) void semi_output_kernel(
 
 using namespace flare;
 
+namespace {
+// per-block (max, den, num) summaries; chunks of the MFMA path are whole blocks,
+// so their summaries fit in the same room
+size_t semi_summary_bytes(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t block) {
+    const int64_t NB = N / block;
+    const size_t per = (size_t)B * H * NB * M;
+    return (sizeof(float) * (per * 2 + per * Dv) + 3 * 256 + 255) & ~(size_t)255;
+}
+// fp16 decoder softmax [B*H, N, M], placed after the summaries
+size_t semi_alpha_bytes(int64_t B, int64_t N, int64_t H, int64_t M) {
+    return ((size_t)B * H * N * M * 2 + 255) & ~(size_t)255;
+}
+}  // namespace
+
 extern "C" {
 
 size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                     int64_t block) {
     if (block <= 0) return 0;
-    const int64_t NB = N / block;
-    const size_t per = (size_t)B * H * NB * M;
-    return sizeof(float) * (per * 2 + per * Dv) + 3 * 256;
+    // blocks whose decoder softmax does not fit in LDS keep it in the workspace
+    return semi_summary_bytes(B, N, H, M, Dv, block) +
+           (semi_alpha_in_lds(M, block) ? 0 : semi_alpha_bytes(B, N, H, M));
 }
 
 size_t flare_semi_ar_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                         int64_t block) {
     if (block <= 0) return 0;
-    const size_t base = (flare_semi_ar_workspace_size(B, N, H, M, Dv, block) + 255) & ~(size_t)255;
-    return base + (((size_t)B * H * N * M * 2 + 255) & ~(size_t)255);
+    return semi_summary_bytes(B, N, H, M, Dv, block) + semi_alpha_bytes(B, N, H, M);
 }
 
 int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
@@ -151,7 +164,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                   "semi_ar_forward: need block %% 16 == 0 and N %% block == 0 (N=%lld, block=%lld)",
                   (long long)N, (long long)block);
     FLARE_REQUIRE(Dv <= 64 * kSemiCols, "semi_ar_forward: Dv=%lld exceeds %d", (long long)Dv, 64 * kSemiCols);
-    const size_t need = flare_semi_ar_workspace_size(B, N, H, M, Dv, block);
+    const size_t need = semi_summary_bytes(B, N, H, M, Dv, block);
     if (!workspace || workspace_bytes < need) {
         set_error("semi_ar_forward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
         return FLARE_ERR_WORKSPACE;
@@ -165,14 +178,14 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
     float* bnum = (float*)(ws + 2 * align(per * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
     const bool shared = Qdec == nullptr && Kdec == nullptr;
-    // separate decoder tensors take the MFMA path when the workspace has room for
-    // their softmax (flare_semi_ar_workspace_size_sep)
+    // separate decoder tensors, and blocks whose softmax does not fit in LDS, take the
+    // MFMA path when the workspace has room for the [B*H, N, M] softmax
+    // (flare_semi_ar_workspace_size_sep)
     void* alpha_ws = nullptr;
-    if (!shared && workspace_bytes >= flare_semi_ar_workspace_size_sep(B, N, H, M, Dv, block))
-        alpha_ws = ws + ((need + 255) & ~(size_t)255);
-    if ((mfma_phase_mask() & 3) == 3 && (shared || alpha_ws) &&
+    if (workspace_bytes >= need + semi_alpha_bytes(B, N, H, M)) alpha_ws = ws + need;
+    if ((mfma_phase_mask() & 3) == 3 && (shared || alpha_ws) && (semi_alpha_in_lds(M, block) || alpha_ws) &&
         mfma_semi_supported(dtype, out_dtype, true, M, Dk, Dv, block) && mfma_prepare_supported(dtype, M, Dk, Dv)) {
-        if (alpha_ws) {
+        if (!shared) {
             const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, nullptr,
                                                 alpha_ws, lse_dec, s);
             if (rc) return rc;
@@ -193,7 +206,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                                   nullptr, nullptr, s);
         if (rc) return rc;
         return launch_semi_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, block, bmax, bden, bnum, Y,
-                                       out_dtype, lse_dec, lse_enc, alpha_ws, s);
+                                       out_dtype, lse_dec, lse_enc, alpha_ws, !shared, s);
     }
     int rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, block, bmax, bden, bnum, s);
     if (rc) return rc;

@@ -43,14 +43,18 @@ struct SemiLayout {
 
 // SEP: separate decoder tensors; alpha [B*H, N, M] (fp16, from decoder_alpha_mfma,
 // which also writes LSE_dec) replaces the softmax of the shared scores.
-template <int M, int D, int NW, int NSUB, bool SEP>
+// GA: alpha of the block lives in global memory (the [B*H, N, M] buffer) instead of
+// LDS, for blocks whose alpha does not fit next to the Q bank: written there from
+// the shared scores (or, with SEP, read as the decoder pass left it); the block is
+// nsub = block / 32 subtiles at run time and NSUB is unused.
+template <int M, int D, int NW, int NSUB, bool SEP, bool GA>
 __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, float* __restrict__ lse_dec,
-    float* __restrict__ lse_enc, const f16* __restrict__ alpha) {
+    float* __restrict__ lse_enc, f16* __restrict__ alpha, int nsub_ga) {
     using L = SemiLayout<M, D, NW, NSUB>;
-    __shared__ __attribute__((aligned(16))) f16 al[NSUB * T * L::AP];   // alpha[t][m] of the block
+    __shared__ __attribute__((aligned(16))) f16 al[GA ? 8 : NSUB * T * L::AP];   // alpha[t][m] of the block
     __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];         // E^T[m][tau]
     __shared__ __attribute__((aligned(16))) f16 vtl[D * L::EP];         // V^T[d][tau] (bf16 if moved)
     __shared__ __attribute__((aligned(16))) float lsep[NW * T * 2];     // (max, sum) per wave/token
@@ -61,7 +65,13 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
     const int NC = gridDim.x;
-    const int NB = N / L::BLOCK;
+    const int nsub = GA ? nsub_ga : NSUB;
+    const int blockT = nsub * T;
+    const int NB = N / blockT;
+    // alpha row of token t (block-relative index jt = j * T + row): LDS or global
+    auto arow = [&](int blk, int jt) -> f16* {
+        return GA ? alpha + ((size_t)bh * N + blk + jt) * M : al + jt * L::AP;
+    };
     const int b = bh / H, h = bh % H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -105,8 +115,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
         for (int ks = 0; ks < L::KS; ++ks)
             kb[ti][ks] = load8<bf16x8>(K + row0 + (size_t)(t_begin + 16 * ti + c) * stride + 32 * ks + 8 * g);
 
-    for (int blk0 = t_begin; blk0 < t_end; blk0 += L::BLOCK) {
-        for (int j = 0; j < NSUB; ++j) {
+    for (int blk0 = t_begin; blk0 < t_end; blk0 += blockT) {
+        for (int j = 0; j < nsub; ++j) {
             const int t0 = blk0 + j * T;
             const bool vbig = __any(vt.template store_f16<L::EP>(vtl, dw0, lane));
             vt.load(V, row0, stride, t0 + T, t_end, dw0, lane);
@@ -184,7 +194,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
             __syncthreads();   // S1: lse partials, E^T, rescale factors, moved flags visible
             // ---- alpha = softmax over the bank (fp16 -> LDS), LSE_dec; separate decoder
             //      tensors: alpha copied from the decoder pass
-            if constexpr (SEP) {
+            if constexpr (SEP && !GA) {
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) {
                     const int t = 16 * ti + c;
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                     f16x4 a4;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) a4[r] = (f16)exp2f_fast(s[mi][ti][r] - lse2);
-                    *reinterpret_cast<f16x4*>(al + (j * T + t) * L::AP + mw0 + 16 * mi + 4 * g) = a4;
+                    *reinterpret_cast<f16x4*>(arow(blk0, j * T + t) + mw0 + 16 * mi + 4 * g) = a4;
                 }
             }
             // ---- numerator: move to new reference maxima (rare), then U += E^T V
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
             __syncthreads();   // S2: E^T, V^T and the lse table are rewritten next subtile
         }
         // ---- block end: LSE_enc and 1/d for the readout
-        const int gblk = blk0 / L::BLOCK;
+        const int gblk = blk0 / blockT;
 #pragma unroll
         for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
@@ -286,7 +296,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                 }
         }
         bool bad = false;
-        for (int j = 0; j < NSUB; ++j) {
+        for (int j = 0; j < nsub; ++j) {
 #pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
                 f32x4 yacc[L::DTW];
@@ -294,7 +304,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                 for (int di = 0; di < L::DTW; ++di) yacc[di] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < L::MB; ++kk) {
-                    const f16* ar = al + (j * T + 16 * ti + c) * L::AP + 32 * kk;
+                    const f16* ar = arow(blk0, j * T + 16 * ti + c) + 32 * kk;
                     const f16x8 ab = cat8<f16x8>(load4<f16x4>(ar + 4 * g), load4<f16x4>(ar + 16 + 4 * g));
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di) yacc[di] = mma(za[kk][di], ab, yacc[di]);
@@ -310,13 +320,13 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
         }
         if (__any(bad)) {
             // |z| <= max|v| overflowed fp16 (|v| > 65504 somewhere): redo the block's readout in bf16
-            for (int j = 0; j < NSUB; ++j)
+            for (int j = 0; j < nsub; ++j)
                 for (int ti = 0; ti < 2; ++ti) {
                     f32x4 yacc[L::DTW];
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di) yacc[di] = f32x4{0.f, 0.f, 0.f, 0.f};
                     for (int kk = 0; kk < L::MB; ++kk) {
-                        const f16* ar = al + (j * T + 16 * ti + c) * L::AP + 32 * kk;
+                        const f16* ar = arow(blk0, j * T + 16 * ti + c) + 32 * kk;
                         bf16x8 ab;
 #pragma unroll
                         for (int e2 = 0; e2 < 4; ++e2) {
@@ -356,30 +366,48 @@ bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64
     if (!(dtype == FLARE_BF16 && shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256) &&
           (out_dtype == FLARE_BF16 || out_dtype == FLARE_F32)))
         return false;
+    return block % 32 == 0;
+}
+
+bool semi_alpha_in_lds(int64_t M, int64_t block) {
     return block == 32 || block == 64 || (block == 128 && M == 128);
 }
 
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, const void* alpha, hipStream_t stream) {
+                            float* lse_dec, float* lse_enc, void* alpha, bool sep, hipStream_t stream) {
     FLARE_REQUIRE(chunk % block == 0 && N % block == 0, "semi_output_mfma: chunk and N must be whole blocks");
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, SP)                                                           \
-    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS, SP>), grid, dim3(64 * NWW), 0, stream,          \
+    const bool ga = !semi_alpha_in_lds(M, block);
+    FLARE_REQUIRE(block % T == 0 && (!ga || alpha) && (!sep || alpha),
+                  "semi_output_mfma: block=%lld needs whole subtiles and an alpha buffer", (long long)block);
+#define FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, SP, G)                                                        \
+    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS, SP, G>), grid, dim3(64 * NWW), 0, stream,       \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk,     \
-                       pmax, pden, pnum, Y, out_dtype, lse_dec, lse_enc, (const f16*)alpha)
-#define FLARE_SEMI_MFMA(MM, DD, NWW, NS)                              \
-    do {                                                             \
-        if (alpha) FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, true);       \
-        else FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, false);            \
+                       pmax, pden, pnum, Y, out_dtype, lse_dec, lse_enc, (f16*)alpha, (int)(block / T))
+#define FLARE_SEMI_MFMA(MM, DD, NWW, NS)                                \
+    do {                                                               \
+        if (sep) FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, true, false);    \
+        else FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, false, false);       \
+    } while (0)
+#define FLARE_SEMI_GA(MM, DD, NWW)                                      \
+    do {                                                               \
+        if (sep) FLARE_SEMI_MFMA_SEP(MM, DD, NWW, 1, true, true);      \
+        else FLARE_SEMI_MFMA_SEP(MM, DD, NWW, 1, false, true);         \
     } while (0)
 #define FLARE_SEMI_BLOCKS(MM, DD, NWW)                       \
-    if (block == 32) FLARE_SEMI_MFMA(MM, DD, NWW, 1);        \
+    if (ga) FLARE_SEMI_GA(MM, DD, NWW);                      \
+    else if (block == 32) FLARE_SEMI_MFMA(MM, DD, NWW, 1);   \
     else FLARE_SEMI_MFMA(MM, DD, NWW, 2);
-    if (M == 128 && D == 64) {
+    if (ga) {
+        if (M == 128 && D == 64) FLARE_SEMI_GA(128, 64, 4);
+        else if (M == 128 && D == 128) FLARE_SEMI_GA(128, 128, 4);
+        else if (M == 256 && D == 64) FLARE_SEMI_GA(256, 64, 4);
+        else FLARE_SEMI_GA(256, 128, 8);
+    } else if (M == 128 && D == 64) {
         if (block == 128) FLARE_SEMI_MFMA(128, 64, 4, 4);
         else { FLARE_SEMI_BLOCKS(128, 64, 4) }
     } else if (M == 128 && D == 128) {
@@ -391,6 +419,7 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
         FLARE_SEMI_BLOCKS(256, 128, 8)
     }
 #undef FLARE_SEMI_BLOCKS
+#undef FLARE_SEMI_GA
 #undef FLARE_SEMI_MFMA
 #undef FLARE_SEMI_MFMA_SEP
     return check_launch("semi_output_mfma");

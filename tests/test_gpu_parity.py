@@ -335,6 +335,34 @@ def test_semi_ar_separate_decoder_mfma_bf16(M, D, block, mode):
     assert_parity(aux["LSE_enc"], lse_enc, torch.bfloat16, "semi sep LSE_enc")
 
 
+@pytest.mark.parametrize("M,D,block,N", [(128, 64, 96, 1152), (256, 128, 256, 1024), (128, 128, 512, 1024),
+                                         (256, 64, 160, 960), (128, 64, 1024, 1024)])
+@pytest.mark.parametrize("mode", ["shared", "both"])
+def test_semi_ar_large_blocks_mfma_bf16(M, D, block, N, mode):
+    """Blocks whose decoder softmax does not fit in LDS (any multiple of 32 tokens):
+    the MFMA readout keeps it in the workspace, written from the shared scores or by
+    the decoder pass.  Odd subtile counts (96 = 3 x 32, 160 = 5 x 32) and block = N
+    included; chunk_size is only a launch hint in the reference."""
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_large_block", M, D, block, N, mode)
+    B, H = 2, 2
+    q, k, v = seeded(7 * block + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(block)
+    qd = torch.randn(B, N, H, D, generator=g).bfloat16() if mode == "both" else None
+    kd = (torch.randn(H, M, D, generator=g) * D ** -0.5).bfloat16() if mode == "both" else None
+    dev = lambda t: None if t is None else t.to(DEV)
+    y, aux = flare_semi_autoregressive_trition(dev(q), dev(k), dev(v), block_size=block, chunk_size=32,
+                                               Q_dec=dev(qd), K_dec=dev(kd))
+    y_ref, lse_dec, lse_enc = O.semi_ar(q, k, v, block, 32, Q_dec=qd, K_dec=kd, nthreads=16)
+    assert_parity(y, y_ref, torch.bfloat16, f"semi large block M={M} D={D} block={block} {mode}")
+    if mode == "shared":
+        np.testing.assert_allclose(to_np(aux["LSE_dec"]), lse_dec, rtol=1e-4, atol=1e-4)
+        np.testing.assert_allclose(to_np(aux["LSE_enc"]), lse_enc, rtol=1e-4, atol=1e-4)
+    else:
+        assert_parity(aux["LSE_dec"], lse_dec, torch.bfloat16, "semi large block LSE_dec")
+        assert_parity(aux["LSE_enc"], lse_enc, torch.bfloat16, "semi large block LSE_enc")
+
+
 def test_cfg5_semi_ar_bf16():
     """B=2, N=8192, H=16, M=128, D=64, block 64, bf16, seed 4."""
     from causal_flare import flare_semi_autoregressive_trition
@@ -488,7 +516,8 @@ def test_reference_correctness_suite_bf16(D, qk_std, dec_mode):
 @pytest.mark.parametrize("M,D", [(128, 64), (128, 128), (256, 64), (256, 128)])
 @pytest.mark.parametrize("block", [32, 64, 128])
 def test_semi_ar_mfma_shapes_bf16(M, D, block):
-    """Shapes served by the block-causal MFMA readout (block 128 only for M = 128)."""
+    """Shapes served by the block-causal MFMA readout (M = 256 with block 128 keeps
+    the decoder softmax in the workspace instead of LDS)."""
     from causal_flare import flare_semi_autoregressive_trition
     _print_case("semi_mfma", M, D, block)
     B, N, H = 2, 1024, 2
