@@ -45,8 +45,9 @@ struct SemiLayout {
 // which also writes LSE_dec) replaces the softmax of the shared scores.
 // GA: alpha of the block lives in global memory (the [B*H, N, M] buffer) instead of
 // LDS, for blocks whose alpha does not fit next to the Q bank: written there from
-// the shared scores (or, with SEP, read as the decoder pass left it); the block is
-// nsub = block / 32 subtiles at run time and NSUB is unused.
+// the shared scores (or, with SEP, read as the decoder pass left it) and staged into
+// LDS one subtile at a time for the readout; the block is nsub = block / 32
+// subtiles at run time and NSUB is unused.
 template <int M, int D, int NW, int NSUB, bool SEP, bool GA>
 __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, float* __restrict__ lse_dec,
     float* __restrict__ lse_enc, f16* __restrict__ alpha, int nsub_ga) {
     using L = SemiLayout<M, D, NW, NSUB>;
-    __shared__ __attribute__((aligned(16))) f16 al[GA ? 8 : NSUB * T * L::AP];   // alpha[t][m] of the block
+    __shared__ __attribute__((aligned(16))) f16 al[(GA ? 1 : NSUB) * T * L::AP];   // alpha[t][m] of the block
     __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];         // E^T[m][tau]
     __shared__ __attribute__((aligned(16))) f16 vtl[D * L::EP];         // V^T[d][tau] (bf16 if moved)
     __shared__ __attribute__((aligned(16))) float lsep[NW * T * 2];     // (max, sum) per wave/token
@@ -68,10 +69,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const int nsub = GA ? nsub_ga : NSUB;
     const int blockT = nsub * T;
     const int NB = N / blockT;
-    // alpha row of token t (block-relative index jt = j * T + row): LDS or global
-    auto arow = [&](int blk, int jt) -> f16* {
-        return GA ? alpha + ((size_t)bh * N + blk + jt) * M : al + jt * L::AP;
-    };
+    // alpha row of token blk + jt in global memory (GA)
+    auto grow = [&](int blk, int jt) -> f16* { return alpha + ((size_t)bh * N + blk + jt) * M; };
     const int b = bh / H, h = bh % H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
@@ -221,7 +220,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                     f16x4 a4;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) a4[r] = (f16)exp2f_fast(s[mi][ti][r] - lse2);
-                    *reinterpret_cast<f16x4*>(arow(blk0, j * T + t) + mw0 + 16 * mi + 4 * g) = a4;
+                    f16* dst = GA ? grow(blk0, j * T + t) : al + (j * T + t) * L::AP;
+                    *reinterpret_cast<f16x4*>(dst + mw0 + 16 * mi + 4 * g) = a4;
                 }
             }
             // ---- numerator: move to new reference maxima (rare), then U += E^T V
@@ -297,6 +297,14 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
         }
         bool bad = false;
         for (int j = 0; j < nsub; ++j) {
+            if constexpr (GA) {   // subtile j's alpha rows -> LDS (every wave reads all of them)
+                __syncthreads();
+                for (int vi = tid; vi < T * M / 8; vi += L::NT) {
+                    const int t = vi / (M / 8), m8 = vi % (M / 8);
+                    *reinterpret_cast<f16x8*>(al + t * L::AP + 8 * m8) = load8<f16x8>(grow(blk0, j * T + t) + 8 * m8);
+                }
+                __syncthreads();
+            }
 #pragma unroll
             for (int ti = 0; ti < 2; ++ti) {
                 f32x4 yacc[L::DTW];
@@ -304,7 +312,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                 for (int di = 0; di < L::DTW; ++di) yacc[di] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int kk = 0; kk < L::MB; ++kk) {
-                    const f16* ar = arow(blk0, j * T + 16 * ti + c) + 32 * kk;
+                    const f16* ar = al + ((GA ? 0 : j * T) + 16 * ti + c) * L::AP + 32 * kk;
                     const f16x8 ab = cat8<f16x8>(load4<f16x4>(ar + 4 * g), load4<f16x4>(ar + 16 + 4 * g));
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di) yacc[di] = mma(za[kk][di], ab, yacc[di]);
@@ -326,7 +334,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di) yacc[di] = f32x4{0.f, 0.f, 0.f, 0.f};
                     for (int kk = 0; kk < L::MB; ++kk) {
-                        const f16* ar = arow(blk0, j * T + 16 * ti + c) + 32 * kk;
+                        // (wave-divergent branch: no staging barrier; GA reads global rows)
+                        const f16* ar = (GA ? grow(blk0, j * T + 16 * ti + c) : al + (j * T + 16 * ti + c) * L::AP) + 32 * kk;
                         bf16x8 ab;
 #pragma unroll
                         for (int e2 = 0; e2 < 4; ++e2) {
