@@ -39,6 +39,8 @@
 //   bwd_reduce   sum of the partials over (b, group)
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "flare_common.h"
 #include "flare_internal.h"
 
@@ -841,10 +843,14 @@ static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, boo
                            float* P2, hipStream_t st) {
     const int64_t BH = B * H, NG = (N + kBGroup - 1) / kBGroup;
     int rc;
-    hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT), 0,
-                       st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
-                       static_cast<T*>(dK), static_cast<T*>(dQd));
-    if ((rc = check_launch("bwd_dk_kernel"))) return rc;
+    if (std::is_same<T, __hip_bfloat16>::value && bwd_dk_mfma_supported(M, Dk)) {
+        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dK, dQd, st))) return rc;
+    } else {
+        hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT),
+                           0, st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
+                           static_cast<T*>(dK), static_cast<T*>(dQd));
+        if ((rc = check_launch("bwd_dk_kernel"))) return rc;
+    }
     hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
                        dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
     if ((rc = check_launch("bwd_dq_kernel"))) return rc;
