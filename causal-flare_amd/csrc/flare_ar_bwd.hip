@@ -51,7 +51,7 @@ constexpr int kBNT = 256;      // threads per workgroup; thread m owns latent m 
 constexpr int kBSlab = 64;     // value / key columns per LDS slab
 constexpr int kBP = 65;        // padded pitch of [kBT][64] LDS tiles read as scalars
 constexpr int kBTok = 16;      // tokens per tile in the token-row kernels
-constexpr int kBGroup = 512;   // tokens per partial sum of dQ / dK_dec
+constexpr int kBGroup = kBwdGroup;   // tokens per partial sum of dQ / dK_dec
 
 __device__ __forceinline__ size_t tok_index(int b, int t, int h, int N, int H, int D) {
     return (((size_t)b * N + t) * H + h) * D;
@@ -851,9 +851,13 @@ static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, boo
                            static_cast<T*>(dK), static_cast<T*>(dQd));
         if ((rc = check_launch("bwd_dk_kernel"))) return rc;
     }
-    hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
-                       dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
-    if ((rc = check_launch("bwd_dq_kernel"))) return rc;
+    if (std::is_same<T, __hip_bfloat16>::value && bwd_dq_mfma_supported(M, Dk)) {
+        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, P1, P2, st))) return rc;
+    } else {
+        hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
+                           dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
+        if ((rc = check_launch("bwd_dq_kernel"))) return rc;
+    }
     const int64_t red = H * M * Dk;
     hipLaunchKernelGGL(bwd_reduce_kernel<T>, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, P1, (int)B,
                        (int)H, (int)NG, (int)(M * Dk), scale, static_cast<T*>(dQ));

@@ -139,7 +139,171 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
         }
 }
 
+// dQ / dK_dec partial sums over a group of kDqGroup tokens (the bf16 MFMA form
+// of bwd_dq in flare_ar_bwd.hip):
+//     P1_m = sum_t ds_tm k_t (+ da_tm qd_t when Kd = Q),   P2_m = sum_t da_tm qd_t
+// The contraction runs over tokens, the row index of both ds and K, so each
+// 32-token subtile is staged transposed in LDS: ds^T (bf16 hi and lo) and K^T.
+// Wave w owns latent rows [w M / 4, (w + 1) M / 4) and the DKS value columns of
+// blockIdx.z.
+constexpr int kDqGroup = kBwdGroup;
+constexpr int kDqTP = 32 + 8;       // padded row of the transposed subtiles
+
+template <int MW, int DKS, bool TWO_A, bool TWO_B, bool TWO_OUT>
+__global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, const bf16* __restrict__ Qd, int N,
+                                                   int H, int Dk, const float* __restrict__ DS,
+                                                   const float* __restrict__ AL, const float* __restrict__ C,
+                                                   const float* __restrict__ gy, float* __restrict__ P1,
+                                                   float* __restrict__ P2) {
+    constexpr int M = 64 * MW, NJ = DKS / 16;
+    __shared__ __attribute__((aligned(16))) bf16 sh[M * kDqTP], sl[M * kDqTP];                    // ds^T hi, lo
+    __shared__ __attribute__((aligned(16))) bf16 ah[TWO_A ? M * kDqTP : 8], alo[TWO_A ? M * kDqTP : 8];   // da^T
+    __shared__ __attribute__((aligned(16))) bf16 kt[DKS * kDqTP];                                   // K^T
+    __shared__ __attribute__((aligned(16))) bf16 qt[TWO_B ? DKS * kDqTP : 8];                       // Qd^T
+    const int grp = blockIdx.x, NG = gridDim.x, bh = blockIdx.y, b = bh / H, h = bh % H;
+    const int d0 = blockIdx.z * DKS;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int mw0 = w * 16 * MW;
+    f32x4 acc[MW][NJ], acc2[TWO_OUT ? MW : 1][TWO_OUT ? NJ : 1];
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) {
+            acc[mi][nj] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (TWO_OUT) acc2[mi][nj] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    const int tg0 = grp * kDqGroup, tg1 = min(N, tg0 + kDqGroup);
+    const size_t stride = (size_t)H * Dk;
+    for (int t0 = tg0; t0 < tg1; t0 += 32) {
+        __syncthreads();   // the previous subtile's operands are consumed
+        // ---- ds (and da) rows -> transposed hi / lo; lanes run over m (coalesced loads)
+        for (int e = tid; e < M * 8; e += 256) {
+            const int m = e % M, tq = e / M;
+            float x[4], y[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = t0 + 4 * tq + i;
+                if (t < tg1) {
+                    const size_t o = ((size_t)bh * N + t) * M + m;
+                    x[i] = DS[o];
+                    y[i] = C[o] - AL[o] * gy[(size_t)bh * N + t];
+                } else {
+                    x[i] = y[i] = 0.0f;
+                }
+            }
+            bf16x4 hi, lo;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) SPLIT2(bf16, TWO_A ? x[i] : x[i] + y[i], hi[i], lo[i]);
+            *reinterpret_cast<bf16x4*>(sh + m * kDqTP + 4 * tq) = hi;
+            *reinterpret_cast<bf16x4*>(sl + m * kDqTP + 4 * tq) = lo;
+            if constexpr (TWO_A) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) SPLIT2(bf16, y[i], hi[i], lo[i]);
+                *reinterpret_cast<bf16x4*>(ah + m * kDqTP + 4 * tq) = hi;
+                *reinterpret_cast<bf16x4*>(alo + m * kDqTP + 4 * tq) = lo;
+            }
+        }
+        // ---- K (and Qd) columns d0 .. d0 + DKS -> transposed
+        for (int e = tid; e < DKS * 8; e += 256) {
+            const int d = e % DKS, tq = e / DKS;
+            bf16x4 kv, qv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = t0 + 4 * tq + i;
+                const size_t o = ((size_t)b * N + t) * stride + (size_t)h * Dk + d0 + d;
+                kv[i] = t < tg1 ? K[o] : (bf16)0.0f;
+                if constexpr (TWO_B) qv[i] = t < tg1 ? Qd[o] : (bf16)0.0f;
+            }
+            *reinterpret_cast<bf16x4*>(kt + d * kDqTP + 4 * tq) = kv;
+            if constexpr (TWO_B) *reinterpret_cast<bf16x4*>(qt + d * kDqTP + 4 * tq) = qv;
+        }
+        __syncthreads();
+        // ---- D[m][d] += A[m][t] B[t][d]: A = ds^T rows (hi, lo), B = K^T rows
+        bf16x8 bk[NJ], bq[TWO_B ? NJ : 1];
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) {
+            bk[nj] = load8<bf16x8>(kt + (16 * nj + c) * kDqTP + 8 * g);
+            if constexpr (TWO_B) bq[nj] = load8<bf16x8>(qt + (16 * nj + c) * kDqTP + 8 * g);
+        }
+#pragma unroll
+        for (int mi = 0; mi < MW; ++mi) {
+            const int row = (mw0 + 16 * mi + c) * kDqTP + 8 * g;
+            const bf16x8 a0 = load8<bf16x8>(sh + row), a1 = load8<bf16x8>(sl + row);
+#pragma unroll
+            for (int nj = 0; nj < NJ; ++nj) {
+                acc[mi][nj] = mma(a0, bk[nj], acc[mi][nj]);
+                acc[mi][nj] = mma(a1, bk[nj], acc[mi][nj]);
+            }
+            if constexpr (TWO_A) {
+                const bf16x8 e0 = load8<bf16x8>(ah + row), e1 = load8<bf16x8>(alo + row);
+#pragma unroll
+                for (int nj = 0; nj < NJ; ++nj) {
+                    const bf16x8 bb = TWO_B ? bq[nj] : bk[nj];
+                    if constexpr (TWO_OUT) {
+                        acc2[mi][nj] = mma(e0, bb, acc2[mi][nj]);
+                        acc2[mi][nj] = mma(e1, bb, acc2[mi][nj]);
+                    } else {
+                        acc[mi][nj] = mma(e0, bb, acc[mi][nj]);
+                        acc[mi][nj] = mma(e1, bb, acc[mi][nj]);
+                    }
+                }
+            }
+        }
+    }
+    // ---- partials: row m = mw0 + 16 mi + 4 g + r, column d0 + 16 nj + c
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const size_t o = (((size_t)bh * NG + grp) * M + mw0 + 16 * mi + 4 * g + r) * Dk + d0 + c;
+#pragma unroll
+            for (int nj = 0; nj < NJ; ++nj) {
+                P1[o + 16 * nj] = acc[mi][nj][r];
+                if constexpr (TWO_OUT) P2[o + 16 * nj] = acc2[mi][nj][r];
+            }
+        }
+}
+
 }  // namespace mfma
+
+bool bwd_dq_mfma_supported(int64_t M, int64_t Dk) {
+    return (M == 64 || M == 128 || M == 256) && (Dk == 64 || Dk == 128);
+}
+
+// partial sums per group of 512 tokens into P1 (and P2 when sep_k), as bwd_dq_kernel
+int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
+                   int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
+                   float* P1, float* P2, hipStream_t st) {
+    using namespace mfma;
+    FLARE_REQUIRE(bwd_dq_mfma_supported(M, Dk), "bwd_dq_mfma: unsupported M=%lld Dk=%lld", (long long)M,
+                  (long long)Dk);
+    const int64_t NG = (N + kDqGroup - 1) / kDqGroup;
+    // two accumulator sets (sep_k) keep 64 columns per workgroup
+    const int dks = sep_k ? 64 : (int)Dk;
+    dim3 grid((unsigned)NG, (unsigned)(B * H), (unsigned)(Dk / dks));
+#define FLARE_DQ(MW, DKS, TA, TB, TO)                                                                          \
+    hipLaunchKernelGGL((bwd_dq_mfma<MW, DKS, TA, TB, TO>), grid, dim3(256), 0, st, (const bf16*)K,            \
+                       (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, P1, P2)
+#define FLARE_DQ_MODES(MW, DKS)                                                          \
+    if (sep_k) {                                                                        \
+        if (sep_q) FLARE_DQ(MW, 64, true, true, true);                                  \
+        else FLARE_DQ(MW, 64, true, false, true);                                       \
+    } else {                                                                            \
+        if (sep_q) FLARE_DQ(MW, DKS, true, true, false);                                \
+        else FLARE_DQ(MW, DKS, false, false, false);                                    \
+    }
+#define FLARE_DQ_D(MW)                     \
+    if (Dk == 64) { FLARE_DQ_MODES(MW, 64) } \
+    else { FLARE_DQ_MODES(MW, 128) }
+    if (M == 64) { FLARE_DQ_D(1) }
+    else if (M == 128) { FLARE_DQ_D(2) }
+    else { FLARE_DQ_D(4) }
+#undef FLARE_DQ_D
+#undef FLARE_DQ_MODES
+#undef FLARE_DQ
+    return check_launch("bwd_dq_mfma");
+}
 
 bool bwd_dk_mfma_supported(int64_t M, int64_t Dk) {
     return M % 32 == 0 && M <= mfma::kDkMaxM && (Dk == 64 || Dk == 128);

@@ -64,11 +64,17 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
 // true when the semi MFMA readout keeps a block's decoder softmax in LDS; otherwise
 // it needs a [B*H, N, M] fp16 alpha buffer in the workspace
 bool semi_alpha_in_lds(int64_t M, int64_t block);
+// tokens per partial sum of the backward's dQ / dK_dec contraction
+constexpr int kBwdGroup = 512;
 // bf16 MFMA form of the backward's dK / dQ_dec contraction (flare_bwd_mfma.hip)
 bool bwd_dk_mfma_supported(int64_t M, int64_t Dk);
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
                    const float* gy, void* dK, void* dQd, hipStream_t st);
+bool bwd_dq_mfma_supported(int64_t M, int64_t Dk);
+int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
+                   int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
+                   float* P1, float* P2, hipStream_t st);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);

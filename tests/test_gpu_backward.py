@@ -64,6 +64,7 @@ def _check(grads, ref, tol, what):
         assert a.shape == r.shape, (what, name, a.shape, r.shape)
         assert np.isfinite(a).all(), f"{what}: non-finite {name}"
         err = np.abs(a - r).max() / max(np.abs(r).max(), 1e-2)
+        print(f"  {what}: {name} normalised max error {err:.3e}")
         assert err <= tol, f"{what}: {name} normalised max error {err:.3e} > {tol}"
 
 
@@ -127,16 +128,23 @@ def test_backward_sharp_scores_fp32(q_std):
     _check(grads, O.ar_grads(Q, K, V, G, 1.0, Qd, Kd), 1e-4, f"sharp q_std={q_std}")
 
 
-@pytest.mark.parametrize("M,D,N", [(128, 64, 1000), (256, 128, 300)])
-@pytest.mark.parametrize("sep", [(False, False), (True, False), (False, True)])
+@pytest.mark.parametrize("M,D,N", [(128, 64, 1000), (256, 128, 300), (64, 64, 1100), (64, 128, 77)])
+@pytest.mark.parametrize("sep", [(False, False), (True, False), (False, True), (True, True)])
 def test_backward_bf16(M, D, N, sep):
+    """bf16 inputs: dK / dQ_dec and dQ / dK_dec run as bf16 MFMA contractions (hi/lo
+    split gradients) for these shapes, in all four decoder-weight modes; N = 1100
+    leaves a ragged last token group of the dQ partial sums."""
     _case("bwd_bf16", M, D, N, sep)
     Q, K, V, Qd, Kd, G = _inputs(9, 1, N, 2, M, D, D, torch.bfloat16, *sep)
     Q = (Q.float() / math.sqrt(D)).to(torch.bfloat16)
+    if Kd is not None:   # latent decoder keys scaled like the latent queries
+        Kd = (Kd.float() / math.sqrt(D)).to(torch.bfloat16)
     scale = 1.0 / math.sqrt(D)
     y, grads = _run(Q, K, V, Qd, Kd, G, scale)
     assert y.dtype == torch.bfloat16 and all(g is None or g.dtype == torch.bfloat16 for g in grads)
-    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), 2e-2, f"bf16 M={M} D={D} N={N} sep={sep}")
+    # the reference's bf16 bar: 2e-2, 3e-2 for D >= 128 (test_block_causal.py:178-255)
+    tol = 3e-2 if D >= 128 else 2e-2
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 M={M} D={D} N={N} sep={sep}")
 
 
 def test_backward_c_abi_rejects_bad_arguments():
