@@ -43,6 +43,7 @@
 
 #include "flare_common.h"
 #include "flare_internal.h"
+#include "flare_mfma.h"
 
 namespace flare {
 
@@ -218,13 +219,19 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const float* __restrict__ pmax, const float* __restrict__ pnum, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ AL, float* __restrict__ C) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
-    __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
-    __shared__ __attribute__((aligned(16))) float vs[kBT * kGT];
+    // dY and V slabs; afterwards (bf16) g_t . pu_m of one 16-token half as [m][17]
+    __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
+    static_assert(2 * kBT * kGT >= 256 * 17, "g . pu half tile must fit in the slab staging");
+    float* gs = gsv;
+    float* vs = gsv + kBT * kGT;
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
+    // bf16 inputs with whole 16-latent / 32-column tiles: g . pu on the MFMA
+    const bool mf = kBf16 && M % 16 == 0 && Dv % 32 == 0;
     float gv[kGVJ];
 #pragma unroll
     for (int j = 0; j < kGVJ; ++j) gv[j] = 0.0f;
@@ -239,13 +246,47 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
         stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
-        if (act) {
+        if (act && !mf) {
             for (int d = 0; d < ds; d += 4) {
                 const float4 p = ld4(pu + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
                     const float4 g4 = ld4(gs + t * kGT + d);
                     acc[t] += g4.x * p.x + g4.y * p.y + g4.z * p.z + g4.w * p.w;
+                }
+            }
+        }
+    }
+    if constexpr (kBf16) {
+        if (mf) {
+            // D[m][t] = sum_d pu[m][d] g[t][d] per 16-token half: A = pu rows (fp32 as
+            // bf16 hi + lo), B = dY rows; through LDS to the thread of latent m
+            using namespace mfma;
+            const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+            for (int ti = 0; ti < kBT / 16; ++ti) {
+                __syncthreads();   // the slabs (or the previous half) are consumed
+                const int t = 16 * ti + cl;
+                const bf16* grow = reinterpret_cast<const bf16*>(dY) + tok_index(b, t0 + min(t, nt - 1), h, N, H, Dv) + 8 * g4;
+                for (int mt = w; mt < M / 16; mt += kBNT / 64) {
+                    f32x4 d2 = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const float* prow = pnum + (((size_t)bh * NC + c) * M + 16 * mt + cl) * Dv + 8 * g4;
+                    for (int k0 = 0; k0 < Dv; k0 += 32) {
+                        const float4 p0 = ld4(prow + k0), p1 = ld4(prow + k0 + 4);
+                        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                        bf16x8 ph, pl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+                        const bf16x8 gb = t < nt ? load8<bf16x8>(grow + k0) : zero8();
+                        d2 = mma(ph, gb, d2);
+                        d2 = mma(pl, gb, d2);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
+                }
+                __syncthreads();
+                if (act) {
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) acc[16 * ti + u] = gsv[m * 17 + u];
                 }
             }
         }
