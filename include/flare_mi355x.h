@@ -166,6 +166,9 @@ int flare_decode_step(const void* Q, const void* K, const void* V, const void* Q
  * Replaces _semi_autoregressive_forward_triton and its kernels
  * (causal_flare/semi_autoregressive/training.py:540-1399, 1836-1961).
  */
+/* Workspace of flare_semi_ar_forward: per-block summaries, plus an fp16
+ * [B*H, N, M] buffer for the decoder softmax when the block is too large for
+ * the MFMA readout to keep it in LDS. */
 size_t flare_semi_ar_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                     int64_t block);
 /*
