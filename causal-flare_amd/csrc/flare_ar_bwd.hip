@@ -71,7 +71,7 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 // LA = L2 - log2(alpha), so that e^{s_tau - L_t} alpha_t = exp2(s2_tau - LA_t).
 // S, L and LA hold log2-domain values: every later factor is one exp2.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool MF>
 __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ Qd, const T* __restrict__ Kd,
     int N, int H, int M, int Dk, float scale, bool shared, const float* __restrict__ pmax,
@@ -92,14 +92,46 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     }
     const T* qrow = Q + ((size_t)h * M + (act ? m : 0)) * Dk;
     const T* kdrow = Kd + ((size_t)h * M + (act ? m : 0)) * Dk;
+    // MF (bf16 inputs with whole 16-latent / 32-column tiles): the scores on the
+    // MFMA (exact: bf16 products, fp32 sums), written to LDS as [token][m]
+    // (encoder in at, decoder in kt) for the thread of latent m
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+    constexpr bool mf = kBf16 && MF;
     for (int i0 = 0; i0 < nt; i0 += kBTok) {
         const int ni = min(kBTok, nt - i0);
         __syncthreads();
-        for (int e = tid; e < kBTok * Dk; e += kBNT) {
-            const int i = e / Dk, d = e % Dk;
-            const size_t gi = tok_index(b, t0 + i0 + i, h, N, H, Dk) + d;
-            kt[e] = i < ni ? to_f32(K[gi]) : 0.0f;
-            if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
+        if constexpr (mf) {
+            {
+                using namespace mfma;
+                const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+                const bool ok = cl < ni;
+                const size_t trow = tok_index(b, t0 + i0 + min(cl, ni - 1), h, N, H, Dk) + 8 * g4;
+                const bf16* kr = reinterpret_cast<const bf16*>(K) + trow;
+                const bf16* qdr = reinterpret_cast<const bf16*>(Qd) + trow;
+                for (int mt = w; mt < M / 16; mt += kBNT / 64) {
+                    const size_t lrow = ((size_t)h * M + 16 * mt + cl) * Dk + 8 * g4;
+                    const bf16* qr = reinterpret_cast<const bf16*>(Q) + lrow;
+                    const bf16* kdr = reinterpret_cast<const bf16*>(Kd) + lrow;
+                    f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, sd = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int k0 = 0; k0 < Dk; k0 += 32) {
+                        se = mma(load8<bf16x8>(qr + k0), ok ? load8<bf16x8>(kr + k0) : zero8(), se);
+                        if (!shared) sd = mma(load8<bf16x8>(kdr + k0), ok ? load8<bf16x8>(qdr + k0) : zero8(), sd);
+                    }
+                    // D[m = 16 mt + 4 g + r][token cl]
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        at[cl * M + 16 * mt + 4 * g4 + r] = se[r];
+                        if (!shared) kt[cl * M + 16 * mt + 4 * g4 + r] = sd[r];
+                    }
+                }
+            }
+        } else {
+            for (int e = tid; e < kBTok * Dk; e += kBNT) {
+                const int i = e / Dk, d = e % Dk;
+                const size_t gi = tok_index(b, t0 + i0 + i, h, N, H, Dk) + d;
+                kt[e] = i < ni ? to_f32(K[gi]) : 0.0f;
+                if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
+            }
         }
         __syncthreads();
         float lv[kBTok];
@@ -107,7 +139,14 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
             float as[kBTok], aa[kBTok];
 #pragma unroll
             for (int i = 0; i < kBTok; ++i) as[i] = aa[i] = 0.0f;
-            for (int d = 0; d < Dk; d += 4) {
+            if constexpr (mf) {
+#pragma unroll
+                for (int i = 0; i < kBTok; ++i) {
+                    as[i] = at[i * M + m];
+                    if (!shared) aa[i] = kt[i * M + m];
+                }
+            }
+            for (int d = 0; d < (mf ? 0 : Dk); d += 4) {
                 const float q0 = to_f32(qrow[d]), q1 = to_f32(qrow[d + 1]), q2 = to_f32(qrow[d + 2]),
                             q3 = to_f32(qrow[d + 3]);
 #pragma unroll
@@ -1006,8 +1045,16 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
                                    nullptr, st)))
         return rc;
     const dim3 gc((unsigned)NC, (unsigned)BH);
-    hipLaunchKernelGGL(bwd_stats_kernel<T>, gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M, (int)Dk,
-                       scale, shared, pm, pd, S, L, AL, LA);
+    bool stats_mfma = false;
+    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+        stats_mfma = M % 16 == 0 && Dk % 32 == 0;
+        if (stats_mfma)
+            hipLaunchKernelGGL((bwd_stats_kernel<T, true>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H,
+                               (int)M, (int)Dk, scale, shared, pm, pd, S, L, AL, LA);
+    }
+    if (!stats_mfma)
+        hipLaunchKernelGGL((bwd_stats_kernel<T, false>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M,
+                           (int)Dk, scale, shared, pm, pd, S, L, AL, LA);
     if ((rc = check_launch("bwd_stats_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
                        L, AL, C);
