@@ -1060,9 +1060,14 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
                        L, AL, C);
     if ((rc = check_launch("bwd_gz_kernel"))) return rc;
     if ((rc = launch_gy(dy, y, B, N, H, Dv, gy, st))) return rc;
-    hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
-                       (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
-    if ((rc = check_launch("bwd_summary_kernel"))) return rc;
+    static_assert(kBT == 32, "the MFMA chunk summary assumes 32-token chunks");
+    if (std::is_same<T, __hip_bfloat16>::value && bwd_summary_mfma_supported(M, Dv)) {
+        if ((rc = launch_summary_mfma(dy, B, N, H, M, Dv, L, AL, C, pn, pd, st))) return rc;
+    } else {
+        hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
+                           (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
+        if ((rc = check_launch("bwd_summary_kernel"))) return rc;
+    }
     const int64_t cthreads = BH * M * (Dv / 4);
     hipLaunchKernelGGL(bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, st, pn, pd, L,
                        (int)N, (int)NC, (int)M, (int)Dv, BH * M);

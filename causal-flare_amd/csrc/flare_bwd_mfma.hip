@@ -265,7 +265,108 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
         }
 }
 
+// Per-chunk terms of the backward's reverse scan (the bf16 MFMA form of
+// bwd_summary in flare_ar_bwd.hip), for chunks c >= 1 of 32 tokens:
+//     a_c[m][:] = sum_t w_tm g_t,   b_c[m] = sum_t w_tm c_tm,
+//     w_tm = 2^(Lpre_m - L_tm) alpha_tm   (Lpre = L at the last token of chunk c-1)
+// a is a contraction over tokens: w^T (bf16 hi and lo, computed by the thread of
+// latent m) and g^T (dY, exact) are staged transposed in LDS.
+template <int MW, int DV>
+__global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__ dY, int N, int H,
+                                                        const float* __restrict__ L, const float* __restrict__ AL,
+                                                        const float* __restrict__ C, float* __restrict__ a_out,
+                                                        float* __restrict__ b_out) {
+    constexpr int M = 64 * MW, NJ = DV / 16;
+    __shared__ __attribute__((aligned(16))) bf16 wh[M * kDqTP], wlo[M * kDqTP];   // w^T hi, lo
+    __shared__ __attribute__((aligned(16))) bf16 gt[DV * kDqTP];                  // g^T
+    const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
+    if (c == 0) return;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, g = lane >> 4, cl = lane & 15;
+    const int t0 = c * 32, nt = min(32, N - t0);
+    const size_t rbase = ((size_t)bh * N + t0) * M;
+    const size_t sbase = ((size_t)bh * NC + c) * M;
+    if (tid < M) {
+        const int m = tid;
+        const float lp = L[rbase - M + m];
+        float bsum = 0.0f;
+#pragma unroll
+        for (int t8 = 0; t8 < 4; ++t8) {
+            bf16x8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int t = 8 * t8 + e;
+                float wv = 0.0f;
+                if (t < nt) {
+                    const size_t o = rbase + (size_t)t * M + m;
+                    const float f = __builtin_amdgcn_exp2f(lp - L[o]);
+                    wv = f * AL[o];
+                    bsum += f * C[o];
+                }
+                SPLIT2(bf16, wv, hi[e], lo[e]);
+            }
+            *reinterpret_cast<bf16x8*>(wh + m * kDqTP + 8 * t8) = hi;
+            *reinterpret_cast<bf16x8*>(wlo + m * kDqTP + 8 * t8) = lo;
+        }
+        b_out[sbase + m] = bsum;
+    }
+    const size_t stride = (size_t)H * DV;
+    for (int e = tid; e < DV * 8; e += 256) {
+        const int d = e % DV, tq = e / DV;
+        bf16x4 gv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int t = 4 * tq + i;
+            gv[i] = t < nt ? dY[((size_t)b * N + t0 + t) * stride + (size_t)h * DV + d] : (bf16)0.0f;
+        }
+        *reinterpret_cast<bf16x4*>(gt + d * kDqTP + 4 * tq) = gv;
+    }
+    __syncthreads();
+    bf16x8 bg[NJ];
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj) bg[nj] = load8<bf16x8>(gt + (16 * nj + cl) * kDqTP + 8 * g);
+    const int mw0 = w * 16 * MW;
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi) {
+        const int row = (mw0 + 16 * mi + cl) * kDqTP + 8 * g;
+        const bf16x8 a0 = load8<bf16x8>(wh + row), a1 = load8<bf16x8>(wlo + row);
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            acc = mma(a0, bg[nj], acc);
+            acc = mma(a1, bg[nj], acc);
+            // rows m = mw0 + 16 mi + 4 g + r, column 16 nj + cl
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a_out[(sbase + mw0 + 16 * mi + 4 * g + r) * DV + 16 * nj + cl] = acc[r];
+        }
+    }
+}
+
 }  // namespace mfma
+
+bool bwd_summary_mfma_supported(int64_t M, int64_t Dv) {
+    return (M == 64 || M == 128 || M == 256) && (Dv == 64 || Dv == 128);
+}
+
+int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
+                        const float* AL, const float* C, float* a_out, float* b_out, hipStream_t st) {
+    using namespace mfma;
+    FLARE_REQUIRE(bwd_summary_mfma_supported(M, Dv), "bwd_summary_mfma: unsupported M=%lld Dv=%lld",
+                  (long long)M, (long long)Dv);
+    dim3 grid((unsigned)((N + 31) / 32), (unsigned)(B * H));
+#define FLARE_SUM(MW, DD)                                                                                \
+    hipLaunchKernelGGL((bwd_summary_mfma<MW, DD>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
+                       L, AL, C, a_out, b_out)
+#define FLARE_SUM_D(MW)              \
+    if (Dv == 64) FLARE_SUM(MW, 64); \
+    else FLARE_SUM(MW, 128);
+    if (M == 64) { FLARE_SUM_D(1) }
+    else if (M == 128) { FLARE_SUM_D(2) }
+    else { FLARE_SUM_D(4) }
+#undef FLARE_SUM_D
+#undef FLARE_SUM
+    return check_launch("bwd_summary_mfma");
+}
 
 bool bwd_dq_mfma_supported(int64_t M, int64_t Dk) {
     return (M == 64 || M == 128 || M == 256) && (Dk == 64 || Dk == 128);

@@ -71,6 +71,9 @@ bool bwd_dk_mfma_supported(int64_t M, int64_t Dk);
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
                    const float* gy, void* dK, void* dQd, hipStream_t st);
+bool bwd_summary_mfma_supported(int64_t M, int64_t Dv);
+int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
+                        const float* AL, const float* C, float* a_out, float* b_out, hipStream_t st);
 bool bwd_dq_mfma_supported(int64_t M, int64_t Dk);
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
