@@ -333,9 +333,11 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
                           hipStream_t stream, const int32_t* tmask = nullptr) {
     if ((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv)) {
         if (output_pc_enabled() && (M == 128 || M == 256))
-            return launch_prepare_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, tmask, stream);
+            return launch_prepare_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, tmask,
+                                     dtype == FLARE_F16, stream);
         if (tmask == nullptr)
-            return launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, stream);
+            return launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, dtype == FLARE_F16,
+                                       stream);
     }
     FLARE_REQUIRE(Dv <= 4 * kPrepCols, "chunk_prepare: Dv=%lld exceeds %d", (long long)Dv, 4 * kPrepCols);
     const int64_t NC = (N + chunk - 1) / chunk;
@@ -389,16 +391,16 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
     if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr) {
         if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled()))
             return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
-                                      tmask, stream);
+                                      tmask, dtype == FLARE_F16, stream);
         // separate decoder tensors: the decoder softmax first (alpha_ws, [B*H, N, M] fp16),
         // then the producer/consumer kernel reading it
         if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
             mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
             const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, tmask,
-                                                alpha_ws, nullptr, stream);
+                                                alpha_ws, nullptr, dtype == FLARE_F16, stream);
             if (rc) return rc;
             return launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask,
-                                    alpha_ws, stream);
+                                    alpha_ws, dtype == FLARE_F16, stream);
         }
     }
     const int DT = pick_dt(M, Dv);

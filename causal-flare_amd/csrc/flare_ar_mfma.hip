@@ -751,19 +751,24 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
 using namespace mfma;
 
 bool mfma_prepare_supported(int dtype, int64_t M, int64_t Dk, int64_t Dv) {
-    return dtype == FLARE_BF16 && Dk == Dv && (Dk == 64 || Dk == 128) && M % 32 == 0 && M >= 32 && M <= kMaxPrepM;
+    const bool shape = Dk == Dv && (Dk == 64 || Dk == 128);
+    if (dtype == FLARE_BF16) return shape && M % 32 == 0 && M >= 32 && M <= kMaxPrepM;
+    // fp16 inputs: the producer / consumer kernel only
+    return dtype == FLARE_F16 && shape && output_pc_enabled() && (M == 128 || M == 256);
 }
 
 bool mfma_output_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv) {
-    return dtype == FLARE_BF16 && shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256) &&
-           (out_dtype == FLARE_BF16 || out_dtype == FLARE_F32);
+    const bool shape = shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256);
+    if (dtype == FLARE_BF16) return shape && (out_dtype == FLARE_BF16 || out_dtype == FLARE_F32);
+    return dtype == FLARE_F16 && shape && output_pc_enabled() && (out_dtype == FLARE_F16 || out_dtype == FLARE_F32);
 }
 
 int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                         int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
-                        float* cnum, hipStream_t stream) {
+                        float* cnum, bool f16in, hipStream_t stream) {
     if (output_pc_enabled() && (M == 128 || M == 256))
-        return launch_prepare_pc(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, nullptr, stream);
+        return launch_prepare_pc(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, nullptr, f16in, stream);
+    FLARE_REQUIRE(!f16in, "chunk_prepare_mfma: fp16 inputs need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_mfma: chunk must be a multiple of %d", T);
     FLARE_REQUIRE(M % 32 == 0 && M >= 32 && M <= kMaxPrepM && (D == 64 || D == 128),
                   "chunk_prepare_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
@@ -794,10 +799,11 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
-                       hipStream_t stream) {
+                       bool f16in, hipStream_t stream) {
     if (output_pc_enabled())
         return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, nullptr,
-                                stream);
+                                f16in, stream);
+    FLARE_REQUIRE(!f16in, "chunk_output_mfma: fp16 inputs need the producer/consumer kernel");
     FLARE_REQUIRE(tmask == nullptr, "chunk_output_mfma: token masks need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);
     const int64_t NC = (N + chunk - 1) / chunk;

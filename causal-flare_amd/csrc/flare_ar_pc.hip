@@ -67,7 +67,7 @@ struct PCLayout {
 // SEP: separate decoder weights.  alpha [B*H, N, M] (fp16) then holds the
 // decoder softmax, written by decoder_alpha_mfma; the producers read it in place
 // of the token softmax of the shared scores (no meeting, no factorised p).
-template <int M, int D, int NPW, bool SEP>
+template <int M, int D, int NPW, bool SEP, bool F16>
 __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa[mi][kq], kb[ti], acc[mi][ti]);
+                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma_in<F16>(qa[mi][kq], kb[ti], acc[mi][ti]);
                 }
                 if (ragged || tmask != nullptr) {
 #pragma unroll
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                     const int row = 16 * ti + c;
 #pragma unroll
                     for (int kq = 0; kq < L::KS; ++kq)
-                        a = mma(qa[mi][kq], load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g)), a);
+                        a = mma_in<F16>(qa[mi][kq], load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g)), a);
                     if ((ragged && t0 + row >= t_end) || !keep[ti]) a = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
                     return a;
                 };
@@ -541,7 +541,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                     for (int di = 0; di < L::DTC; ++di) U[mi][di] *= vs;
             }
         }
-        VTile<L::DC, 64> vt;
+        VTile<L::DC, 64, F16> vt;
         vt.load(V, row0, stride, t_begin, t_end, dc0, lane);
         __syncthreads();   // B0
         for (int it = 0; it <= NS; ++it) {
@@ -704,7 +704,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
 // output kernel above.  The summary is returned relative to the true chunk
 // max: (max, den 2^(R - max), U 2^(R - max)) in natural-log units.
 // ---------------------------------------------------------------------------
-template <int M, int D, int NPW>
+template <int M, int D, int NPW, bool F16>
 __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum,
@@ -798,7 +798,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 #pragma unroll
                     for (int mt = 0; mt < L::MTP; ++mt)
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) acc[mt][ti] = mma(ka[ti], qb[mt][kq], acc[mt][ti]);
+                        for (int ti = 0; ti < 2; ++ti) acc[mt][ti] = mma_in<F16>(ka[ti], qb[mt][kq], acc[mt][ti]);
                 }
                 if (t0 + T > t_end || tmask != nullptr) {      // the ragged last subtile, masked tokens
 #pragma unroll
@@ -891,7 +891,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
             for (int di = 0; di < L::DTC; ++di) U[mi][di] = f32x4{0.f, 0.f, 0.f, 0.f};
         float vs = 1.0f;     // V' = V vs, U' = U vs (powers of two keep |V'| <= kVCap)
         // V of subtiles j (vt) and j + 1 (vn) in registers: fetched two subtiles ahead
-        VTile<L::DC, 64> vt, vn;
+        VTile<L::DC, 64, F16> vt, vn;
         vt.load(V, row0, stride, t_begin, t_end, dc0, lane);
         vn.load(V, row0, stride, t_begin + T, t_end, dc0, lane);
         lds_barrier();   // B0
@@ -967,7 +967,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_prepare_pc(
 // grid (ceil(N / 128), B*H), 4 waves; wave w takes tokens 32 w .. 32 w + 31 of the
 // block, with Kd rows as the A operand and the token rows as B.
 // ---------------------------------------------------------------------------
-template <int M, int D>
+template <int M, int D, bool F16>
 __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict__ Qd, const bf16* __restrict__ Kd,
                                                           int N, int H, float scale2,
                                                           const int32_t* __restrict__ tmask, f16* __restrict__ alpha,
@@ -993,8 +993,8 @@ __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict
 #pragma unroll
         for (int kq = 0; kq < KS; ++kq) {
             const bf16x8 a = load8<bf16x8>(Kd + ((size_t)h * M + 16 * mt + c) * D + 32 * kq + 8 * g);
-            acc[mt][0] = mma(a, bq[0][kq], acc[mt][0]);
-            acc[mt][1] = mma(a, bq[1][kq], acc[mt][1]);
+            acc[mt][0] = mma_in<F16>(a, bq[0][kq], acc[mt][0]);
+            acc[mt][1] = mma_in<F16>(a, bq[1][kq], acc[mt][1]);
         }
     }
     // acc[mt][ti][r] = a[m = 16 mt + 4 g + r][t = tb + 16 ti + c]
@@ -1039,40 +1039,51 @@ __global__ __launch_bounds__(256) void decoder_alpha_mfma(const bf16* __restrict
 using namespace mfma;
 
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
-                         float scale, const int32_t* tmask, void* alpha, float* lse, hipStream_t stream) {
+                         float scale, const int32_t* tmask, void* alpha, float* lse, bool f16in, hipStream_t stream) {
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "decoder_alpha_mfma: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     dim3 grid((unsigned)((N + 127) / 128), (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_DEC_ALPHA(MM, DD)                                                                          \
-    hipLaunchKernelGGL((decoder_alpha_mfma<MM, DD>), grid, dim3(256), 0, stream, (const bf16*)Qd,         \
+#define FLARE_DEC_ALPHA_T(MM, DD, F)                                                                     \
+    hipLaunchKernelGGL((decoder_alpha_mfma<MM, DD, F>), grid, dim3(256), 0, stream, (const bf16*)Qd,      \
                        (const bf16*)Kd, (int)N, (int)H, s2, tmask, (f16*)alpha, lse)
+#define FLARE_DEC_ALPHA(MM, DD)                        \
+    do {                                               \
+        if (f16in) FLARE_DEC_ALPHA_T(MM, DD, true);    \
+        else FLARE_DEC_ALPHA_T(MM, DD, false);         \
+    } while (0)
     if (M == 128 && D == 64) FLARE_DEC_ALPHA(128, 64);
     else if (M == 128 && D == 128) FLARE_DEC_ALPHA(128, 128);
     else if (M == 256 && D == 64) FLARE_DEC_ALPHA(256, 64);
     else FLARE_DEC_ALPHA(256, 128);
 #undef FLARE_DEC_ALPHA
+#undef FLARE_DEC_ALPHA_T
     return check_launch("decoder_alpha_mfma");
 }
 
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     hipStream_t stream) {
+                     bool f16in, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_OUT_PC_SEP(MM, DD, NW, SP)                                                                     \
-    hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW, SP>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
+#define FLARE_OUT_PC_SEP(MM, DD, NW, SP, F)                                                                  \
+    hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW, SP, F>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q, \
                        (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y,    \
                        out_dtype, tmask, (const f16*)alpha)
-#define FLARE_OUT_PC(MM, DD, NW)                   \
-    do {                                           \
-        if (alpha) FLARE_OUT_PC_SEP(MM, DD, NW, true);  \
-        else FLARE_OUT_PC_SEP(MM, DD, NW, false);       \
+#define FLARE_OUT_PC(MM, DD, NW)                                  \
+    do {                                                          \
+        if (f16in) {                                              \
+            if (alpha) FLARE_OUT_PC_SEP(MM, DD, NW, true, true);  \
+            else FLARE_OUT_PC_SEP(MM, DD, NW, false, true);       \
+        } else {                                                  \
+            if (alpha) FLARE_OUT_PC_SEP(MM, DD, NW, true, false); \
+            else FLARE_OUT_PC_SEP(MM, DD, NW, false, false);      \
+        }                                                         \
     } while (0)
     // The 128 x 64 bank runs 2 + 2 waves (72 KiB of LDS: two workgroups share a CU);
     // the larger banks 4 + 4 (one workgroup fills a CU).
@@ -1092,21 +1103,27 @@ using namespace mfma;
 
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      const int32_t* tmask, hipStream_t stream) {
+                      const int32_t* tmask, bool f16in, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_prepare_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_PREP_PC(MM, DD, NW)                                                                            \
-    hipLaunchKernelGGL((chunk_prepare_pc<MM, DD, NW>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,       \
+#define FLARE_PREP_PC_T(MM, DD, NW, F)                                                                       \
+    hipLaunchKernelGGL((chunk_prepare_pc<MM, DD, NW, F>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q,    \
                        (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, cmax, cden, cnum, tmask)
+#define FLARE_PREP_PC(MM, DD, NW)                         \
+    do {                                                  \
+        if (f16in) FLARE_PREP_PC_T(MM, DD, NW, true);     \
+        else FLARE_PREP_PC_T(MM, DD, NW, false);          \
+    } while (0)
     if (M == 128 && D == 64) FLARE_PREP_PC(128, 64, 2);
     else if (M == 128 && D == 128) FLARE_PREP_PC(128, 128, 4);
     else if (M == 256 && D == 64) FLARE_PREP_PC(256, 64, 4);
     else FLARE_PREP_PC(256, 128, 4);
 #undef FLARE_PREP_PC
+#undef FLARE_PREP_PC_T
     return check_launch("chunk_prepare_pc");
 }
 

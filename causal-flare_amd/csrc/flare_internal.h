@@ -10,15 +10,17 @@ int64_t default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 #include <stdlib.h>
 
 namespace flare {
+// bf16 inputs, or fp16 inputs on the producer / consumer kernels (M in {128, 256});
+// the launchers below take f16in = (dtype == FLARE_F16)
 bool mfma_prepare_supported(int dtype, int64_t M, int64_t Dk, int64_t Dv);
 bool mfma_output_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv);
 int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                         int64_t M, int64_t D, float scale, int64_t chunk, float* cmax, float* cden,
-                        float* cnum, hipStream_t stream);
+                        float* cnum, bool f16in, hipStream_t stream);
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
-                       hipStream_t stream);
+                       bool f16in, hipStream_t stream);
 
 // FLARE_DISABLE_MFMA=1 routes every shape to the scalar-fp32 kernels (A/B checks);
 // FLARE_MFMA_PHASES=<bits> keeps the MFMA kernel only for phase 1 (bit 0) and/or
@@ -44,15 +46,15 @@ inline bool output_pc_enabled() {
 }
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      const int32_t* tmask, hipStream_t stream);
+                      const int32_t* tmask, bool f16in, hipStream_t stream);
 // alpha: NULL for shared decoder weights; else the decoder softmax [B*H, N, M]
 // (fp16) written by launch_decoder_alpha, for separate Qdec / Kdec.
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     hipStream_t stream);
+                     bool f16in, hipStream_t stream);
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
-                         float scale, const int32_t* tmask, void* alpha, float* lse, hipStream_t stream);
+                         float scale, const int32_t* tmask, void* alpha, float* lse, bool f16in, hipStream_t stream);
 }  // namespace flare
 
 namespace flare {
@@ -60,7 +62,7 @@ bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, void* alpha, bool sep, hipStream_t stream);
+                            float* lse_dec, float* lse_enc, void* alpha, bool sep, bool f16in, hipStream_t stream);
 // true when the semi MFMA readout keeps a block's decoder softmax in LDS; otherwise
 // it needs a [B*H, N, M] fp16 alpha buffer in the workspace
 bool semi_alpha_in_lds(int64_t M, int64_t block);

@@ -32,6 +32,20 @@ __device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
 }
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Input tensors (Q, K, V and the decoder tensors) travel as raw 16-bit words in
+// bf16-typed storage; F16 selects the fp16 reading of those words for the MFMA
+// that consumes them and for conversions to float.
+template <bool F16>
+__device__ __forceinline__ f32x4 mma_in(bf16x8 a, bf16x8 b, f32x4 c) {
+    if constexpr (F16) return mma(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c);
+    else return mma(a, b, c);
+}
+template <bool F16>
+__device__ __forceinline__ float in_f32(bf16 x) {
+    if constexpr (F16) return (float)__builtin_bit_cast(f16, x);
+    else return (float)x;
+}
+
 // x = hi + lo, both halves of type TY.
 #define SPLIT2(TY, x, HI, LO)              \
     do {                                   \
@@ -167,6 +181,8 @@ __device__ __forceinline__ void store4(void* Y, size_t idx, f32x4 v, int out_dty
         bf16x4 o;
         o[0] = (bf16)v[0]; o[1] = (bf16)v[1]; o[2] = (bf16)v[2]; o[3] = (bf16)v[3];
         *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(Y) + idx) = o;
+    } else if (out_dtype == FLARE_F16) {
+        *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(Y) + idx) = __builtin_convertvector(v, f16x4);
     } else {
         *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(Y) + idx) = v;
     }
@@ -292,7 +308,7 @@ __device__ __forceinline__ void lds_barrier() {
 // One subtile of V[t0 .. t0+T) x [d0, d0+ND) held in registers, NTHR threads
 // of the group each holding NS 8-column slots, so that the next subtile can be
 // fetched from HBM while the current one is being used.
-template <int ND, int NTHR>
+template <int ND, int NTHR, bool F16 = false>
 struct VTile {
     static constexpr int SLOTS = T * ND / 8;
     static constexpr int NS = (SLOTS + NTHR - 1) / NTHR;
@@ -335,7 +351,7 @@ struct VTile {
                 slot(vi, tau, d8);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const float x = (float)v[k][e];
+                    const float x = in_f32<F16>(v[k][e]);
                     big = fmaxf(big, fabsf(x));
                     vt[(d0 + 8 * d8 + e) * P + tau] = (f16)x;
                 }
@@ -350,7 +366,7 @@ struct VTile {
         for (int k = 0; k < NS; ++k)
             if (SLOTS % NTHR == 0 || tid + k * NTHR < SLOTS)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) big = fmaxf(big, fabsf((float)v[k][e]));
+                for (int e = 0; e < 8; ++e) big = fmaxf(big, fabsf(in_f32<F16>(v[k][e])));
         return big;
     }
     // V^T[d][tau] (row pitch P) as fp16 of v * sc (sc a power of two).
@@ -363,7 +379,7 @@ struct VTile {
                 int tau, d8;
                 slot(vi, tau, d8);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = (f16)((float)v[k][e] * sc);
+                for (int e = 0; e < 8; ++e) vt[(d0 + 8 * d8 + e) * P + tau] = (f16)(in_f32<F16>(v[k][e]) * sc);
             }
         }
     }

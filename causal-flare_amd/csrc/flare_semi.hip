@@ -187,7 +187,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
         mfma_semi_supported(dtype, out_dtype, true, M, Dk, Dv, block) && mfma_prepare_supported(dtype, M, Dk, Dv)) {
         if (!shared) {
             const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, nullptr,
-                                                alpha_ws, lse_dec, s);
+                                                alpha_ws, lse_dec, dtype == FLARE_F16, s);
             if (rc) return rc;
         }
         // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
@@ -200,13 +200,13 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
         chunk = ((chunk + block - 1) / block) * block;
         if (chunk > N) chunk = N;
         const int64_t NC = (N + chunk - 1) / chunk;
-        int rc = launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, bmax, bden, bnum, s);
+        int rc = launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, bmax, bden, bnum, dtype == FLARE_F16, s);
         if (rc) return rc;
         rc = launch_prefix_public(bmax, bden, bnum, B * H, NC, M, Dv, nullptr, nullptr, nullptr, nullptr,
                                   nullptr, nullptr, s);
         if (rc) return rc;
         return launch_semi_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, block, bmax, bden, bnum, Y,
-                                       out_dtype, lse_dec, lse_enc, alpha_ws, !shared, s);
+                                       out_dtype, lse_dec, lse_enc, alpha_ws, !shared, dtype == FLARE_F16, s);
     }
     int rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, block, bmax, bden, bnum, s);
     if (rc) return rc;

@@ -48,7 +48,7 @@ struct SemiLayout {
 // the shared scores (or, with SEP, read as the decoder pass left it) and staged into
 // LDS one subtile at a time for the readout; the block is nsub = block / 32
 // subtiles at run time and NSUB is unused.
-template <int M, int D, int NW, int NSUB, bool SEP, bool GA>
+template <int M, int D, int NW, int NSUB, bool SEP, bool GA, bool F16>
 __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     const int t_end = min(N, t_begin + chunk);      // chunk and N are whole blocks
     const size_t stride = (size_t)H * D;
     const size_t row0 = (size_t)b * N * stride + (size_t)h * D;
-    VTile<L::DW, 64> vt;
+    VTile<L::DW, 64, F16> vt;
     vt.load(V, row0, stride, t_begin, t_end, dw0, lane);
     bf16x8 kb[2][L::KS];
 #pragma unroll
@@ -117,7 +117,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
     for (int blk0 = t_begin; blk0 < t_end; blk0 += blockT) {
         for (int j = 0; j < nsub; ++j) {
             const int t0 = blk0 + j * T;
-            const bool vbig = __any(vt.template store_f16<L::EP>(vtl, dw0, lane));
+            // (fp16 inputs are always in the fp16 range: no bf16 fallback)
+            const bool vbig = __any(vt.template store_f16<L::EP>(vtl, dw0, lane)) && !F16;
             vt.load(V, row0, stride, t0 + T, t_end, dw0, lane);
             // ---- S^T = Q K^T (log2 domain); prefetch the next subtile's K rows
             float s[L::MT][2][4];
@@ -131,7 +132,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                     for (int mi = 0; mi < L::MT; ++mi) {
                         const bf16x8 qa = load8<bf16x8>(qs + (mw0 + 16 * mi + c) * L::QP + 32 * ks + 8 * g);
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma(qa, kb[ti][ks], acc[mi][ti]);
+                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma_in<F16>(qa, kb[ti][ks], acc[mi][ti]);
                     }
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) {
@@ -372,9 +373,10 @@ using namespace mfma;
 // shared: true also for separate decoder tensors served through decoder_alpha_mfma
 bool mfma_semi_supported(int dtype, int out_dtype, bool shared, int64_t M, int64_t Dk, int64_t Dv,
                          int64_t block) {
-    if (!(dtype == FLARE_BF16 && shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256) &&
-          (out_dtype == FLARE_BF16 || out_dtype == FLARE_F32)))
-        return false;
+    const bool shape = shared && Dk == Dv && (Dk == 64 || Dk == 128) && (M == 128 || M == 256);
+    const bool bf = dtype == FLARE_BF16 && (out_dtype == FLARE_BF16 || out_dtype == FLARE_F32);
+    const bool hf = dtype == FLARE_F16 && (out_dtype == FLARE_F16 || out_dtype == FLARE_F32);
+    if (!(shape && (bf || hf))) return false;
     return block % 32 == 0;
 }
 
@@ -385,7 +387,7 @@ bool semi_alpha_in_lds(int64_t M, int64_t block) {
 int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                             int64_t M, int64_t D, float scale, int64_t chunk, int64_t block,
                             const float* pmax, const float* pden, const float* pnum, void* Y, int out_dtype,
-                            float* lse_dec, float* lse_enc, void* alpha, bool sep, hipStream_t stream) {
+                            float* lse_dec, float* lse_enc, void* alpha, bool sep, bool f16in, hipStream_t stream) {
     FLARE_REQUIRE(chunk % block == 0 && N % block == 0, "semi_output_mfma: chunk and N must be whole blocks");
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
@@ -394,7 +396,12 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
     FLARE_REQUIRE(block % T == 0 && (!ga || alpha) && (!sep || alpha),
                   "semi_output_mfma: block=%lld needs whole subtiles and an alpha buffer", (long long)block);
 #define FLARE_SEMI_MFMA_SEP(MM, DD, NWW, NS, SP, G)                                                        \
-    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS, SP, G>), grid, dim3(64 * NWW), 0, stream,       \
+    do {                                                                                                   \
+        if (f16in) FLARE_SEMI_MFMA_T(MM, DD, NWW, NS, SP, G, true);                                        \
+        else FLARE_SEMI_MFMA_T(MM, DD, NWW, NS, SP, G, false);                                             \
+    } while (0)
+#define FLARE_SEMI_MFMA_T(MM, DD, NWW, NS, SP, G, F)                                                       \
+    hipLaunchKernelGGL((semi_output_mfma<MM, DD, NWW, NS, SP, G, F>), grid, dim3(64 * NWW), 0, stream,    \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk,     \
                        pmax, pden, pnum, Y, out_dtype, lse_dec, lse_enc, (f16*)alpha, (int)(block / T))
 #define FLARE_SEMI_MFMA(MM, DD, NWW, NS)                                \
@@ -431,6 +438,7 @@ int launch_semi_output_mfma(const void* Q, const void* K, const void* V, int64_t
 #undef FLARE_SEMI_GA
 #undef FLARE_SEMI_MFMA
 #undef FLARE_SEMI_MFMA_SEP
+#undef FLARE_SEMI_MFMA_T
     return check_launch("semi_output_mfma");
 }
 

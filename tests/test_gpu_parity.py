@@ -528,3 +528,87 @@ def test_semi_ar_mfma_shapes_bf16(M, D, block):
     assert_parity(y, y_ref, torch.bfloat16, f"semi mfma M={M} D={D} block={block}")
     np.testing.assert_allclose(to_np(aux["LSE_dec"]), lse_dec, rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(to_np(aux["LSE_enc"]), lse_enc, rtol=1e-4, atol=1e-4)
+
+
+# --------------------------------------------------------------------------
+# fp16 inputs: the reference computes fp16 inputs in fp16 MMA
+# (_get_chunked_forward_config, training.py:315-326) with the 1e-2 bar of
+# _get_allclose_tols (_common.py:132-137); here they run on the same
+# producer / consumer MFMA kernels as bf16 (fp16 MFMA on the raw input words)
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("M,D,N,chunk", [(128, 64, 1000, None), (256, 128, 1000, None), (128, 128, 700, 64),
+                                         (256, 64, 700, 64)])
+def test_mfma_fp16_forward(M, D, N, chunk):
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_fp16", M, D, N, chunk)
+    B, H = 2, 2
+    q, k, v = seeded(71 + M + D, B, N, H, M, D, D, torch.float16, q_std=D ** -0.5, device=DEV)
+    y = flare_autoregressive_triton(q, k, v, chunk_size=chunk)
+    assert y.dtype == torch.float16
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    assert_parity(y, ref, torch.float16, f"mfma fp16 M={M} D={D} N={N} chunk={chunk}")
+
+
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("mode", ["sep_q", "both"])
+def test_mfma_fp16_separate_decoder(M, D, mode):
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_fp16_sep", M, D, mode)
+    B, N, H = 2, 1000, 2
+    q, k, v = seeded(43 + M + D, B, N, H, M, D, D, torch.float16, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(M + D + 1)
+    qd = torch.randn(B, N, H, D, generator=g).half()
+    kd = (torch.randn(H, M, D, generator=g) * D ** -0.5).half() if mode == "both" else None
+    dev = lambda t: None if t is None else t.to(DEV)
+    y = flare_autoregressive_triton(dev(q), dev(k), dev(v), Q_dec=dev(qd), K_dec=dev(kd))
+    ref = O.brute_ar(q, k, v, scale=D ** -0.5, Q_dec=qd, K_dec=kd)
+    assert_parity(y, ref, torch.float16, f"mfma fp16 sep M={M} D={D} {mode}")
+
+
+def test_masked_prefill_fp16():
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("masked_prefill_fp16")
+    B, T, H, M, D = 2, 700, 2, 128, 64
+    q, k, v = seeded(17, B, T, H, M, D, D, torch.float16, q_std=D ** -0.5)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[:, :40] = 0
+    mask[1, 300:333] = 0
+    y, st = flare_autoregressive_prefill_triton(q.to(DEV), k.to(DEV), v.to(DEV), attention_mask=mask.to(DEV))
+    y_ref, st_ref = O.ar_recurrent(q, k, v, attention_mask=mask, nthreads=16)
+    assert torch.all(y[mask == 0].float() == 0), "masked tokens must give y = 0"
+    assert_parity(y, y_ref, torch.float16, "masked prefill fp16")
+    assert_state_parity(st, st_ref, torch.float16, "masked prefill fp16")
+
+
+def test_mfma_fp16_large_values():
+    """Values near the fp16 limit: the output kernel's power-of-two V scale keeps the
+    numerator finite."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("mfma_fp16_large_values")
+    B, N, H, M, D = 1, 2000, 2, 128, 64
+    q, k, v = seeded(59, B, N, H, M, D, D, torch.float16, q_std=D ** -0.5)
+    v = v.float()
+    v[:, 500:510] = v[:, 500:510].sign() * 6e4
+    v = v.half()
+    y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), chunk_size=256)
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    a, b = to_np(y), np.asarray(ref, np.float64)
+    assert np.isfinite(a).all(), "non-finite output with large fp16 values"
+    assert_parity(y[:, :500], ref[:, :500], torch.float16, "mfma fp16 large values, before")
+    scale = np.abs(b[:, 500:]).max(axis=(1, 3), keepdims=True)
+    err = float((np.abs(a[:, 500:] - b[:, 500:]) / scale).max())
+    assert err <= 1e-2, f"mfma fp16 large values: max |err| / max |ref| = {err:.3e}"
+
+
+@pytest.mark.parametrize("M,D,block", [(128, 64, 64), (256, 128, 32), (256, 128, 128)])
+def test_semi_ar_mfma_fp16(M, D, block):
+    from causal_flare import flare_semi_autoregressive_trition
+    _print_case("semi_mfma_fp16", M, D, block)
+    B, N, H = 2, 1024, 2
+    q, k, v = seeded(97 + M + D + block, B, N, H, M, D, D, torch.float16, q_std=D ** -0.5, device=DEV)
+    y, aux = flare_semi_autoregressive_trition(q, k, v, block_size=block, chunk_size=32)
+    assert y.dtype == torch.float16
+    y_ref, lse_dec, lse_enc = O.semi_ar(q, k, v, block, 32, nthreads=16)
+    assert_parity(y, y_ref, torch.float16, f"semi mfma fp16 M={M} D={D} block={block}")
+    np.testing.assert_allclose(to_np(aux["LSE_dec"]), lse_dec, rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(to_np(aux["LSE_enc"]), lse_enc, rtol=1e-4, atol=1e-4)
