@@ -193,8 +193,10 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
         // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
         // block-causal MFMA readout.  The summaries fit in the workspace since
         // chunks are never shorter than blocks.
-        // ~2048 chunk workgroups (several per compute unit), whole blocks each
-        const int64_t target = (2048 + B * H - 1) / (B * H);
+        // ~512 chunk workgroups (one round at two per compute unit), whole blocks each:
+        // measured on config 5 (B*H = 32), 2048 / 1024 / 512 / 256 workgroups take
+        // 151 / 126 / 119 / 168 us, the shorter chunks paying in summary traffic
+        const int64_t target = (512 + B * H - 1) / (B * H);
         int64_t chunk = (N + target - 1) / target;
         if (chunk > 2048) chunk = 2048;
         chunk = ((chunk + block - 1) / block) * block;
