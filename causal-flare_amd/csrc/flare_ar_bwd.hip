@@ -682,14 +682,19 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ C,
     const float* __restrict__ X, const float* __restrict__ Ysum) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
-    __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
-    __shared__ __attribute__((aligned(16))) float vs[kBT * kGT];
+    // dY and V slabs; afterwards (bf16) v_t . X_m of one 16-token half as [m][17]
+    __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
+    float* gs = gsv;
+    float* vs = gsv + kBT * kGT;
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const bool carry = c + 1 < NC;
     const size_t rbase = ((size_t)bh * N + t0) * M;
+    // bf16 inputs with whole 16-latent / 32-column tiles: v . X on the MFMA
+    const bool mf = kBf16 && M % 16 == 0 && Dv % 32 == 0;
     float gv[kGVJ];
 #pragma unroll
     for (int j = 0; j < kGVJ; ++j) gv[j] = 0.0f;
@@ -704,13 +709,47 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
         stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
-        if (act && carry) {
+        if (act && carry && !mf) {
             for (int d = 0; d < ds; d += 4) {
                 const float4 p = ld4(xr + d0 + d);
 #pragma unroll
                 for (int t = 0; t < kBT; ++t) {
                     const float4 v4 = ld4(vs + t * kGT + d);
                     acc[t] += v4.x * p.x + v4.y * p.y + v4.z * p.z + v4.w * p.w;
+                }
+            }
+        }
+    }
+    if constexpr (kBf16) {
+        if (mf && carry) {
+            // D[m][t] = sum_d X[m][d] v[t][d] per 16-token half: A = X rows (fp32 as bf16
+            // hi + lo), B = V rows; through LDS to the thread of latent m
+            using namespace mfma;
+            const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+            for (int ti = 0; ti < kBT / 16; ++ti) {
+                __syncthreads();   // the slabs (or the previous half) are consumed
+                const int t = 16 * ti + cl;
+                const bf16* vrow = reinterpret_cast<const bf16*>(V) + tok_index(b, t0 + min(t, nt - 1), h, N, H, Dv) + 8 * g4;
+                for (int mt = w; mt < M / 16; mt += kBNT / 64) {
+                    f32x4 d2 = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const float* xrow = X + (((size_t)bh * NC + c) * M + 16 * mt + cl) * Dv + 8 * g4;
+                    for (int k0 = 0; k0 < Dv; k0 += 32) {
+                        const float4 p0 = ld4(xrow + k0), p1 = ld4(xrow + k0 + 4);
+                        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                        bf16x8 ph, pl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+                        const bf16x8 vb = t < nt ? load8<bf16x8>(vrow + k0) : zero8();
+                        d2 = mma(ph, vb, d2);
+                        d2 = mma(pl, vb, d2);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
+                }
+                __syncthreads();
+                if (act) {
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) acc[16 * ti + u] = gsv[m * 17 + u];
                 }
             }
         }
