@@ -628,7 +628,77 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token, per latent slab
         const float* lend = L + rbase + (size_t)(nt - 1) * M;
         const float* xb = X + ((size_t)bh * NC + c) * M * Dv;
-        for (int m0 = 0; m0 < M; m0 += 64) {
+        constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+        bool done = false;
+        if constexpr (kBf16) {
+            if (M % 32 == 0 && (Dv == 64 || Dv == 128)) {
+                // bf16 inputs: P X on the MFMA, P = e^{s - Lend} <= 1 and X both fp32 as
+                // bf16 hi + lo (three products); D[tau][d] through LDS (uni) to acc
+                using namespace mfma;
+                const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+                constexpr int kNjw = 2;                  // value tiles per wave (Dv <= 128)
+                f32x4 xa[kNjw][2];
+#pragma unroll
+                for (int q = 0; q < kNjw; ++q) xa[q][0] = xa[q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int m0 = 0; m0 < M; m0 += 32) {
+                    const float4 l0 = ld4(lend + m0 + 8 * g4), l1 = ld4(lend + m0 + 8 * g4 + 4);
+                    const float lv[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+                    bf16x8 ph[2], pl[2];
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti) {
+                        const int tau = 16 * ti + cl;
+                        float sv[8];
+                        if (tau < nt) {
+                            const float* srow = S + rbase + (size_t)tau * M + m0 + 8 * g4;
+                            const float4 s0 = ld4(srow), s1 = ld4(srow + 4);
+                            sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
+                            sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) sv[e] = ex2(sv[e] - lv[e]);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) sv[e] = 0.0f;
+                        }
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) SPLIT2(bf16, sv[e], ph[ti][e], pl[ti][e]);
+                    }
+#pragma unroll
+                    for (int q = 0; q < kNjw; ++q) {
+                        const int nj = w + 4 * q;
+                        if (16 * nj >= Dv) break;
+                        bf16x8 xh, xl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            SPLIT2(bf16, xb[(size_t)(m0 + 8 * g4 + e) * Dv + 16 * nj + cl], xh[e], xl[e]);
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) {
+                            xa[q][ti] = mma(ph[ti], xh, xa[q][ti]);
+                            xa[q][ti] = mma(ph[ti], xl, xa[q][ti]);
+                            xa[q][ti] = mma(pl[ti], xh, xa[q][ti]);
+                        }
+                    }
+                }
+                __syncthreads();   // uni is free (its last readers were before the slab loop)
+#pragma unroll
+                for (int q = 0; q < kNjw; ++q) {
+                    const int nj = w + 4 * q;
+                    if (16 * nj >= Dv) break;
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) uni[(16 * ti + 4 * g4 + r) * Dv + 16 * nj + cl] = xa[q][ti][r];
+                }
+                __syncthreads();
+#pragma unroll
+                for (int sl = 0; sl < kMaxVSlab; ++sl) {
+                    if (sl * kBSlab >= Dv) break;
+#pragma unroll
+                    for (int r = 0; r < kRT; ++r) acc[sl][r] += uni[(rg + 4 * r) * Dv + sl * kBSlab + col];
+                }
+                done = true;
+            }
+        }
+        for (int m0 = 0; m0 < (done ? 0 : M); m0 += 64) {
             const int mc = min(64, M - m0);
             __syncthreads();
             for (int e = tid; e < kBT * 64; e += kBNT) {
