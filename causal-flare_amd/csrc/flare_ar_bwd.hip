@@ -568,10 +568,83 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     constexpr int kNB = kBlockPairs;
     const int u = tid & 15, v = tid >> 4;
     for (int e = tid; e < kBT * kGT; e += kBNT) gl[e] = 0.0f;
+    // bf16 inputs, M in {128, 256}: G = E' W^T on the MFMA with the chunk's first-token
+    // L as per-latent reference c, E' = 2^(s - c) and W = 2^(c - LA) <= 1 (L grows
+    // along the chunk and LA >= L), one exponential per (token, latent) instead of one
+    // per pair.  A chunk whose scores pass c by more than 2^64 (E' near the fp32
+    // range) redoes G pair by pair below.
+    bool exact = true;
+    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+        if (M % 128 == 0) {
+            using namespace mfma;
+            __shared__ int big_any;
+            if (tid == 0) big_any = 0;
+            const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+            f32x4 gp[3] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+            bool big = false;
+            const int mw = M / 4;
+            for (int m0 = w * mw; m0 < (w + 1) * mw; m0 += 32) {
+                const float4 c0 = ld4(L + rbase + m0 + 8 * g4), c1 = ld4(L + rbase + m0 + 8 * g4 + 4);
+                const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                bf16x8 eh[2], el[2], wh[2], wl[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int row = 16 * q + cl;
+                    float ev[8], wv[8];
+                    if (row < nt) {
+                        const size_t o = rbase + (size_t)row * M + m0 + 8 * g4;
+                        const float4 s0 = ld4(S + o), s1 = ld4(S + o + 4), a0 = ld4(LA + o), a1 = ld4(LA + o + 4);
+                        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+                        const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            big |= sv[e] - cv[e] > 64.0f;
+                            ev[e] = ex2(sv[e] - cv[e]);
+                            wv[e] = ex2(cv[e] - av[e]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) ev[e] = wv[e] = 0.0f;
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        SPLIT2(bf16, ev[e], eh[q][e], el[q][e]);
+                        SPLIT2(bf16, wv[e], wh[q][e], wl[q][e]);
+                    }
+                }
+                // causal tile pairs (tau tile, t tile): (0, 0), (0, 1), (1, 1)
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    const int ti = k == 2 ? 1 : 0, tj = k == 0 ? 0 : 1;
+                    gp[k] = mma(eh[ti], wh[tj], gp[k]);
+                    gp[k] = mma(eh[ti], wl[tj], gp[k]);
+                    gp[k] = mma(el[ti], wh[tj], gp[k]);
+                }
+            }
+            if (__any(big) && lane == 0) big_any = 1;
+            // partial G of each wave (rows tau = 4 g + r, columns t = cl) -> summed in LDS
+            float* gpart = uni;   // [4 waves][3 tiles][16][16]
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gpart[((w * 3 + k) * 16 + 4 * g4 + r) * 16 + cl] = gp[k][r];
+            __syncthreads();
+            for (int e = tid; e < 3 * 256; e += kBNT) {
+                const int k = e >> 8, i = (e >> 4) & 15, j = e & 15;
+                const int tau = 16 * (k == 2 ? 1 : 0) + i, t = 16 * (k == 0 ? 0 : 1) + j;
+                float sum = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < 4; ++w2) sum += gpart[((w2 * 3 + k) * 16 + i) * 16 + j];
+                gl[tau * kGT + t] = t >= tau ? sum : 0.0f;
+            }
+            __syncthreads();
+            exact = big_any != 0;
+        }
+    }
     float g[kNB];
 #pragma unroll
     for (int k = 0; k < kNB; ++k) g[k] = 0.0f;
-    for (int m0 = 0; m0 < M; m0 += 64) {
+    for (int m0 = 0; m0 < (exact ? M : 0); m0 += 64) {
         const int mc = min(64, M - m0);
         __syncthreads();
         for (int e = tid; e < kBT * 64; e += kBNT) {
@@ -596,10 +669,12 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
             }
         }
     }
+    if (exact) {
 #pragma unroll
-    for (int k = 0; k < kNB; ++k) {
-        const int tau = 16 * kP.ib[k] + u, t = 16 * kP.jb[k] + v;
-        gl[tau * kGT + t] = (t >= tau) ? g[k] : 0.0f;
+        for (int k = 0; k < kNB; ++k) {
+            const int tau = 16 * kP.ib[k] + u, t = 16 * kP.jb[k] + v;
+            gl[tau * kGT + t] = (t >= tau) ? g[k] : 0.0f;
+        }
     }
     const int col = tid & 63, rg = tid >> 6;
     float acc[kMaxVSlab][kRT];

@@ -147,6 +147,24 @@ def test_backward_bf16(M, D, N, sep):
     _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 M={M} D={D} N={N} sep={sep}")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_backward_bf16_score_jump(M, D):
+    """A token whose scores pass the chunk's starting log-den by far more than 2^64
+    (one K row scaled by 300): the pair sums of that chunk take the exact per-pair
+    path instead of the factorised MFMA form."""
+    _case("bwd_bf16_jump", M, D)
+    N = 200
+    Q, K, V, Qd, Kd, G = _inputs(21, 1, N, 2, M, D, D, torch.bfloat16, False, False)
+    Q = (Q.float() / math.sqrt(D)).to(torch.bfloat16)
+    K = K.float()
+    K[:, 45] *= 300.0
+    K = K.to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    y, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    tol = 3e-2 if D >= 128 else 2e-2
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 jump M={M} D={D}")
+
+
 def test_backward_c_abi_rejects_bad_arguments():
     from causal_flare import _lib
     lib = _lib.lib()
