@@ -26,8 +26,11 @@
 //   then gy and the dQ / dK contractions (flare_ar_bwd.hip)
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "flare_common.h"
 #include "flare_internal.h"
+#include "flare_mfma.h"
 
 namespace flare {
 
@@ -69,9 +72,11 @@ struct BlockStates {
 
 // ---------------------------------------------------------------------------
 // semi_bwd_tok: s2 = scale log2(e) k.q, alpha = softmax_m(a), c = alpha gz with
-// gz_tm = dY_t . z_g,m.  Thread m; tokens in tiles of kSTok.
+// gz_tm = dY_t . z_g,m.  Thread m; tokens in tiles of kSTok.  MF (bf16 inputs,
+// whole 16-latent / 32-column tiles): the scores (exact) and dY . num (num as
+// bf16 hi + lo) on the MFMA, handed to the thread of latent m through LDS.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool MF>
 __global__ __launch_bounds__(kSNT) void semi_bwd_tok_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ Qd, const T* __restrict__ Kd,
     const T* __restrict__ dY, int N, int H, int M, int Dk, int Dv, int blk, float scale, bool shared, BlockStates st,
@@ -95,22 +100,74 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_tok_kernel(
         const int ni = min(kSTok, blk - i0);
         const int t0 = tb0 + i0;
         __syncthreads();
-        for (int e = tid; e < kSTok * Dk; e += kSNT) {
-            const int i = e / Dk, d = e % Dk;
-            const size_t gi = stok(b, t0 + i, h, N, H, Dk) + d;
-            kt[e] = i < ni ? to_f32(K[gi]) : 0.0f;
-            if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
-        }
-        for (int e = tid; e < kSTok * Dv; e += kSNT) {
-            const int i = e / Dv, d = e % Dv;
-            gt[e] = i < ni ? to_f32(dY[stok(b, t0 + i, h, N, H, Dv) + d]) : 0.0f;
+        if constexpr (MF) {
+            // D[m][token] for the encoder scores (at), decoder scores (kt) and dY . num (gt),
+            // each as [token][m]
+            using namespace mfma;
+            const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+            const bool ok = cl < ni;
+            const size_t krow = stok(b, t0 + min(cl, ni - 1), h, N, H, Dk) + 8 * g4;
+            const size_t grow = stok(b, t0 + min(cl, ni - 1), h, N, H, Dv) + 8 * g4;
+            for (int mt = w; mt < M / 16; mt += kSNT / 64) {
+                const size_t lrow = ((size_t)h * M + 16 * mt + cl) * Dk + 8 * g4;
+                f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, sd = f32x4{0.f, 0.f, 0.f, 0.f}, gzz = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int k0 = 0; k0 < Dk; k0 += 32) {
+                    se = mma(load8<bf16x8>(reinterpret_cast<const bf16*>(Q) + lrow + k0),
+                             ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(K) + krow + k0) : zero8(), se);
+                    if (!shared)
+                        sd = mma(load8<bf16x8>(reinterpret_cast<const bf16*>(Kd) + lrow + k0),
+                                 ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(Qd) + krow + k0) : zero8(), sd);
+                }
+                float zm, zd;
+                const float* zr;
+                st.get(bh, g, 16 * mt + cl, zm, zd, zr);
+                for (int k0 = 0; k0 < Dv; k0 += 32) {
+                    const float4 p0 = *reinterpret_cast<const float4*>(zr + k0 + 8 * g4);
+                    const float4 p1 = *reinterpret_cast<const float4*>(zr + k0 + 8 * g4 + 4);
+                    const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                    bf16x8 ph, pl;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+                    const bf16x8 gb = ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(dY) + grow + k0) : zero8();
+                    gzz = mma(ph, gb, gzz);
+                    gzz = mma(pl, gb, gzz);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int mm = 16 * mt + 4 * g4 + r;
+                    at[cl * M + mm] = se[r];
+                    if (!shared) kt[cl * M + mm] = sd[r];
+                    gt[cl * M + mm] = gzz[r];
+                }
+            }
+        } else {
+            for (int e = tid; e < kSTok * Dk; e += kSNT) {
+                const int i = e / Dk, d = e % Dk;
+                const size_t gi = stok(b, t0 + i, h, N, H, Dk) + d;
+                kt[e] = i < ni ? to_f32(K[gi]) : 0.0f;
+                if (!shared) qdt[e] = i < ni ? to_f32(Qd[gi]) : 0.0f;
+            }
+            for (int e = tid; e < kSTok * Dv; e += kSNT) {
+                const int i = e / Dv, d = e % Dv;
+                gt[e] = i < ni ? to_f32(dY[stok(b, t0 + i, h, N, H, Dv) + d]) : 0.0f;
+            }
         }
         __syncthreads();
-        float as[kSTok], aa[kSTok];
+        float as[kSTok], aa[kSTok], gzm[kSTok];
 #pragma unroll
-        for (int i = 0; i < kSTok; ++i) as[i] = aa[i] = 0.0f;
+        for (int i = 0; i < kSTok; ++i) as[i] = aa[i] = gzm[i] = 0.0f;
+        if constexpr (MF) {
+            if (act) {
+#pragma unroll
+                for (int i = 0; i < kSTok; ++i) {
+                    as[i] = at[i * M + m];
+                    if (!shared) aa[i] = kt[i * M + m];
+                    gzm[i] = gt[i * M + m];
+                }
+            }
+        }
         if (act) {
-            for (int d = 0; d < Dk; d += 4) {
+            for (int d = 0; d < (MF ? 0 : Dk); d += 4) {
                 const float q0 = to_f32(qrow[d]), q1 = to_f32(qrow[d + 1]), q2 = to_f32(qrow[d + 2]),
                             q3 = to_f32(qrow[d + 3]);
 #pragma unroll
@@ -154,8 +211,8 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_tok_kernel(
         if (!act) continue;
         float gz[kSTok];
 #pragma unroll
-        for (int i = 0; i < kSTok; ++i) gz[i] = 0.0f;
-        for (int d = 0; d < Dv; d += 4) {
+        for (int i = 0; i < kSTok; ++i) gz[i] = gzm[i];
+        for (int d = 0; d < (MF ? 0 : Dv); d += 4) {
             const float4 u = *reinterpret_cast<const float4*>(znum + d);
 #pragma unroll
             for (int i = 0; i < kSTok; ++i) {
@@ -439,8 +496,18 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
     if ((rc = launch_prefix_public(bm, bd, bn, BH, NB, M, Dv, nullptr, nullptr, nullptr, fm, fd, fu, s))) return rc;
     const BlockStates st{bm, bd, bn, fm, fd, fu, (int)NB, (int)M, (int)Dv};
     const dim3 gb((unsigned)NB, (unsigned)BH);
-    hipLaunchKernelGGL(semi_bwd_tok_kernel<T>, gb, dim3(kSNT), 0, s, q, k, qd, kd, static_cast<const T*>(dY), (int)N,
-                       (int)H, (int)M, (int)Dk, (int)Dv, (int)block, scale, shared, st, S, AL, C);
+    bool tok_mfma = false;
+    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+        tok_mfma = M % 16 == 0 && Dk % 32 == 0 && Dv % 32 == 0;
+        if (tok_mfma)
+            hipLaunchKernelGGL((semi_bwd_tok_kernel<T, true>), gb, dim3(kSNT), 0, s, q, k, qd, kd,
+                               static_cast<const T*>(dY), (int)N, (int)H, (int)M, (int)Dk, (int)Dv, (int)block, scale,
+                               shared, st, S, AL, C);
+    }
+    if (!tok_mfma)
+        hipLaunchKernelGGL((semi_bwd_tok_kernel<T, false>), gb, dim3(kSNT), 0, s, q, k, qd, kd,
+                           static_cast<const T*>(dY), (int)N, (int)H, (int)M, (int)Dk, (int)Dv, (int)block, scale,
+                           shared, st, S, AL, C);
     if ((rc = check_launch("semi_bwd_tok_kernel"))) return rc;
     hipLaunchKernelGGL(semi_bwd_dz_kernel<T>, gb, dim3(kSNT), 0, s, static_cast<const T*>(dY), (int)N, (int)H,
                        (int)M, (int)Dv, (int)block, (int)NB, AL, C, X, Yb);
