@@ -342,7 +342,108 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
     }
 }
 
+// Block sums of the block-causal backward (the bf16 MFMA form of semi_bwd_dz in
+// flare_semi_bwd.hip): dz_g[m][:] = sum_{t in g} alpha_tm g_t and Yb_g[m] = sum_t c_tm,
+// over the block's tokens in 32-token steps (alpha^T as bf16 hi + lo, g^T exact),
+// staged transposed in LDS as in bwd_summary_mfma.
+template <int MW, int DV>
+__global__ __launch_bounds__(256) void semi_dz_mfma(const bf16* __restrict__ dY, int N, int H, int blk,
+                                                    const float* __restrict__ AL, const float* __restrict__ C,
+                                                    float* __restrict__ X, float* __restrict__ Yb) {
+    constexpr int M = 64 * MW, NJ = DV / 16;
+    __shared__ __attribute__((aligned(16))) bf16 ah[M * kDqTP], alo[M * kDqTP];   // alpha^T hi, lo
+    __shared__ __attribute__((aligned(16))) bf16 gt[DV * kDqTP];                  // g^T
+    const int g = blockIdx.x, bh = blockIdx.y, NB = gridDim.x;
+    const int b = bh / H, h = bh % H, tid = threadIdx.x;
+    const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+    const int tb0 = g * blk;
+    const size_t sbase = ((size_t)bh * NB + g) * M;
+    const size_t stride = (size_t)H * DV;
+    const int mw0 = w * 16 * MW;
+    f32x4 acc[MW][NJ];
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float ysum = 0.0f;
+    for (int k0 = 0; k0 < blk; k0 += 32) {
+        const int nk = min(32, blk - k0);
+        __syncthreads();   // the previous step's operands are consumed
+        if (tid < M) {
+            const int m = tid;
+#pragma unroll
+            for (int t8 = 0; t8 < 4; ++t8) {
+                bf16x8 hi, lo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const int t = 8 * t8 + e;
+                    float av = 0.0f;
+                    if (t < nk) {
+                        const size_t o = ((size_t)bh * N + tb0 + k0 + t) * M + m;
+                        av = AL[o];
+                        ysum += C[o];
+                    }
+                    SPLIT2(bf16, av, hi[e], lo[e]);
+                }
+                *reinterpret_cast<bf16x8*>(ah + m * kDqTP + 8 * t8) = hi;
+                *reinterpret_cast<bf16x8*>(alo + m * kDqTP + 8 * t8) = lo;
+            }
+        }
+        for (int e = tid; e < DV * 8; e += 256) {
+            const int d = e % DV, tq = e / DV;
+            bf16x4 gv;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int t = 4 * tq + i;
+                gv[i] = t < nk ? dY[((size_t)b * N + tb0 + k0 + t) * stride + (size_t)h * DV + d] : (bf16)0.0f;
+            }
+            *reinterpret_cast<bf16x4*>(gt + d * kDqTP + 4 * tq) = gv;
+        }
+        __syncthreads();
+        bf16x8 bg[NJ];
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) bg[nj] = load8<bf16x8>(gt + (16 * nj + cl) * kDqTP + 8 * g4);
+#pragma unroll
+        for (int mi = 0; mi < MW; ++mi) {
+            const int row = (mw0 + 16 * mi + cl) * kDqTP + 8 * g4;
+            const bf16x8 a0 = load8<bf16x8>(ah + row), a1 = load8<bf16x8>(alo + row);
+#pragma unroll
+            for (int nj = 0; nj < NJ; ++nj) {
+                acc[mi][nj] = mma(a0, bg[nj], acc[mi][nj]);
+                acc[mi][nj] = mma(a1, bg[nj], acc[mi][nj]);
+            }
+        }
+    }
+    if (tid < M) Yb[sbase + tid] = ysum;
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) X[(sbase + mw0 + 16 * mi + 4 * g4 + r) * DV + 16 * nj + cl] = acc[mi][nj][r];
+}
+
 }  // namespace mfma
+
+int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t blk,
+                        const float* AL, const float* C, float* X, float* Yb, hipStream_t st) {
+    using namespace mfma;
+    FLARE_REQUIRE(bwd_summary_mfma_supported(M, Dv) && blk % 16 == 0 && N % blk == 0,
+                  "semi_dz_mfma: unsupported M=%lld Dv=%lld block=%lld", (long long)M, (long long)Dv, (long long)blk);
+    dim3 grid((unsigned)(N / blk), (unsigned)(B * H));
+#define FLARE_DZ(MW, DD)                                                                                   \
+    hipLaunchKernelGGL((semi_dz_mfma<MW, DD>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
+                       (int)blk, AL, C, X, Yb)
+#define FLARE_DZ_D(MW)              \
+    if (Dv == 64) FLARE_DZ(MW, 64); \
+    else FLARE_DZ(MW, 128);
+    if (M == 64) { FLARE_DZ_D(1) }
+    else if (M == 128) { FLARE_DZ_D(2) }
+    else { FLARE_DZ_D(4) }
+#undef FLARE_DZ_D
+#undef FLARE_DZ
+    return check_launch("semi_dz_mfma");
+}
 
 bool bwd_summary_mfma_supported(int64_t M, int64_t Dv) {
     return (M == 64 || M == 128 || M == 256) && (Dv == 64 || Dv == 128);

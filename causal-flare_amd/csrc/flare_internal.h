@@ -76,6 +76,9 @@ int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_
 bool bwd_summary_mfma_supported(int64_t M, int64_t Dv);
 int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
                         const float* AL, const float* C, float* a_out, float* b_out, hipStream_t st);
+// block sums dz_g, Yb_g of the block-causal backward (M and Dv as bwd_summary_mfma_supported)
+int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t blk,
+                        const float* AL, const float* C, float* X, float* Yb, hipStream_t st);
 bool bwd_dq_mfma_supported(int64_t M, int64_t Dk);
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,

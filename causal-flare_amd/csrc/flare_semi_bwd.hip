@@ -509,9 +509,13 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
                            static_cast<const T*>(dY), (int)N, (int)H, (int)M, (int)Dk, (int)Dv, (int)block, scale,
                            shared, st, S, AL, C);
     if ((rc = check_launch("semi_bwd_tok_kernel"))) return rc;
-    hipLaunchKernelGGL(semi_bwd_dz_kernel<T>, gb, dim3(kSNT), 0, s, static_cast<const T*>(dY), (int)N, (int)H,
-                       (int)M, (int)Dv, (int)block, (int)NB, AL, C, X, Yb);
-    if ((rc = check_launch("semi_bwd_dz_kernel"))) return rc;
+    if (std::is_same<T, __hip_bfloat16>::value && bwd_summary_mfma_supported(M, Dv)) {
+        if ((rc = launch_semi_dz_mfma(dY, B, N, H, M, Dv, block, AL, C, X, Yb, s))) return rc;
+    } else {
+        hipLaunchKernelGGL(semi_bwd_dz_kernel<T>, gb, dim3(kSNT), 0, s, static_cast<const T*>(dY), (int)N, (int)H,
+                           (int)M, (int)Dv, (int)block, (int)NB, AL, C, X, Yb);
+        if ((rc = check_launch("semi_bwd_dz_kernel"))) return rc;
+    }
     const int64_t cthreads = BH * M * (Dv / 4);
     hipLaunchKernelGGL(semi_bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, s, X, Yb, st,
                        (int)NB, (int)M, (int)Dv, BH * M);
