@@ -398,7 +398,7 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_dv_kernel(int N, int H, int M, 
 // semi_bwd_ds: ds_tau m = e^{s_tau m - L_g,m} (v_tau . X_g,m - Y_g,m), written
 // over s.  Thread m; value tiles of kSTok tokens staged in LDS.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool MF>
 __global__ __launch_bounds__(kSNT) void semi_bwd_ds_kernel(const T* __restrict__ V, int N, int H, int M, int Dv,
                                                            int blk, int NB, float* __restrict__ S, BlockStates st,
                                                            const float* __restrict__ X,
@@ -415,16 +415,41 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_ds_kernel(const T* __restrict__
     for (int i0 = 0; i0 < blk; i0 += kSTok) {
         const int ni = min(kSTok, blk - i0);
         __syncthreads();
-        for (int e = tid; e < kSTok * Dv; e += kSNT) {
-            const int i = e / Dv, d = e % Dv;
-            vt[e] = i < ni ? to_f32(V[stok(b, tb0 + i0 + i, h, N, H, Dv) + d]) : 0.0f;
+        if constexpr (MF) {
+            // D[m][token] = X[m] . v_token (X as bf16 hi + lo, V exact) to LDS as [token][m]
+            using namespace mfma;
+            const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+            const bool ok = cl < ni;
+            const bf16* vrow = reinterpret_cast<const bf16*>(V) + stok(b, tb0 + i0 + min(cl, ni - 1), h, N, H, Dv) + 8 * g4;
+            for (int mt = w; mt < M / 16; mt += kSNT / 64) {
+                const float* xrow = X + (((size_t)bh * NB + g) * M + 16 * mt + cl) * Dv + 8 * g4;
+                f32x4 d2 = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int k0 = 0; k0 < Dv; k0 += 32) {
+                    const float4 p0 = *reinterpret_cast<const float4*>(xrow + k0);
+                    const float4 p1 = *reinterpret_cast<const float4*>(xrow + k0 + 4);
+                    const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                    bf16x8 ph, pl;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+                    const bf16x8 vb = ok ? load8<bf16x8>(vrow + k0) : zero8();
+                    d2 = mma(ph, vb, d2);
+                    d2 = mma(pl, vb, d2);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) vt[cl * M + 16 * mt + 4 * g4 + r] = d2[r];
+            }
+        } else {
+            for (int e = tid; e < kSTok * Dv; e += kSNT) {
+                const int i = e / Dv, d = e % Dv;
+                vt[e] = i < ni ? to_f32(V[stok(b, tb0 + i0 + i, h, N, H, Dv) + d]) : 0.0f;
+            }
         }
         __syncthreads();
         if (!act) continue;
         float vx[kSTok];
 #pragma unroll
-        for (int i = 0; i < kSTok; ++i) vx[i] = 0.0f;
-        for (int d = 0; d < Dv; d += 4) {
+        for (int i = 0; i < kSTok; ++i) vx[i] = MF ? vt[i * M + m] : 0.0f;
+        for (int d = 0; d < (MF ? 0 : Dv); d += 4) {
             const float4 x = *reinterpret_cast<const float4*>(xr + d);
 #pragma unroll
             for (int i = 0; i < kSTok; ++i) {
@@ -524,8 +549,16 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
                        dim3(kSNT), 0, s, (int)N, (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X,
                        static_cast<T*>(dV));
     if ((rc = check_launch("semi_bwd_dv_kernel"))) return rc;
-    hipLaunchKernelGGL(semi_bwd_ds_kernel<T>, gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N, (int)H,
-                       (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
+    bool ds_mfma = false;
+    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+        ds_mfma = M % 16 == 0 && Dv % 32 == 0;
+        if (ds_mfma)
+            hipLaunchKernelGGL((semi_bwd_ds_kernel<T, true>), gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N,
+                               (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
+    }
+    if (!ds_mfma)
+        hipLaunchKernelGGL((semi_bwd_ds_kernel<T, false>), gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N,
+                           (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
     if ((rc = check_launch("semi_bwd_ds_kernel"))) return rc;
     if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, gy, s))) return rc;
     return launch_bwd_contract(Q, K, Qdec, Kdec, dtype, B, N, H, M, Dk, scale, S, AL, C, gy, dQ, dK, dQd, dKd, P1,
