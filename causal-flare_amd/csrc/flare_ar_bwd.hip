@@ -568,13 +568,13 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     constexpr int kNB = kBlockPairs;
     const int u = tid & 15, v = tid >> 4;
     for (int e = tid; e < kBT * kGT; e += kBNT) gl[e] = 0.0f;
-    // bf16 inputs, M in {128, 256}: G = E' W^T on the MFMA with the chunk's first-token
+    // bf16 / fp16 inputs, M in {128, 256}: G = E' W^T on the MFMA with the chunk's first-token
     // L as per-latent reference c, E' = 2^(s - c) and W = 2^(c - LA) <= 1 (L grows
     // along the chunk and LA >= L), one exponential per (token, latent) instead of one
     // per pair.  A chunk whose scores pass c by more than 2^64 (E' near the fp32
     // range) redoes G pair by pair below.
     bool exact = true;
-    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+    if constexpr (!std::is_same<T, float>::value) {
         if (M % 128 == 0) {
             using namespace mfma;
             __shared__ int big_any;
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         // e^{s_tau m - Lend_m}, Lend = L at the chunk's last token, per latent slab
         const float* lend = L + rbase + (size_t)(nt - 1) * M;
         const float* xb = X + ((size_t)bh * NC + c) * M * Dv;
-        constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+        constexpr bool kBf16 = !std::is_same<T, float>::value;   // 16-bit inputs (operands here are fp32 intermediates)
         bool done = false;
         if constexpr (kBf16) {
             if (M % 32 == 0 && (Dv == 64 || Dv == 128)) {

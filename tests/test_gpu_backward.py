@@ -165,6 +165,23 @@ def test_backward_bf16_score_jump(M, D):
     _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 jump M={M} D={D}")
 
 
+@pytest.mark.parametrize("M,D,N", [(128, 64, 300), (256, 128, 200)])
+@pytest.mark.parametrize("sep", [(False, False), (True, True)])
+def test_backward_fp16(M, D, N, sep):
+    """fp16 inputs (computed in fp16 by the reference, training.py:315-326), bar of
+    _get_allclose_tols for 16-bit inputs with the D >= 128 allowance."""
+    _case("bwd_fp16", M, D, N, sep)
+    Q, K, V, Qd, Kd, G = _inputs(19, 1, N, 2, M, D, D, torch.float16, *sep)
+    Q = (Q.float() / math.sqrt(D)).to(torch.float16)
+    if Kd is not None:
+        Kd = (Kd.float() / math.sqrt(D)).to(torch.float16)
+    scale = 1.0 / math.sqrt(D)
+    y, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    assert y.dtype == torch.float16 and all(g is None or g.dtype == torch.float16 for g in grads)
+    tol = 3e-2 if D >= 128 else 2e-2
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"fp16 M={M} D={D} N={N} sep={sep}")
+
+
 def test_backward_c_abi_rejects_bad_arguments():
     from causal_flare import _lib
     lib = _lib.lib()
@@ -255,6 +272,17 @@ def test_semi_backward_reference_shape_bf16(sep):
             continue
         torch.testing.assert_close(g.cpu().double(), torch.as_tensor(r), rtol=2e-2, atol=2e-2,
                                    msg=lambda m: f"semi {name}: {m}")
+
+
+def test_semi_backward_fp16():
+    """Block-causal backward with fp16 inputs, the reference's 16-bit bar."""
+    _case("semi_bwd_fp16")
+    Q, K, V, Qd, Kd, G = _inputs(8, 1, 256, 2, 128, 64, 64, torch.float16, False, False)
+    Q = (Q.float() / 8.0).to(torch.float16)
+    scale = 64 ** -0.5
+    _, grads = _run_semi(Q, K, V, Qd, Kd, G, 64, scale)
+    ref = O.semi_grads(Q, K, V, G, 64, scale, Qd, Kd)
+    _check(grads, ref, 2e-2, "semi fp16")
 
 
 @pytest.mark.parametrize("block", [16, 64])
