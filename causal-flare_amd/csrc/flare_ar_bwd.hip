@@ -95,7 +95,7 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     // MF (bf16 inputs with whole 16-latent / 32-column tiles): the scores on the
     // MFMA (exact: bf16 products, fp32 sums), written to LDS as [token][m]
     // (encoder in at, decoder in kt) for the thread of latent m
-    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value;   // 16-bit inputs
     constexpr bool mf = kBf16 && MF;
     for (int i0 = 0; i0 < nt; i0 += kBTok) {
         const int ni = min(kBTok, nt - i0);
@@ -114,8 +114,8 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
                     const bf16* kdr = reinterpret_cast<const bf16*>(Kd) + lrow;
                     f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, sd = f32x4{0.f, 0.f, 0.f, 0.f};
                     for (int k0 = 0; k0 < Dk; k0 += 32) {
-                        se = mma(load8<bf16x8>(qr + k0), ok ? load8<bf16x8>(kr + k0) : zero8(), se);
-                        if (!shared) sd = mma(load8<bf16x8>(kdr + k0), ok ? load8<bf16x8>(qdr + k0) : zero8(), sd);
+                        se = mma_in<std::is_same<T, __half>::value>(load8<bf16x8>(qr + k0), ok ? load8<bf16x8>(kr + k0) : zero8(), se);
+                        if (!shared) sd = mma_in<std::is_same<T, __half>::value>(load8<bf16x8>(kdr + k0), ok ? load8<bf16x8>(qdr + k0) : zero8(), sd);
                     }
                     // D[m = 16 mt + 4 g + r][token cl]
 #pragma unroll
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     static_assert(2 * kBT * kGT >= 256 * 17, "g . pu half tile must fit in the slab staging");
     float* gs = gsv;
     float* vs = gsv + kBT * kGT;
-    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value;   // 16-bit inputs
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
@@ -316,8 +316,7 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
 #pragma unroll
                         for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
                         const bf16x8 gb = t < nt ? load8<bf16x8>(grow + k0) : zero8();
-                        d2 = mma(ph, gb, d2);
-                        d2 = mma(pl, gb, d2);
+                        d2 = mma_split<std::is_same<T, __half>::value>(ph, pl, gb, d2);
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
@@ -831,7 +830,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
     float* gs = gsv;
     float* vs = gsv + kBT * kGT;
-    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value;
+    constexpr bool kBf16 = std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value;   // 16-bit inputs
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
     const bool act = m < M;
@@ -885,8 +884,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 #pragma unroll
                         for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
                         const bf16x8 vb = t < nt ? load8<bf16x8>(vrow + k0) : zero8();
-                        d2 = mma(ph, vb, d2);
-                        d2 = mma(pl, vb, d2);
+                        d2 = mma_split<std::is_same<T, __half>::value>(ph, pl, vb, d2);
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
@@ -1107,16 +1105,19 @@ static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, boo
                            float* P2, hipStream_t st) {
     const int64_t BH = B * H, NG = (N + kBGroup - 1) / kBGroup;
     int rc;
-    if (std::is_same<T, __hip_bfloat16>::value && bwd_dk_mfma_supported(M, Dk)) {
-        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dK, dQd, st))) return rc;
+    constexpr bool kHalf = std::is_same<T, __half>::value;
+    constexpr bool k16 = std::is_same<T, __hip_bfloat16>::value || kHalf;
+    if (k16 && bwd_dk_mfma_supported(M, Dk)) {
+        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dK, dQd, kHalf, st)))
+            return rc;
     } else {
         hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT),
                            0, st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
                            static_cast<T*>(dK), static_cast<T*>(dQd));
         if ((rc = check_launch("bwd_dk_kernel"))) return rc;
     }
-    if (std::is_same<T, __hip_bfloat16>::value && bwd_dq_mfma_supported(M, Dk)) {
-        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, P1, P2, st))) return rc;
+    if (k16 && bwd_dq_mfma_supported(M, Dk)) {
+        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, P1, P2, kHalf, st))) return rc;
     } else {
         hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
                            dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
@@ -1230,7 +1231,7 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
         return rc;
     const dim3 gc((unsigned)NC, (unsigned)BH);
     bool stats_mfma = false;
-    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+    if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
         stats_mfma = M % 16 == 0 && Dk % 32 == 0;
         if (stats_mfma)
             hipLaunchKernelGGL((bwd_stats_kernel<T, true>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H,
@@ -1245,8 +1246,10 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     if ((rc = check_launch("bwd_gz_kernel"))) return rc;
     if ((rc = launch_gy(dy, y, B, N, H, Dv, gy, st))) return rc;
     static_assert(kBT == 32, "the MFMA chunk summary assumes 32-token chunks");
-    if (std::is_same<T, __hip_bfloat16>::value && bwd_summary_mfma_supported(M, Dv)) {
-        if ((rc = launch_summary_mfma(dy, B, N, H, M, Dv, L, AL, C, pn, pd, st))) return rc;
+    if ((std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) &&
+        bwd_summary_mfma_supported(M, Dv)) {
+        if ((rc = launch_summary_mfma(dy, B, N, H, M, Dv, L, AL, C, pn, pd, std::is_same<T, __half>::value, st)))
+            return rc;
     } else {
         hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
                            (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);

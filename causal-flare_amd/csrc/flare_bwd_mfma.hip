@@ -27,7 +27,7 @@ __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
 
 // TWO_B: a second latent tensor Kd (transposed in LDS) multiplies da
 // TWO_OUT: da goes to a second output dQd instead of into dK
-template <int DK, bool TWO_B, bool TWO_OUT>
+template <int DK, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, const bf16* __restrict__ Kd, int N,
                                                    int H, int M, float scale, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
@@ -102,8 +102,7 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
             split8(ds, sh, sl);
 #pragma unroll
             for (int nj = 0; nj < NJ; ++nj) {
-                acc[ti][nj] = mma(sh, bq[nj], acc[ti][nj]);
-                acc[ti][nj] = mma(sl, bq[nj], acc[ti][nj]);
+                acc[ti][nj] = mma_split<F16>(sh, sl, bq[nj], acc[ti][nj]);
             }
             if constexpr (TWO_B || TWO_OUT) {
                 bf16x8 ah, alo;
@@ -112,11 +111,9 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
                 for (int nj = 0; nj < NJ; ++nj) {
                     const bf16x8 bb = TWO_B ? bk[nj] : bq[nj];
                     if constexpr (TWO_OUT) {
-                        acc2[ti][nj] = mma(ah, bb, acc2[ti][nj]);
-                        acc2[ti][nj] = mma(alo, bb, acc2[ti][nj]);
+                        acc2[ti][nj] = mma_split<F16>(ah, alo, bb, acc2[ti][nj]);
                     } else {
-                        acc[ti][nj] = mma(ah, bb, acc[ti][nj]);
-                        acc[ti][nj] = mma(alo, bb, acc[ti][nj]);
+                        acc[ti][nj] = mma_split<F16>(ah, alo, bb, acc[ti][nj]);
                     }
                 }
             }
@@ -133,8 +130,14 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
             const size_t o = ((size_t)b * N + t) * stride + (size_t)h * DK + c;
 #pragma unroll
             for (int nj = 0; nj < NJ; ++nj) {
-                dK[o + 16 * nj] = __float2bfloat16(scale * acc[ti][nj][r]);
-                if constexpr (TWO_OUT) dQd[o + 16 * nj] = __float2bfloat16(scale * acc2[ti][nj][r]);
+                // outputs in the input dtype (the pointers are bf16-typed 16-bit storage)
+                if constexpr (F16) {
+                    reinterpret_cast<f16*>(dK)[o + 16 * nj] = (f16)(scale * acc[ti][nj][r]);
+                    if constexpr (TWO_OUT) reinterpret_cast<f16*>(dQd)[o + 16 * nj] = (f16)(scale * acc2[ti][nj][r]);
+                } else {
+                    dK[o + 16 * nj] = __float2bfloat16(scale * acc[ti][nj][r]);
+                    if constexpr (TWO_OUT) dQd[o + 16 * nj] = __float2bfloat16(scale * acc2[ti][nj][r]);
+                }
             }
         }
 }
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
 constexpr int kDqGroup = kBwdGroup;
 constexpr int kDqTP = 32 + 8;       // padded row of the transposed subtiles
 
-template <int MW, int DKS, bool TWO_A, bool TWO_B, bool TWO_OUT>
+template <int MW, int DKS, bool TWO_A, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, const bf16* __restrict__ Qd, int N,
                                                    int H, int Dk, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
@@ -232,8 +235,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
             const bf16x8 a0 = load8<bf16x8>(sh + row), a1 = load8<bf16x8>(sl + row);
 #pragma unroll
             for (int nj = 0; nj < NJ; ++nj) {
-                acc[mi][nj] = mma(a0, bk[nj], acc[mi][nj]);
-                acc[mi][nj] = mma(a1, bk[nj], acc[mi][nj]);
+                acc[mi][nj] = mma_split<F16>(a0, a1, bk[nj], acc[mi][nj]);
             }
             if constexpr (TWO_A) {
                 const bf16x8 e0 = load8<bf16x8>(ah + row), e1 = load8<bf16x8>(alo + row);
@@ -241,11 +243,9 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
                 for (int nj = 0; nj < NJ; ++nj) {
                     const bf16x8 bb = TWO_B ? bq[nj] : bk[nj];
                     if constexpr (TWO_OUT) {
-                        acc2[mi][nj] = mma(e0, bb, acc2[mi][nj]);
-                        acc2[mi][nj] = mma(e1, bb, acc2[mi][nj]);
+                        acc2[mi][nj] = mma_split<F16>(e0, e1, bb, acc2[mi][nj]);
                     } else {
-                        acc[mi][nj] = mma(e0, bb, acc[mi][nj]);
-                        acc[mi][nj] = mma(e1, bb, acc[mi][nj]);
+                        acc[mi][nj] = mma_split<F16>(e0, e1, bb, acc[mi][nj]);
                     }
                 }
             }
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
 //     w_tm = 2^(Lpre_m - L_tm) alpha_tm   (Lpre = L at the last token of chunk c-1)
 // a is a contraction over tokens: w^T (bf16 hi and lo, computed by the thread of
 // latent m) and g^T (dY, exact) are staged transposed in LDS.
-template <int MW, int DV>
+template <int MW, int DV, bool F16>
 __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__ dY, int N, int H,
                                                         const float* __restrict__ L, const float* __restrict__ AL,
                                                         const float* __restrict__ C, float* __restrict__ a_out,
@@ -333,8 +333,7 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
 #pragma unroll
         for (int nj = 0; nj < NJ; ++nj) {
             f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-            acc = mma(a0, bg[nj], acc);
-            acc = mma(a1, bg[nj], acc);
+            acc = mma_split<F16>(a0, a1, bg[nj], acc);
             // rows m = mw0 + 16 mi + 4 g + r, column 16 nj + cl
 #pragma unroll
             for (int r = 0; r < 4; ++r) a_out[(sbase + mw0 + 16 * mi + 4 * g + r) * DV + 16 * nj + cl] = acc[r];
@@ -346,7 +345,7 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
 // flare_semi_bwd.hip): dz_g[m][:] = sum_{t in g} alpha_tm g_t and Yb_g[m] = sum_t c_tm,
 // over the block's tokens in 32-token steps (alpha^T as bf16 hi + lo, g^T exact),
 // staged transposed in LDS as in bwd_summary_mfma.
-template <int MW, int DV>
+template <int MW, int DV, bool F16>
 __global__ __launch_bounds__(256) void semi_dz_mfma(const bf16* __restrict__ dY, int N, int H, int blk,
                                                     const float* __restrict__ AL, const float* __restrict__ C,
                                                     float* __restrict__ X, float* __restrict__ Yb) {
@@ -409,8 +408,7 @@ __global__ __launch_bounds__(256) void semi_dz_mfma(const bf16* __restrict__ dY,
             const bf16x8 a0 = load8<bf16x8>(ah + row), a1 = load8<bf16x8>(alo + row);
 #pragma unroll
             for (int nj = 0; nj < NJ; ++nj) {
-                acc[mi][nj] = mma(a0, bg[nj], acc[mi][nj]);
-                acc[mi][nj] = mma(a1, bg[nj], acc[mi][nj]);
+                acc[mi][nj] = mma_split<F16>(a0, a1, bg[nj], acc[mi][nj]);
             }
         }
     }
@@ -426,14 +424,19 @@ __global__ __launch_bounds__(256) void semi_dz_mfma(const bf16* __restrict__ dY,
 }  // namespace mfma
 
 int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t blk,
-                        const float* AL, const float* C, float* X, float* Yb, hipStream_t st) {
+                        const float* AL, const float* C, float* X, float* Yb, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_summary_mfma_supported(M, Dv) && blk % 16 == 0 && N % blk == 0,
                   "semi_dz_mfma: unsupported M=%lld Dv=%lld block=%lld", (long long)M, (long long)Dv, (long long)blk);
     dim3 grid((unsigned)(N / blk), (unsigned)(B * H));
-#define FLARE_DZ(MW, DD)                                                                                   \
-    hipLaunchKernelGGL((semi_dz_mfma<MW, DD>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
+#define FLARE_DZ_T(MW, DD, F)                                                                              \
+    hipLaunchKernelGGL((semi_dz_mfma<MW, DD, F>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
                        (int)blk, AL, C, X, Yb)
+#define FLARE_DZ(MW, DD)                        \
+    do {                                        \
+        if (f16in) FLARE_DZ_T(MW, DD, true);    \
+        else FLARE_DZ_T(MW, DD, false);         \
+    } while (0)
 #define FLARE_DZ_D(MW)              \
     if (Dv == 64) FLARE_DZ(MW, 64); \
     else FLARE_DZ(MW, 128);
@@ -442,6 +445,7 @@ int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t
     else { FLARE_DZ_D(4) }
 #undef FLARE_DZ_D
 #undef FLARE_DZ
+#undef FLARE_DZ_T
     return check_launch("semi_dz_mfma");
 }
 
@@ -450,14 +454,19 @@ bool bwd_summary_mfma_supported(int64_t M, int64_t Dv) {
 }
 
 int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
-                        const float* AL, const float* C, float* a_out, float* b_out, hipStream_t st) {
+                        const float* AL, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_summary_mfma_supported(M, Dv), "bwd_summary_mfma: unsupported M=%lld Dv=%lld",
                   (long long)M, (long long)Dv);
     dim3 grid((unsigned)((N + 31) / 32), (unsigned)(B * H));
-#define FLARE_SUM(MW, DD)                                                                                \
-    hipLaunchKernelGGL((bwd_summary_mfma<MW, DD>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
+#define FLARE_SUM_T(MW, DD, F)                                                                              \
+    hipLaunchKernelGGL((bwd_summary_mfma<MW, DD, F>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
                        L, AL, C, a_out, b_out)
+#define FLARE_SUM(MW, DD)                        \
+    do {                                         \
+        if (f16in) FLARE_SUM_T(MW, DD, true);    \
+        else FLARE_SUM_T(MW, DD, false);         \
+    } while (0)
 #define FLARE_SUM_D(MW)              \
     if (Dv == 64) FLARE_SUM(MW, 64); \
     else FLARE_SUM(MW, 128);
@@ -466,6 +475,7 @@ int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t
     else { FLARE_SUM_D(4) }
 #undef FLARE_SUM_D
 #undef FLARE_SUM
+#undef FLARE_SUM_T
     return check_launch("bwd_summary_mfma");
 }
 
@@ -476,7 +486,7 @@ bool bwd_dq_mfma_supported(int64_t M, int64_t Dk) {
 // partial sums per group of 512 tokens into P1 (and P2 when sep_k), as bwd_dq_kernel
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
-                   float* P1, float* P2, hipStream_t st) {
+                   float* P1, float* P2, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dq_mfma_supported(M, Dk), "bwd_dq_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
@@ -484,9 +494,14 @@ int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_
     // two accumulator sets (sep_k) keep 64 columns per workgroup
     const int dks = sep_k ? 64 : (int)Dk;
     dim3 grid((unsigned)NG, (unsigned)(B * H), (unsigned)(Dk / dks));
-#define FLARE_DQ(MW, DKS, TA, TB, TO)                                                                          \
-    hipLaunchKernelGGL((bwd_dq_mfma<MW, DKS, TA, TB, TO>), grid, dim3(256), 0, st, (const bf16*)K,            \
+#define FLARE_DQ_T(MW, DKS, TA, TB, TO, F)                                                                     \
+    hipLaunchKernelGGL((bwd_dq_mfma<MW, DKS, TA, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)K,         \
                        (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, P1, P2)
+#define FLARE_DQ(MW, DKS, TA, TB, TO)                          \
+    do {                                                       \
+        if (f16in) FLARE_DQ_T(MW, DKS, TA, TB, TO, true);      \
+        else FLARE_DQ_T(MW, DKS, TA, TB, TO, false);           \
+    } while (0)
 #define FLARE_DQ_MODES(MW, DKS)                                                          \
     if (sep_k) {                                                                        \
         if (sep_q) FLARE_DQ(MW, 64, true, true, true);                                  \
@@ -504,6 +519,7 @@ int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_
 #undef FLARE_DQ_D
 #undef FLARE_DQ_MODES
 #undef FLARE_DQ
+#undef FLARE_DQ_T
     return check_launch("bwd_dq_mfma");
 }
 
@@ -514,14 +530,19 @@ bool bwd_dk_mfma_supported(int64_t M, int64_t Dk) {
 // sep_q: dQd is its own output; sep_k: Kd is not Q (Q / Kd as in bwd_dk_kernel)
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
-                   const float* gy, void* dK, void* dQd, hipStream_t st) {
+                   const float* gy, void* dK, void* dQd, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dk_mfma_supported(M, Dk), "bwd_dk_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
     dim3 grid((unsigned)((N + kDkMfmaTok - 1) / kDkMfmaTok), (unsigned)(B * H));
-#define FLARE_DK(DD, TB, TO)                                                                                   \
-    hipLaunchKernelGGL((bwd_dk_mfma<DD, TB, TO>), grid, dim3(256), 0, st, (const bf16*)Q, (const bf16*)Kd,     \
+#define FLARE_DK_T(DD, TB, TO, F)                                                                              \
+    hipLaunchKernelGGL((bwd_dk_mfma<DD, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)Q, (const bf16*)Kd,  \
                        (int)N, (int)H, (int)M, scale, DS, AL, C, gy, (__hip_bfloat16*)dK, (__hip_bfloat16*)dQd)
+#define FLARE_DK(DD, TB, TO)                          \
+    do {                                              \
+        if (f16in) FLARE_DK_T(DD, TB, TO, true);      \
+        else FLARE_DK_T(DD, TB, TO, false);           \
+    } while (0)
 #define FLARE_DK_MODES(DD)                                          \
     if (sep_q) {                                                   \
         if (sep_k) FLARE_DK(DD, true, true);                       \
@@ -534,6 +555,7 @@ int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_
     else { FLARE_DK_MODES(128) }
 #undef FLARE_DK_MODES
 #undef FLARE_DK
+#undef FLARE_DK_T
     return check_launch("bwd_dk_mfma");
 }
 

@@ -46,6 +46,7 @@ __device__ __forceinline__ float in_f32(bf16 x) {
     else return (float)x;
 }
 
+
 // x = hi + lo, both halves of type TY.
 #define SPLIT2(TY, x, HI, LO)              \
     do {                                   \
@@ -54,6 +55,26 @@ __device__ __forceinline__ float in_f32(bf16 x) {
         HI = _h;                           \
         LO = (TY)(_x - (float)_h);         \
     } while (0)
+
+// (a_hi + a_lo) x b, a an fp32 operand split into bf16 halves, b a raw 16-bit input
+// operand: bf16 b enters exactly (two products); fp16 b is split into an exact bf16
+// pair b_hi + b_lo (11 mantissa bits in 8 + 8) and the a_lo x b_lo product, about
+// 2^-16 of the whole, is dropped (three products).
+template <bool F16>
+__device__ __forceinline__ f32x4 mma_split(bf16x8 ah, bf16x8 al, bf16x8 b, f32x4 c) {
+    if constexpr (F16) {
+        const f16x8 bf = __builtin_bit_cast(f16x8, b);
+        bf16x8 bh, bl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) SPLIT2(bf16, (float)bf[e], bh[e], bl[e]);
+        c = mma(ah, bh, c);
+        c = mma(al, bh, c);
+        return mma(ah, bl, c);
+    } else {
+        c = mma(ah, b, c);
+        return mma(al, b, c);
+    }
+}
 
 typedef bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef f16 f16x2 __attribute__((ext_vector_type(2)));

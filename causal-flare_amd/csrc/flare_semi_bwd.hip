@@ -112,10 +112,10 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_tok_kernel(
                 const size_t lrow = ((size_t)h * M + 16 * mt + cl) * Dk + 8 * g4;
                 f32x4 se = f32x4{0.f, 0.f, 0.f, 0.f}, sd = f32x4{0.f, 0.f, 0.f, 0.f}, gzz = f32x4{0.f, 0.f, 0.f, 0.f};
                 for (int k0 = 0; k0 < Dk; k0 += 32) {
-                    se = mma(load8<bf16x8>(reinterpret_cast<const bf16*>(Q) + lrow + k0),
+                    se = mma_in<std::is_same<T, __half>::value>(load8<bf16x8>(reinterpret_cast<const bf16*>(Q) + lrow + k0),
                              ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(K) + krow + k0) : zero8(), se);
                     if (!shared)
-                        sd = mma(load8<bf16x8>(reinterpret_cast<const bf16*>(Kd) + lrow + k0),
+                        sd = mma_in<std::is_same<T, __half>::value>(load8<bf16x8>(reinterpret_cast<const bf16*>(Kd) + lrow + k0),
                                  ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(Qd) + krow + k0) : zero8(), sd);
                 }
                 float zm, zd;
@@ -129,8 +129,7 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_tok_kernel(
 #pragma unroll
                     for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
                     const bf16x8 gb = ok ? load8<bf16x8>(reinterpret_cast<const bf16*>(dY) + grow + k0) : zero8();
-                    gzz = mma(ph, gb, gzz);
-                    gzz = mma(pl, gb, gzz);
+                    gzz = mma_split<std::is_same<T, __half>::value>(ph, pl, gb, gzz);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -432,8 +431,7 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_ds_kernel(const T* __restrict__
 #pragma unroll
                     for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
                     const bf16x8 vb = ok ? load8<bf16x8>(vrow + k0) : zero8();
-                    d2 = mma(ph, vb, d2);
-                    d2 = mma(pl, vb, d2);
+                    d2 = mma_split<std::is_same<T, __half>::value>(ph, pl, vb, d2);
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) vt[cl * M + 16 * mt + 4 * g4 + r] = d2[r];
@@ -522,7 +520,7 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
     const BlockStates st{bm, bd, bn, fm, fd, fu, (int)NB, (int)M, (int)Dv};
     const dim3 gb((unsigned)NB, (unsigned)BH);
     bool tok_mfma = false;
-    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+    if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
         tok_mfma = M % 16 == 0 && Dk % 32 == 0 && Dv % 32 == 0;
         if (tok_mfma)
             hipLaunchKernelGGL((semi_bwd_tok_kernel<T, true>), gb, dim3(kSNT), 0, s, q, k, qd, kd,
@@ -534,8 +532,10 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
                            static_cast<const T*>(dY), (int)N, (int)H, (int)M, (int)Dk, (int)Dv, (int)block, scale,
                            shared, st, S, AL, C);
     if ((rc = check_launch("semi_bwd_tok_kernel"))) return rc;
-    if (std::is_same<T, __hip_bfloat16>::value && bwd_summary_mfma_supported(M, Dv)) {
-        if ((rc = launch_semi_dz_mfma(dY, B, N, H, M, Dv, block, AL, C, X, Yb, s))) return rc;
+    if ((std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) &&
+        bwd_summary_mfma_supported(M, Dv)) {
+        if ((rc = launch_semi_dz_mfma(dY, B, N, H, M, Dv, block, AL, C, X, Yb, std::is_same<T, __half>::value, s)))
+            return rc;
     } else {
         hipLaunchKernelGGL(semi_bwd_dz_kernel<T>, gb, dim3(kSNT), 0, s, static_cast<const T*>(dY), (int)N, (int)H,
                            (int)M, (int)Dv, (int)block, (int)NB, AL, C, X, Yb);
@@ -550,7 +550,7 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
                        static_cast<T*>(dV));
     if ((rc = check_launch("semi_bwd_dv_kernel"))) return rc;
     bool ds_mfma = false;
-    if constexpr (std::is_same<T, __hip_bfloat16>::value) {
+    if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
         ds_mfma = M % 16 == 0 && Dv % 32 == 0;
         if (ds_mfma)
             hipLaunchKernelGGL((semi_bwd_ds_kernel<T, true>), gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N,
