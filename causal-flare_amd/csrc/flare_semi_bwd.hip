@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) void semi_bwd_carry_kernel(float* __restrict__
 // ceil(Dv / 64)); thread (col, rg) owns dv[tau = rg + 4 r][d0 + col] of each
 // token tile, whose factors are staged in LDS.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool MF>
 __global__ __launch_bounds__(kSNT) void semi_bwd_dv_kernel(int N, int H, int M, int Dv, int blk, int NB,
                                                            const float* __restrict__ S, BlockStates st,
                                                            const float* __restrict__ X, T* __restrict__ dV) {
@@ -363,6 +363,36 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_dv_kernel(int N, int H, int M, 
     const int b = bh / H, h = bh % H, tid = threadIdx.x;
     const int tb0 = g * blk;
     if (tid < M) lg[tid] = st.log2den(bh, g, tid);
+    if constexpr (MF) {
+        // 16-bit inputs, M % 32 == 0, whole 64-column slabs: D[token][d] = sum_m P X on the
+        // MFMA, P = 2^(s - L_g) and X both fp32 as bf16 hi + lo (three products); wave w
+        // owns columns d0 + 16 w ..
+        using namespace mfma;
+        __syncthreads();   // lg visible
+        const int lane = tid & 63, w = tid >> 6, g4 = lane >> 4, cl = lane & 15;
+        const float* xb = X + ((size_t)bh * NB + g) * M * Dv + d0 + 16 * w + cl;
+        for (int i0 = 0; i0 < blk; i0 += 16) {
+            const int tok = tb0 + i0 + cl;
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int m0 = 0; m0 < M; m0 += 32) {
+                const float* srow = S + ((size_t)bh * N + tok) * M + m0 + 8 * g4;
+                bf16x8 ph, pl, xh, xl;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    SPLIT2(bf16, sexp2(srow[e] - lg[m0 + 8 * g4 + e]), ph[e], pl[e]);
+                    SPLIT2(bf16, xb[(size_t)(m0 + 8 * g4 + e) * Dv], xh[e], xl[e]);
+                }
+                acc = mma(ph, xh, acc);
+                acc = mma(ph, xl, acc);
+                acc = mma(pl, xh, acc);
+            }
+            // rows: tokens i0 + 4 g + r, column d0 + 16 w + cl
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                dV[stok(b, tb0 + i0 + 4 * g4 + r, h, N, H, Dv) + d0 + 16 * w + cl] = from_f32<T>(acc[r]);
+        }
+        return;
+    }
     const int col = tid & 63, rg = tid >> 6;
     const bool act = d0 + col < Dv;
     const float* xr = X + ((size_t)bh * NB + g) * M * Dv + d0 + col;
@@ -545,9 +575,17 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
     hipLaunchKernelGGL(semi_bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, s, X, Yb, st,
                        (int)NB, (int)M, (int)Dv, BH * M);
     if ((rc = check_launch("semi_bwd_carry_kernel"))) return rc;
-    hipLaunchKernelGGL(semi_bwd_dv_kernel<T>, dim3((unsigned)NB, (unsigned)BH, (unsigned)((Dv + 63) / 64)),
-                       dim3(kSNT), 0, s, (int)N, (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X,
-                       static_cast<T*>(dV));
+    const dim3 gdv((unsigned)NB, (unsigned)BH, (unsigned)((Dv + 63) / 64));
+    bool dv_mfma = false;
+    if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
+        dv_mfma = M % 32 == 0 && Dv % 64 == 0;
+        if (dv_mfma)
+            hipLaunchKernelGGL((semi_bwd_dv_kernel<T, true>), gdv, dim3(kSNT), 0, s, (int)N, (int)H, (int)M, (int)Dv,
+                               (int)block, (int)NB, S, st, X, static_cast<T*>(dV));
+    }
+    if (!dv_mfma)
+        hipLaunchKernelGGL((semi_bwd_dv_kernel<T, false>), gdv, dim3(kSNT), 0, s, (int)N, (int)H, (int)M, (int)Dv,
+                           (int)block, (int)NB, S, st, X, static_cast<T*>(dV));
     if ((rc = check_launch("semi_bwd_dv_kernel"))) return rc;
     bool ds_mfma = false;
     if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
