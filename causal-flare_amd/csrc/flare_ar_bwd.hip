@@ -400,6 +400,32 @@ __global__ __launch_bounds__(256) void bwd_gy_kernel(const T* __restrict__ dY, c
     }
 }
 
+// 16-bit inputs with Dv / 8 a power of two <= 64: lpr = Dv / 8 lanes per row, each
+// with one 16-byte load of dY and of Y, and a shuffle reduction over the row's lanes.
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_gy_vec_kernel(const T* __restrict__ dY, const T* __restrict__ Y, int N,
+                                                         int H, int Dv, int64_t rows, float* __restrict__ gy) {
+    const int lpr = Dv >> 3;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = gid / lpr;
+    const int sub = (int)(gid % lpr);
+    float sum = 0.0f;
+    if (row < rows) {
+        union { uint4 raw; T el[8]; } a, y;
+        a.raw = *reinterpret_cast<const uint4*>(dY + row * Dv + 8 * sub);
+        y.raw = *reinterpret_cast<const uint4*>(Y + row * Dv + 8 * sub);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += to_f32(a.el[e]) * to_f32(y.el[e]);
+    }
+    for (int off = lpr >> 1; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (row < rows && sub == 0) {
+        const int h = (int)(row % H);
+        const int64_t bt = row / H;
+        const int b = (int)(bt / N), t = (int)(bt % N);
+        gy[((int64_t)b * H + h) * N + t] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Register-blocked accumulation shared by bwd_summary and bwd_dq:
 // acc[i][j] += a[8 mi + i] * b[8 di + j] for one token row of each operand.
@@ -1138,6 +1164,14 @@ static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, boo
 template <typename T>
 static int launch_gy(const T* dy, const T* y, int64_t B, int64_t N, int64_t H, int64_t Dv, float* gy, hipStream_t st) {
     const int64_t rows = B * N * H;
+    const int64_t lpr = Dv / 8;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(dy) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+    if (!std::is_same<T, float>::value && aligned && Dv % 8 == 0 && lpr <= 64 && (lpr & (lpr - 1)) == 0) {
+        const int64_t threads = rows * lpr;
+        hipLaunchKernelGGL(bwd_gy_vec_kernel<T>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, dy, y,
+                           (int)N, (int)H, (int)Dv, rows, gy);
+        return check_launch("bwd_gy_vec_kernel");
+    }
     hipLaunchKernelGGL(bwd_gy_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, dy, y, (int)N, (int)H,
                        (int)Dv, rows, gy);
     return check_launch("bwd_gy_kernel");
