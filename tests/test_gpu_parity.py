@@ -152,7 +152,7 @@ def test_prefill_decode_variants_fp32(q_dec_mode, k_dec_mode, d_score, d_value):
         assert_parity(st1[key], st1_ref[key], torch.float32, f"decode state {key}")
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_decode_continuation_equals_prefill_of_concatenation(dtype):
     """test_cached_suites.py:55-63: prefill(T) + decode steps == prefill(T + steps)."""
     from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
