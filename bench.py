@@ -63,8 +63,9 @@ def bench_prefill(torch, flare, steps, warmup):
     torch.cuda.synchronize()
     dt_eager = time.perf_counter() - t0
     # The same `steps` forwards captured once in a HIP graph and replayed, as for
-    # decode: the kernels are identical, the launches back to back.  The replay's
-    # output must equal the eager one bit for bit, else the eager time is reported.
+    # decode: the kernels are identical, the launches back to back.  Every step's
+    # output of the replay must equal the eager one bit for bit, else the eager time
+    # is reported.
     dt_graph, graph_ok = None, False
     try:
         side = torch.cuda.Stream()
@@ -74,12 +75,13 @@ def bench_prefill(torch, flare, steps, warmup):
                 flare.flare_autoregressive_triton(q, k, v)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
+        ygs = []   # every step's output is kept, so no step's buffers are reused within the graph
         with torch.cuda.graph(graph):
             for _ in range(steps):
-                yg = flare.flare_autoregressive_triton(q, k, v)
+                ygs.append(flare.flare_autoregressive_triton(q, k, v))
         graph.replay()
         torch.cuda.synchronize()
-        graph_ok = bool(torch.equal(yg, y))
+        graph_ok = all(bool(torch.equal(yg, y)) for yg in ygs)
         if graph_ok:
             times = []
             for _ in range(2):
@@ -89,7 +91,7 @@ def bench_prefill(torch, flare, steps, warmup):
                 torch.cuda.synchronize()
                 times.append(time.perf_counter() - t0)
             dt_graph = min(times)
-        del graph, yg
+        del graph, ygs
     except Exception as exc:   # capture unavailable: the eager loop is the measurement
         print(f"prefill graph replay unavailable: {exc}", file=sys.stderr)
     dt = dt_graph if graph_ok else dt_eager
