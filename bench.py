@@ -40,17 +40,6 @@ def _cfg3_inputs(torch, device):
     return (B, N, H, M, D), q.to(device), k.to(device), v.to(device)
 
 
-def _time_kernels(torch, fn, reps):
-    """Average per-phase GPU time (ms) from fn(timings) with events on the launch stream."""
-    acc = {}
-    for _ in range(reps):
-        t = {}
-        fn(t)
-        for k, v in t.items():
-            acc[k] = acc.get(k, 0.0) + v
-    return {k: v / reps for k, v in acc.items()}
-
-
 def bench_prefill(torch, flare, steps, warmup):
     dev = torch.device("cuda:0")
     (B, N, H, M, D), q, k, v = _cfg3_inputs(torch, dev)
@@ -97,10 +86,19 @@ def bench_prefill(torch, flare, steps, warmup):
     dt = dt_graph if graph_ok else dt_eager
     ms = dt * 1e3 / steps
     tok_s = B * N * steps / dt
-    # per-kernel durations (events on the stream the kernels run on)
-    phases = _time_kernels(
-        torch, lambda t: t.update(flare.flare_autoregressive_triton(q, k, v, profile=True)[1]["forward"]),
-        reps=3)
+    # Per-kernel durations: the same `steps` forwards launched back to back (the
+    # library's three phase entry points, the kernels of the API call), with start /
+    # end events recorded on the launch stream around each phase and no
+    # synchronisation until the loop has finished.
+    from causal_flare._common import EventLog
+    from causal_flare.autoregressive.training import run_chunked_forward
+    chunk = int(flare._lib.lib().flare_ar_default_chunk(B, N, H, M, D))
+    log = EventLog()
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        run_chunked_forward(q, k, v, None, None, scale=D ** -0.5, chunk=chunk, out_dtype=v.dtype, timings=log)
+    torch.cuda.synchronize()
+    phases = log.mean_ms()
     flops = 6.0 * M * D * B * N * H
     dom = "flare_chunk_fwd"
     dom_ms = phases.get(dom, ms)
@@ -114,8 +112,10 @@ def bench_prefill(torch, flare, steps, warmup):
         "roofline": {
             "bound": "mfma", "kernel": "chunk_output_pc", "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": measured_traffic("chunk_output_pc"), "whole_pass_tflops": whole,
-            "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
+            "traffic": measured_traffic("traffic_cfg3_prefill.txt", "chunk_output_pc"),
+            "kernel_ms": dom_ms, "alg_flop_per_launch": flops,
+            "timing": f"mean of {steps} back-to-back launches, HIP events on the launch stream",
+            "whole_pass_tflops": whole, "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
         },
     }
 
@@ -155,6 +155,7 @@ def bench_decode(torch, flare, steps=256):
 
     eager()
     dt_eager = min(eager() for _ in range(3))
+    eager_state = {kk: vv.clone() for kk, vv in st.items()}
     # graph capture of the same step loop
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -176,6 +177,10 @@ def bench_decode(torch, flare, steps=256):
         torch.cuda.synchronize()
         times.append(e0.elapsed_time(e1) / 1e3)
     dt_graph = min(times)
+    # the replayed loop must leave the state the eager loop left, bit for bit
+    replay_ok = all(bool(torch.equal(st[kk], eager_state[kk])) for kk in st)
+    if not replay_ok:
+        dt_graph = dt_eager
     k_ms = dt_graph * 1e3 / steps
     state_bytes = 2 * (8 * M + 4 * M * D) * B * H
     io_bytes = B * H * D * 2 * 3 + H * M * D * 2
@@ -184,13 +189,17 @@ def bench_decode(torch, flare, steps=256):
     return {
         "B": B, "H": H, "M": M, "D": D, "prefill_T": T, "steps": steps,
         "tok_s": B * steps / dt_graph, "ms_per_step": k_ms,
+        "timing": "graph replay of the step loop (final state bit-identical to eager)" if replay_ok
+                  else "eager API loop (graph replay differed)",
         "tok_s_eager_api_loop": B * steps / dt_eager, "ms_per_step_eager": dt_eager * 1e3 / steps,
         "roofline": {
             "bound": "hbm", "kernel": "decode_step_fast", "achieved": achieved,
-            "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+            "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": achieved / PEAK_HBM_GBS,
+            "traffic": measured_traffic("traffic_cfg4_decode.txt", "decode_step_fast"),
             "alg_bytes_per_step": bytes_step,
             "note": "graph replay of 256 back-to-back steps; per-step time includes launch gaps",
         },
+        "final_state": {kk: vv.cpu() for kk, vv in st.items()},
     }
 
 
@@ -212,14 +221,23 @@ def bench_others(torch, flare):
         return (time.perf_counter() - t0) / reps
 
     out = {}
+    def hbm_roofline(B, N, H, D, dt):
+        # algorithmic bytes: K and V read, Y written, bf16: 6 D bytes per token-head
+        alg = 6.0 * D * B * N * H
+        gbs = alg / dt / 1e9
+        return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": gbs / PEAK_HBM_GBS, "alg_bytes": alg, "scope": "whole forward (all kernels)"}
+
     q, k, v = inputs(1, 4, 4096, 16, 128, 64)
     dt = timed(lambda: flare.flare_autoregressive_triton(q, k, v))
     out["config2_prefill"] = {"ms": dt * 1e3, "tok_s": 4 * 4096 / dt,
-                              "tflops_alg": 6 * 128 * 64 * 4 * 4096 * 16 / dt / 1e12}
+                              "tflops_alg": 6 * 128 * 64 * 4 * 4096 * 16 / dt / 1e12,
+                              "roofline": hbm_roofline(4, 4096, 16, 64, dt)}
     q, k, v = inputs(4, 2, 8192, 16, 128, 64)
     dt = timed(lambda: flare.flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=64))
     out["config5_semi_ar"] = {"ms": dt * 1e3, "tok_s": 2 * 8192 / dt,
-                              "tflops_alg": 6 * 128 * 64 * 2 * 8192 * 16 / dt / 1e12}
+                              "tflops_alg": 6 * 128 * 64 * 2 * 8192 * 16 / dt / 1e12,
+                              "roofline": hbm_roofline(2, 8192, 16, 64, dt)}
     # backward (autograd through flare_autoregressive_triton) on configs 2 and 3
     for name, shape, reps in (("config2_backward", (4, 4096, 16, 128, 64), 5),
                               ("config3_backward", (1, 65536, 16, 256, 128), 3)):
@@ -238,9 +256,9 @@ def bench_others(torch, flare):
     return out
 
 
-def measured_traffic(kernel):
+def measured_traffic(fname, kernel):
     """HBM bytes per launch of `kernel` from the committed rocprof PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", "traffic_cfg3_prefill.txt")
+    path = os.path.join(ROOT, "profiles", fname)
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -250,12 +268,24 @@ def measured_traffic(kernel):
     return None
 
 
-def cpu_baseline():
-    """fp32 C oracle (OpenMP over heads) on a bounded sample of config 3."""
+def _cpu_threads():
+    """Threads for the CPU baseline: the process's OpenMP share (OMP_NUM_THREADS, which
+    the GPU boxes set to the CPU share of one GPU), else every core it may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env), "OMP_NUM_THREADS"
+    try:
+        return len(os.sched_getaffinity(0)), "sched_getaffinity"
+    except AttributeError:
+        return os.cpu_count() or 1, "os.cpu_count"
+
+
+def cpu_baseline(decode_state=None):
+    """The fp32 C oracle on bounded samples of config 3 (prefill) and config 4 (decode)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import flare_oracle as O
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores, how = _cpu_threads()
     B, N, H, M, D = 1, int(os.environ.get("FLARE_BENCH_CPU_TOKENS", "65536")), 16, 256, 128
     rng = np.random.default_rng(2)
     q = (rng.standard_normal((H, M, D)) / math.sqrt(D)).astype(np.float32)
@@ -264,9 +294,31 @@ def cpu_baseline():
     t0 = time.perf_counter()
     O.ar_chunked(q, k, v, nthreads=cores)
     dt = time.perf_counter() - t0
-    return {"value": B * N / dt, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"config 3 (B=1, N={N}, H=16, M=256, D=128) in fp32 through the C oracle "
-                      f"(chunked 3-phase restatement of reference.py:203-512), one pass, {dt:.1f}s wall"}
+    out = {"value": B * N / dt, "unit": "tok/s", "cores": cores, "kind": "port",
+           "host_cores": os.cpu_count(), "threads_from": how,
+           "sample": f"config 3 (B=1, N={N}, H=16, M=256, D=128) in fp32 through the C oracle "
+                     f"(chunked 3-phase restatement of reference.py:203-512), one pass, {dt:.1f}s wall"}
+    # config 4 decode: 256 single-token steps of the oracle's recurrent step (the
+    # restatement of flare_decode_pytorch, inference.py:318-351) from the 2048-token
+    # prefill state, one call per step as a caller drives decode
+    Bd, Hd, Md, Dd, steps = 64, 16, 128, 64, int(os.environ.get("FLARE_BENCH_CPU_DECODE_STEPS", "256"))
+    rng = np.random.default_rng(3)
+    qd = (rng.standard_normal((Hd, Md, Dd)) / math.sqrt(Dd)).astype(np.float32)
+    if decode_state is not None:
+        st = {kk: vv.numpy().astype(np.float32) for kk, vv in decode_state.items()}
+    else:
+        st = {"m": np.zeros((Bd, Hd, Md), np.float32), "d": np.ones((Bd, Hd, Md), np.float32),
+              "u": rng.standard_normal((Bd, Hd, Md, Dd)).astype(np.float32)}
+    kd = rng.standard_normal((Bd, steps, Hd, Dd)).astype(np.float32)
+    vd = rng.standard_normal((Bd, steps, Hd, Dd)).astype(np.float32)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        _, st = O.ar_recurrent(qd, kd[:, s:s + 1], vd[:, s:s + 1], state=st, nthreads=cores)
+    dtd = time.perf_counter() - t0
+    out["decode"] = {"value": Bd * steps / dtd, "unit": "tok/s", "cores": cores, "kind": "port",
+                     "sample": f"config 4 decode: {steps} steps x B=64 (H=16, M=128, D=64) in fp32, one oracle "
+                               f"call per step from the GPU prefill's state, {dtd:.1f}s wall"}
+    return out
 
 
 def main():
@@ -289,7 +341,8 @@ def main():
     pre = bench_prefill(torch, flare, args.steps, args.warmup)
     dec = None if args.no_decode else bench_decode(torch, flare)
     others = None if args.no_decode else bench_others(torch, flare)
-    cpu = None if args.no_cpu else cpu_baseline()
+    dstate = dec.pop("final_state", None) if dec else None
+    cpu = None if args.no_cpu else cpu_baseline(dstate)
     out = {
         "metric": "prefill tok/s (N=64k) & decode tok/s (B=64) on 1 MI355X; % of roofline",
         "value": pre["tok_s"],

@@ -78,6 +78,27 @@ def _refresh_profile_totals(profile_data) -> None:
     profile_data["total_ms"] = f + b
 
 
+class EventLog:
+    """Per-phase GPU times of back-to-back launches: start/end events recorded on the
+    launch stream with no synchronisation, read by ``mean_ms`` after the caller has
+    synchronised.  Passed where a ``timings`` dict goes in the internal launchers."""
+
+    def __init__(self):
+        self.pairs = {}
+
+    def record(self, key, op):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = op()
+        end.record()
+        self.pairs.setdefault(key, []).append((start, end))
+        return out
+
+    def mean_ms(self):
+        return {k: sum(s.elapsed_time(e) for s, e in v) / len(v) for k, v in self.pairs.items()}
+
+
 class _PhaseTimer:
     """Per-phase GPU time with events on the current stream (``_common.py:51-65``)."""
 
@@ -88,6 +109,8 @@ class _PhaseTimer:
     def __call__(self, key, op):
         if self.bucket is None:
             return op()
+        if isinstance(self.bucket, EventLog):
+            return self.bucket.record(key, op)
         torch.cuda.synchronize(self.device)
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)

@@ -33,6 +33,8 @@ HEADER_FUNCTIONS = (
     "flare_semi_ar_forward",
     "flare_semi_ar_backward_workspace_size",
     "flare_semi_ar_backward",
+    "flare_device_faults",
+    "flare_set_meet_spin_limit",
 )
 
 F32, BF16, F16 = 0, 1, 2
@@ -84,6 +86,10 @@ def _declare(lib):
     lib.flare_semi_ar_backward_workspace_size.argtypes = [_i64] * 7
     lib.flare_semi_ar_backward.restype = _i
     lib.flare_semi_ar_backward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 7 + [_vp, _sz, _vp])
+    lib.flare_device_faults.restype = _i
+    lib.flare_device_faults.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint32), _i]
+    lib.flare_set_meet_spin_limit.restype = _i
+    lib.flare_set_meet_spin_limit.argtypes = [_i]
     lib.flare_semi_ar_forward.restype = _i
     lib.flare_semi_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp, _i, _vp, _vp]
                                           + [_vp, _sz, _vp])
@@ -138,3 +144,17 @@ def check(rc: int, what: str):
         if rc == -1:
             raise ValueError(f"{what}: {msg}")
         raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def device_faults(device=None, reset: bool = False) -> int:
+    """Synchronise the current stream and return the device's count of bounded
+    waits that gave up in the output kernel (0 in a healthy run)."""
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    n = ctypes.c_uint32(0)
+    check(lib().flare_device_faults(stream_of(dev), ctypes.byref(n), 1 if reset else 0), "device_faults")
+    return int(n.value)
+
+
+def set_meet_spin_limit(limit: int) -> None:
+    """Sleeps before a producer meeting of the output kernel gives up (default 1 << 20)."""
+    check(lib().flare_set_meet_spin_limit(int(limit)), "set_meet_spin_limit")

@@ -108,6 +108,57 @@ def _canonicalize_q_dec_for_decode(Q_dec, K_step, K_input=None, K_prefill=None):
     raise ValueError(f"Decode Q_dec must be [B, H, D] or [B, 1, H, D]. Got Q_dec.shape={tuple(Q_dec.shape)}")
 
 
+def _decode_step_fast(Q, K, V, state, scale):
+    """The common decode call, with the host work cut to the launch itself: shared
+    decoder weights, no mask, Q/K/V of one 16-bit or fp32 type and contiguous, and
+    a contiguous fp32 state on the same device.  Returns None (the general path
+    then runs, with its full validation) when any of that does not hold."""
+    if K.dim() == 4:
+        if K.shape[1] != 1:
+            return None
+        B, _, H, Dk = K.shape
+    elif K.dim() == 3:
+        B, H, Dk = K.shape
+    else:
+        return None
+    if V.dim() not in (3, 4) or (V.dim() == 4 and V.shape[1] != 1) or Q.dim() != 3:
+        return None
+    Dv = V.shape[-1]
+    Hq, M, Dq = Q.shape
+    dt = Q.dtype
+    if (Hq != H or Dq != Dk or V.shape[0] != B or V.shape[-2] != H or K.dtype is not dt or V.dtype is not dt
+            or dt not in _FAST_DTYPES or not (Q.is_contiguous() and K.is_contiguous() and V.is_contiguous())):
+        return None
+    if not isinstance(state, dict):
+        return None
+    m, d, u = state.get("m"), state.get("d"), state.get("u")
+    dev = K.device
+    for t in (m, d, u):
+        if (t is None or t.dtype is not torch.float32 or t.device != dev or not t.is_contiguous()):
+            return None
+    if m.shape != (B, H, M) or d.shape != (B, H, M) or u.shape != (B, H, M, Dv) or u.data_ptr() % 16:
+        return None
+    if V.device != dev or Q.device != dev:
+        return None
+    y = torch.empty((B, 1, H, Dv), device=dev, dtype=dt)
+    code = _FAST_DTYPES[dt]
+    rc = _lib.lib().flare_decode_step(Q.data_ptr(), K.data_ptr(), V.data_ptr(), None, None, None, code, B, H, M,
+                                      Dk, Dv, float(scale), m.data_ptr(), d.data_ptr(), u.data_ptr(), y.data_ptr(),
+                                      code, _raw_stream(dev.index))
+    _lib.check(rc, "flare_decode_step")
+    return y, {"m": m, "d": d, "u": u}
+
+
+_FAST_DTYPES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
+
+
+def _raw_stream(index):
+    """Handle of the current stream of device `index` (None: the current device)."""
+    if index is None:
+        index = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
+
+
 def flare_autoregressive_decode_triton(
     Q: torch.Tensor,
     K: torch.Tensor,
@@ -123,6 +174,11 @@ def flare_autoregressive_decode_triton(
     """One recurrent decode step (reference inference.py:492-621); one kernel launch."""
     if Q.device.type != "cuda":
         raise RuntimeError("flare_autoregressive_decode requires CUDA tensors. ")
+    if (Q_dec is None and K_dec is None and attention_mask is None and input_precision is None
+            and not profile and state is not None):
+        out = _decode_step_fast(Q, K, V, state, scale)
+        if out is not None:
+            return out
     K_input = K
     K, V = _canonicalize_kv_for_decode(K, V)
     _normalize_input_precision(input_precision)

@@ -199,7 +199,10 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     const T* __restrict__ Qdec, const T* __restrict__ Kdec, int N, int H, int M, int Dk, int Dv,
     int DT, int TT, float scale, int chunk, bool shared, const float* __restrict__ pmax,
     const float* __restrict__ pden, const float* __restrict__ pnum, void* __restrict__ Y,
-    int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask) {
+    int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask, const int* __restrict__ only) {
+    // only: when given, [B*H, NC] flags; chunks whose flag is 0 are left alone (the
+    // tokenwise replay of the chunks an MFMA output kernel could not resolve)
+    if (only != nullptr && only[(size_t)blockIdx.y * gridDim.x + blockIdx.x] == 0) return;
     extern __shared__ float smem[];
     const int R = kNT / DT;
     float* k_tile = smem;                                   // [TT][Dk]
@@ -386,55 +389,68 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
                          const float* pden, const float* pnum, void* Y, int out_dtype,
                          float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr,
-                         void* alpha_ws = nullptr) {
+                         void* alpha_ws = nullptr, int* redo = nullptr) {
     const bool shared = Qdec == nullptr && Kdec == nullptr;
-    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr) {
-        if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled()))
-            return launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
-                                      tmask, dtype == FLARE_F16, stream);
-        // separate decoder tensors: the decoder softmax first (alpha_ws, [B*H, N, M] fp16),
-        // then the producer/consumer kernel reading it
-        if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
-            mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
-            const int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, tmask,
-                                                alpha_ws, nullptr, dtype == FLARE_F16, stream);
-            if (rc) return rc;
-            return launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask,
-                                    alpha_ws, dtype == FLARE_F16, stream);
-        }
-    }
-    const int DT = pick_dt(M, Dv);
-    FLARE_REQUIRE(DT > 0, "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
-                  (long long)M, (long long)Dv);
-    const int R = kNT / DT;
-    const int64_t rows = (M + R - 1) / R;
-    int TT = 16;
-    OutSmem lay{TT, (int)Dk, DT, (int)M, R, shared};
-    while (lay.floats() * sizeof(float) > 64 * 1024 && lay.TT > 1) lay.TT /= 2;
-    FLARE_REQUIRE(lay.floats() * sizeof(float) <= 64 * 1024, "chunk_output: shape too large for LDS");
-    TT = lay.TT;
-    const int64_t NC = (N + chunk - 1) / chunk;
-    dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)(Dv / DT));
-    const size_t sm = lay.floats() * sizeof(float);
-    // Missing decoder tensors default to the encoder ones (K as Qdec, Q as Kdec).
-    const void* qd = Qdec ? Qdec : K;
-    const void* kd = Kdec ? Kdec : Q;
+    // A launch of the scalar kernel restricted to the chunks flagged in `only` (or all).
+    auto scalar = [&](const int* only) -> int {
+        const int DT = pick_dt(M, Dv);
+        FLARE_REQUIRE(DT > 0,
+                      "chunk_output: unsupported M=%lld Dv=%lld (Dv must be a multiple of 16, M*16 <= 16384)",
+                      (long long)M, (long long)Dv);
+        const int R = kNT / DT;
+        const int64_t rows = (M + R - 1) / R;
+        OutSmem lay{16, (int)Dk, DT, (int)M, R, shared};
+        while (lay.floats() * sizeof(float) > 64 * 1024 && lay.TT > 1) lay.TT /= 2;
+        FLARE_REQUIRE(lay.floats() * sizeof(float) <= 64 * 1024, "chunk_output: shape too large for LDS");
+        const int TT = lay.TT;
+        const int64_t NC = (N + chunk - 1) / chunk;
+        dim3 grid((unsigned)NC, (unsigned)(B * H), (unsigned)(Dv / DT));
+        const size_t sm = lay.floats() * sizeof(float);
+        // Missing decoder tensors default to the encoder ones (K as Qdec, Q as Kdec).
+        const void* qd = Qdec ? Qdec : K;
+        const void* kd = Kdec ? Kdec : Q;
 #define FLARE_OUT(TY, RW)                                                                       \
     hipLaunchKernelGGL((chunk_output_kernel<TY, RW>), grid, dim3(kNT), sm, stream, (const TY*)Q, \
                        (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd, (int)N, (int)H,  \
                        (int)M, (int)Dk, (int)Dv, DT, TT, scale, (int)chunk, shared, pmax, pden,   \
-                       pnum, Y, out_dtype, lse_dec, tmask)
+                       pnum, Y, out_dtype, lse_dec, tmask, only)
 #define FLARE_OUT_ROWS(TY)                   \
     if (rows <= 8) FLARE_OUT(TY, 8);         \
     else if (rows <= 16) FLARE_OUT(TY, 16);  \
     else if (rows <= 32) FLARE_OUT(TY, 32);  \
     else FLARE_OUT(TY, 64);
-    if (dtype == FLARE_BF16) { FLARE_OUT_ROWS(__hip_bfloat16) }
-    else if (dtype == FLARE_F16) { FLARE_OUT_ROWS(__half) }
-    else { FLARE_OUT_ROWS(float) }
+        if (dtype == FLARE_BF16) { FLARE_OUT_ROWS(__hip_bfloat16) }
+        else if (dtype == FLARE_F16) { FLARE_OUT_ROWS(__half) }
+        else { FLARE_OUT_ROWS(float) }
 #undef FLARE_OUT_ROWS
 #undef FLARE_OUT
-    return check_launch("chunk_output_kernel");
+        return check_launch("chunk_output_kernel");
+    };
+    // the MFMA kernels run with the redo flags (the chunks they hand back to the scalar kernel)
+    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr && redo != nullptr) {
+        int rc = -1;
+        if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled())) {
+            rc = launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
+                                    tmask, dtype == FLARE_F16, redo, stream);
+        } else if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
+                   mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
+            // separate decoder tensors: the decoder softmax first (alpha_ws, [B*H, N, M] fp16),
+            // then the producer/consumer kernel reading it
+            rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, tmask,
+                                      alpha_ws, nullptr, dtype == FLARE_F16, stream);
+            if (rc) return rc;
+            rc = launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask,
+                                  alpha_ws, dtype == FLARE_F16, redo, stream);
+        }
+        if (rc >= 0) {
+            if (rc) return rc;
+            // chunks where a latent's reference jumped past what the MFMA kernel resolves
+            // (a score more than kJumpMax above the running max within one subtile) are
+            // replayed tokenwise in fp32; every other chunk's workgroup returns at once
+            return scalar(redo);
+        }
+    }
+    return scalar(nullptr);
 }
 
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
@@ -509,8 +525,19 @@ int flare_chunk_output(const void* Q, const void* K, const void* V, const void* 
     FLARE_REQUIRE(Q && K && V && Y && prefix_max && prefix_den && prefix_num, "chunk_output: null pointer");
     FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0 && chunk > 0,
                   "chunk_output: sizes must be positive");
-    return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, prefix_max,
-                         prefix_den, prefix_num, Y, out_dtype, lse_dec, (hipStream_t)stream);
+    // the MFMA output kernels report the chunks they hand back to the scalar kernel in
+    // [B*H, NC] flags: a stream-ordered allocation of them for this call
+    hipStream_t st = (hipStream_t)stream;
+    int* redo = nullptr;
+    const int64_t NC = (N + chunk - 1) / chunk;
+    if (lse_dec == nullptr && hipMallocAsync((void**)&redo, (size_t)B * H * NC * sizeof(int), st) != hipSuccess) {
+        (void)hipGetLastError();
+        redo = nullptr;     // the scalar kernels alone
+    }
+    const int rc = launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, prefix_max,
+                                 prefix_den, prefix_num, Y, out_dtype, lse_dec, st, nullptr, nullptr, redo);
+    if (redo != nullptr) (void)hipFreeAsync(redo, st);
+    return rc;
 }
 
 int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
@@ -519,11 +546,13 @@ int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Bytes of the chunk summaries (max, den, num), each 256-byte aligned.
+// Bytes of the chunk summaries (max, den, num) and the per-chunk redo flags of the
+// output kernel ([B*H, NC] ints), each 256-byte aligned.
 static size_t summary_bytes(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t chunk) {
     const int64_t NC = (N + chunk - 1) / chunk;
     const size_t per = (size_t)B * H * NC * M;
-    return 2 * align256(per * sizeof(float)) + align256(per * Dv * sizeof(float));
+    return 2 * align256(per * sizeof(float)) + align256(per * Dv * sizeof(float)) +
+           align256((size_t)B * H * NC * sizeof(int));
 }
 
 size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
@@ -573,13 +602,14 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
     float* cmax = (float*)ws;
     float* cden = (float*)(ws + align(per * sizeof(float)));
     float* cnum = (float*)(ws + 2 * align(per * sizeof(float)));
+    int* redo = (int*)(ws + 2 * align(per * sizeof(float)) + align(per * Dv * sizeof(float)));
     hipStream_t s = (hipStream_t)stream;
     int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s, token_mask);
     if (rc) return rc;
     rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
-                         cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws);
+                         cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws, redo);
 }
 
 }  // extern "C"

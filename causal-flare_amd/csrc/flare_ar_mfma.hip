@@ -278,7 +278,7 @@ template <int M, int D, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
-    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype) {
+    const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, int* __restrict__ redo) {
     using L = OutLayout<M, D, NW>;
     __shared__ __attribute__((aligned(16))) f16 wl[T * L::WP];         // W1[t][m]
     __shared__ __attribute__((aligned(16))) f16 etl[M * L::EP];        // E^T[m][tau] (fp16)
@@ -290,6 +290,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
     __shared__ __attribute__((aligned(16))) float gaml[M];             // rescale factor per latent
     __shared__ __attribute__((aligned(16))) float d0l[M];              // den at the subtile start (after moves)
     __shared__ int moved[NW];                                           // wave moved a reference max
+    __shared__ int redol;                                               // a reference jumped past kJumpMax
     __shared__ __attribute__((aligned(16))) bf16 qs[M * D];            // Q[h] (latent bank), swizzled rows
     __shared__ __attribute__((aligned(16))) bf16 ksl[T * D];           // K rows of the subtile, swizzled rows
 
@@ -335,6 +336,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                 U[mi][di][r] = pnum[(pbase + 16 * mi + 4 * g + r) * D + dw0 + 16 * di + c] * ip;
         }
 
+    if (tid == 0) redol = 0;     // visible after the first subtile's barriers
     const int t_begin = c_idx * chunk;
     const int t_end = min(N, t_begin + chunk);
     const size_t stride = (size_t)H * D;
@@ -415,12 +417,19 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
             }
         const bool wave_moved = __any(need);     // a wave-wide vote: every lane takes part
         if (wave_moved) {
+            bool jump = false;
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
                     float Rn = mx > R[mi][r] + kLazy ? mx : R[mi][r];
+                    // running max at the subtile's first valid token (R, or the smallest valid
+                    // score when there is no reference yet); a move past kJumpMax above it
+                    // sends the chunk to the tokenwise fp32 replay
+                    const float s0 = s[mi][0][r], s1 = s[mi][1][r];
+                    const float mn = -row_max16(fmaxf(s0 == kNegInf ? kNegInf : -s0, s1 == kNegInf ? kNegInf : -s1));
+                    jump |= Rn - (R[mi][r] == kNegInf ? mn : R[mi][r]) > kJumpMax;
                     float g1 = exp2f_fast(R[mi][r] - Rn);                  // 0 when R = -inf
                     const float dd = dn[mi][r] * g1;
                     if (dd > kDenMax) {
@@ -431,6 +440,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
                     gam[mi][r] = Rn == R[mi][r] ? 1.0f : g1;
                     R[mi][r] = Rn;
                 }
+            if (jump) redol = 1;
         }
         // ---- decoder max over this wave's latents, per token (cols of S^T)
         float lm[2], off[2];
@@ -744,6 +754,7 @@ __global__ __launch_bounds__(64 * NW, 1) void chunk_output_mfma(
         }
         __syncthreads();   // B3: LDS is rewritten by the next subtile
     }
+    if (redo != nullptr && tid == 0) redo[(size_t)bh * NC + c_idx] = redol;
 }
 
 }  // namespace mfma
@@ -799,10 +810,10 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
-                       bool f16in, hipStream_t stream) {
+                       bool f16in, int* redo, hipStream_t stream) {
     if (output_pc_enabled())
         return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, nullptr,
-                                f16in, stream);
+                                f16in, redo, stream);
     FLARE_REQUIRE(!f16in, "chunk_output_mfma: fp16 inputs need the producer/consumer kernel");
     FLARE_REQUIRE(tmask == nullptr, "chunk_output_mfma: token masks need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);
@@ -812,7 +823,7 @@ int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, i
 #define FLARE_OUT_MFMA(MM, DD, NWW)                                                                    \
     hipLaunchKernelGGL((chunk_output_mfma<MM, DD, NWW>), grid, dim3(64 * NWW), 0, stream,             \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                       pmax, pden, pnum, Y, out_dtype)
+                       pmax, pden, pnum, Y, out_dtype, redo)
     if (M == 128 && D == 64) FLARE_OUT_MFMA(128, 64, 4);
     else if (M == 128 && D == 128) FLARE_OUT_MFMA(128, 128, 4);
     else if (M == 256 && D == 64) FLARE_OUT_MFMA(256, 64, 4);

@@ -41,6 +41,14 @@
 namespace flare {
 namespace mfma {
 
+// Producer meetings of chunk_output_pc that gave up waiting (a fault counter that
+// the host reads with flare_device_faults; it should stay 0).
+__device__ unsigned int g_meet_timeouts = 0;
+// Sleeps (s_sleep 1, about 64 clocks each) a producer waits at a meeting before it
+// gives up: about 28 ms, far beyond any legitimate wait (a few microseconds).
+constexpr int kMeetSpinLimit = 1 << 20;
+int g_spin_limit = kMeetSpinLimit;
+
 template <int M, int D, int NPW>
 struct PCLayout {
     static constexpr int NP = NPW;           // producer waves
@@ -72,7 +80,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, const int32_t* __restrict__ tmask,
-    const f16* __restrict__ alpha) {
+    const f16* __restrict__ alpha, int* __restrict__ redo, int spin_limit) {
     using L = PCLayout<M, D, NPW>;
     // K rows of the even / odd subtiles (swizzled); two arrays rather than one so
     // that reads of one never wait on the DMA that fills the other
@@ -89,6 +97,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
     __shared__ __attribute__((aligned(16))) f16 tril[2 * 64 * 8];               // triangular B operand per lane
     __shared__ __attribute__((aligned(16))) float arl[M];                       // 2^(R - Rmax) per latent
     __shared__ int psync;                                                       // producer arrivals (monotonic)
+    __shared__ int redol;                                                       // a reference jumped past kJumpMax
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
     const int NC = gridDim.x;
@@ -156,13 +165,27 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                 }
         };
         refresh_ar();
-        if (tid == 0) psync = 0;
+        if (tid == 0) {
+            psync = 0;
+            redol = 0;
+        }
         // The producers meet (consumers never take part): each adds one arrival
-        // and waits for the count of meeting n (1, 2, ...), once per subtile.
+        // and waits for the count of meeting n (1, 2, ...), once per subtile.  Every
+        // producer runs the same subtiles (j < NS), so the count always arrives; the
+        // wait is still bounded: past spin_limit sleeps the wave gives up, counts a
+        // fault in g_meet_timeouts and flags the chunk for the tokenwise replay,
+        // which rewrites its outputs.
         auto meet = [&](int n) {
             if (lane == 0) __hip_atomic_fetch_add(&psync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            while (__hip_atomic_load(&psync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < L::NP * n)
+            int spins = 0;
+            while (__hip_atomic_load(&psync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < L::NP * n) {
+                if (spins++ >= spin_limit) {
+                    redol = 1;
+                    if (lane == 0) atomicAdd(&g_meet_timeouts, 1u);
+                    break;
+                }
                 __builtin_amdgcn_s_sleep(1);
+            }
         };
         rows_to_lds<D, 64 * L::NP>(ksl0, K, row0, stride, t_begin, N, tid, lane);
         FLARE_WAIT_VMCNT(0);
@@ -270,12 +293,22 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                 const bool moved = __any((emax > L::kLazyE) | dnbig);
                 if (moved) {
                     float gam[L::MTP][4];
+                    bool jump = false;
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
                             const float mx = row_max16(fmaxf(acc[mi][0][r], acc[mi][1][r])) * scale2;
                             float Rn = mx > R[mi][r] + kLazy ? mx : R[mi][r];
+                            // The running max of this latent at the subtile's first valid token:
+                            // R, or (no reference yet) the smallest valid score.  Tokens whose
+                            // running max lies more than kJumpMax below the new reference would
+                            // see their den underflow against it: such a chunk is replayed
+                            // tokenwise by the fp32 kernel afterwards.
+                            const float s0 = acc[mi][0][r] * scale2, s1 = acc[mi][1][r] * scale2;
+                            const float mn = -row_max16(fmaxf(s0 == kNegInf ? kNegInf : -s0, s1 == kNegInf ? kNegInf : -s1));
+                            const float base = R[mi][r] == kNegInf ? mn : R[mi][r];
+                            jump |= Rn - base > kJumpMax;
                             float g1 = exp2f_fast(R[mi][r] - Rn);                  // 0 when R = -inf
                             const float dd = dn[mi][r] * g1;
                             if (dd > kDenMax) {
@@ -286,6 +319,7 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
                             R[mi][r] = Rn;
                             dn[mi][r] *= gam[mi][r];     // E is recomputed on the general path
                         }
+                    if (jump) redol = 1;
                     refresh_ar();
                     rinf = false;
 #pragma unroll
@@ -692,6 +726,10 @@ __global__ __launch_bounds__(128 * NPW, 4 / NPW) void chunk_output_pc(
             __syncthreads();   // hand-off
         }
     }
+    if (redo != nullptr) {
+        __syncthreads();
+        if (tid == 0) redo[(size_t)bh * NC + c_idx] = redol;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1064,7 +1102,7 @@ int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, i
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, hipStream_t stream) {
+                     bool f16in, int* redo, hipStream_t stream) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
@@ -1074,7 +1112,7 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
 #define FLARE_OUT_PC_SEP(MM, DD, NW, SP, F)                                                                  \
     hipLaunchKernelGGL((chunk_output_pc<MM, DD, NW, SP, F>), grid, dim3(128 * NW), 0, stream, (const bf16*)Q, \
                        (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, pnum, Y,    \
-                       out_dtype, tmask, (const f16*)alpha)
+                       out_dtype, tmask, (const f16*)alpha, redo, g_spin_limit)
 #define FLARE_OUT_PC(MM, DD, NW)                                  \
     do {                                                          \
         if (f16in) {                                              \
@@ -1128,3 +1166,36 @@ int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, in
 }
 
 }  // namespace flare
+
+extern "C" {
+
+int flare_device_faults(void* stream, uint32_t* count, int reset) {
+    FLARE_REQUIRE(count != nullptr, "device_faults: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    unsigned int v = 0;
+    if (hipMemcpyFromSymbolAsync(&v, HIP_SYMBOL(flare::mfma::g_meet_timeouts), sizeof(v), 0, hipMemcpyDeviceToHost,
+                                 st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+        flare::set_error("device_faults: %s", hipGetErrorString(hipGetLastError()));
+        return FLARE_ERR_LAUNCH;
+    }
+    *count = v;
+    if (reset) {
+        const unsigned int z = 0;
+        if (hipMemcpyToSymbolAsync(HIP_SYMBOL(flare::mfma::g_meet_timeouts), &z, sizeof(z), 0, hipMemcpyHostToDevice,
+                                   st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            flare::set_error("device_faults: %s", hipGetErrorString(hipGetLastError()));
+            return FLARE_ERR_LAUNCH;
+        }
+    }
+    return FLARE_OK;
+}
+
+int flare_set_meet_spin_limit(int limit) {
+    FLARE_REQUIRE(limit >= 0, "set_meet_spin_limit: limit must be >= 0");
+    flare::mfma::g_spin_limit = limit;
+    return FLARE_OK;
+}
+
+}  // extern "C"

@@ -21,6 +21,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazy = 8.0f;            // log2 headroom before a reference max moves
 constexpr float kDenMax = 16.0f;         // den (relative to the reference) that moves it in the output kernel
+// Largest move of a latent's reference within one subtile (log2 units, ~66 nats) that the
+// MFMA output kernels resolve; beyond it the earlier tokens' den would approach the fp32
+// underflow against the new reference, and the chunk is replayed tokenwise in fp32.
+constexpr float kJumpMax = 96.0f;
 constexpr float kF16Max = 65504.0f;
 constexpr int kMaxPrepM = 256;           // largest latent bank of the prepare kernel (8 waves)
 

@@ -82,7 +82,10 @@ int flare_chunk_output(const void* Q, const void* K, const void* V, const void* 
                        const float* prefix_max, const float* prefix_den, const float* prefix_num,
                        void* Y, int out_dtype, float* lse_dec, void* stream);
 
-/* Bytes of fp32 workspace flare_ar_forward needs (chunk summaries). */
+/* Bytes of workspace flare_ar_forward needs: the fp32 chunk summaries and one
+ * int per (b*h, chunk) on which the MFMA output kernel marks the chunks it
+ * hands to the tokenwise fp32 replay (a latent whose score jumps more than
+ * ~66 nats above its running max within one 32-token subtile). */
 size_t flare_ar_forward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv,
                                        int64_t chunk);
 /*
@@ -196,6 +199,21 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                           int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,
                           void* Y, int out_dtype, float* lse_dec, float* lse_enc,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Diagnostics (no counterpart in the reference, whose Triton kernels have no
+ * bounded waits).  The producer waves of the bf16/fp16 output kernel meet once
+ * per 32-token subtile at a workgroup-local counter; the wait is bounded.  A
+ * wait that gives up flags its chunk for the tokenwise fp32 replay (so the
+ * output stays correct) and increments a device-wide fault counter.
+ * flare_device_faults synchronises `stream`, reads the counter of the current
+ * device into *count and, if `reset` is nonzero, sets it to 0.
+ * flare_set_meet_spin_limit sets the number of sleeps (about 64 clocks each)
+ * before a wait gives up, for kernels launched afterwards by this process
+ * (default 1 << 20, about 28 ms); tests use 0 to force the fault path.
+ */
+int flare_device_faults(void* stream, uint32_t* count, int reset);
+int flare_set_meet_spin_limit(int limit);
 
 #ifdef __cplusplus
 }

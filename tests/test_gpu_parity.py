@@ -104,17 +104,91 @@ def test_cfg2_chunked_prefill_bf16():
     assert_parity(y, ref, torch.bfloat16, "cfg2")
 
 
-def test_cfg3_long_context_bf16_two_heads():
-    """BASELINE config 3 (B=1, N=65536, H=16, M=256, D=128, bf16, seed 2) on the
-    GPU for all heads; the oracle checks heads 0 and 9 at full length."""
+def test_cfg3_long_context_bf16():
+    """BASELINE config 3 (B=1, N=65536, H=16, M=256, D=128, bf16, seed 2): every
+    head against the oracle at full length."""
     from causal_flare import flare_autoregressive_triton
     _print_case("cfg3")
     q, k, v = _cfg_inputs(2, 1, 65536, 16, 256, 128, torch.bfloat16)
     y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV)).cpu()
-    assert torch.isfinite(y.float()).all()
-    for h in (0, 9):
-        ref = O.ar_chunked(q[h:h + 1], k[:, :, h:h + 1], v[:, :, h:h + 1], scale=128 ** -0.5, nthreads=16)
-        assert_parity(y[:, :, h:h + 1], ref, torch.bfloat16, f"cfg3 head {h}")
+    ref = O.ar_chunked(q, k, v, scale=128 ** -0.5, nthreads=16)
+    assert_parity(y, ref, torch.bfloat16, "cfg3 all heads")
+
+
+def _jump_keys(q, k, tokens, lat, nats, scale):
+    """Key outliers: at each token in `tokens`, the key of every head points along
+    the sum of the latent directions `lat`, scaled so that the smallest of those
+    latents' scores is `nats`; their references jump by far more than the fp32
+    range covers within one 32-token subtile."""
+    k = k.clone().float()
+    qf = q.float()
+    for h in range(q.shape[0]):
+        u = sum(qf[h, m] / qf[h, m].norm() for m in lat)
+        s = torch.stack([qf[h, m] @ u for m in lat]).min() * scale
+        for t in tokens:
+            k[:, t, h] = u * (nats / float(s))
+    return k.to(q.dtype)
+
+
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_score_jump_within_subtile(M, D, dtype):
+    """A latent whose score jumps by ~150 nats in the middle of a 32-token subtile
+    (one in chunk 0 with no reference yet, one deep in a later chunk): the earlier
+    tokens of that subtile must keep the latent, as in the tokenwise recurrence
+    (training.py:1351-1371).  The MFMA output kernel flags such chunks and the
+    tokenwise fp32 kernel replays them."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("score_jump", M, D, dtype)
+    B, N, H = 2, 1100, 2
+    q, k, v = seeded(404 + M, B, N, H, M, D, D, dtype, q_std=D ** -0.5)
+    scale = D ** -0.5
+    k = _jump_keys(q, k, [17, 256 + 3 * 32 + 17, 900 + 9], lat=list(range(0, M, M // 8)), nats=150.0,
+                   scale=scale)
+    for chunk in (None, 256):
+        y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), chunk_size=chunk)
+        ref = O.ar_chunked(q, k, v, scale=scale, nthreads=16)
+        assert_parity(y, ref, dtype, f"score jump M={M} D={D} chunk={chunk}")
+
+
+def test_meeting_timeout_falls_back_to_tokenwise_replay():
+    """The producer meeting of the output kernel is a bounded wait.  With the bound
+    forced to zero from the host, waits give up: the kernel counts the faults and
+    flags the chunks, and the tokenwise fp32 replay still gives the right output."""
+    from causal_flare import _lib, flare_autoregressive_triton
+    _print_case("meet_timeout")
+    q, k, v = seeded(31, 2, 1000, 2, 128, 64, 64, torch.bfloat16, q_std=64 ** -0.5)
+    ref = O.ar_chunked(q, k, v, nthreads=16)
+    _lib.device_faults(reset=True)
+    _lib.set_meet_spin_limit(0)
+    try:
+        y = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), chunk_size=256)
+        faults = _lib.device_faults(reset=True)
+    finally:
+        _lib.set_meet_spin_limit(1 << 20)
+    assert_parity(y, ref, torch.bfloat16, "forced meeting timeouts")
+    assert faults > 0, "a zero spin limit should make some producer give up"
+    y2 = flare_autoregressive_triton(q.to(DEV), k.to(DEV), v.to(DEV), chunk_size=256)
+    assert _lib.device_faults() == 0, "no faults with the default bound"
+    assert_parity(y2, ref, torch.bfloat16, "default bound")
+
+
+def test_score_jump_prefill_with_state_bf16():
+    """The same jump in a prefill continued from a cached state, with a token mask."""
+    from causal_flare import flare_autoregressive_prefill_triton
+    _print_case("score_jump_prefill")
+    B, T, H, M, D = 2, 700, 2, 128, 64
+    q, k, v = seeded(77, B, 2 * T, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    k = _jump_keys(q, k, [T + 40 + 17, T + 500 + 5], lat=list(range(0, M, 16)), nats=150.0, scale=1.0)
+    _, st = flare_autoregressive_prefill_triton(q.to(DEV), k[:, :T].to(DEV), v[:, :T].to(DEV))
+    _, st_o = O.ar_recurrent(q, k[:, :T], v[:, :T], nthreads=16)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[1, 30:50] = 0
+    y, st2 = flare_autoregressive_prefill_triton(q.to(DEV), k[:, T:].to(DEV), v[:, T:].to(DEV), state=st,
+                                                 attention_mask=mask.to(DEV))
+    y_ref, st_ref = O.ar_recurrent(q, k[:, T:], v[:, T:], state=st_o, attention_mask=mask, nthreads=16)
+    assert_parity(y, y_ref, torch.bfloat16, "score jump prefill")
+    assert_state_parity(st2, st_ref, torch.bfloat16, "score jump prefill")
 
 
 # --------------------------------------------------------------------------
@@ -242,25 +316,28 @@ def test_masked_prefill_leading_tokens_fp32():
 
 
 def test_cfg4_decode_bf16():
-    """BASELINE config 4 (reduced steps): B=64, H=16, M=128, D=64, 2048-token prefill then decode."""
+    """B=64, H=16, M=128, D=64, 2048-token prefill, then all 256
+    decode steps, each output and the final in-place fp32 state against the oracle."""
     from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
     _print_case("cfg4")
-    B, T, H, M, D, steps = 64, 2048, 16, 128, 64, 4
+    B, T, H, M, D, steps = 64, 2048, 16, 128, 64, 256
     torch.manual_seed(3)
     q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16)
     k = torch.randn(B, T + steps, H, D).to(torch.bfloat16)
     v = torch.randn(B, T + steps, H, D).to(torch.bfloat16)
     qg, kg, vg = q.to(DEV), k.to(DEV), v.to(DEV)
     y, st = flare_autoregressive_prefill_triton(qg, kg[:, :T], vg[:, :T])
+    u0 = st["u"]
     ys = []
     for t in range(T, T + steps):
         y_t, st = flare_autoregressive_decode_triton(qg, kg[:, t], vg[:, t], state=st)
         ys.append(y_t)
+    assert st["u"] is u0, "decode must update the state in place"
     y_dec = torch.cat(ys, dim=1)
     ref, st_ref = O.ar_recurrent(q, k, v, nthreads=16)
     assert_parity(y, ref[:, :T], torch.bfloat16, "cfg4 prefill")
-    assert_parity(y_dec, ref[:, T:], torch.bfloat16, "cfg4 decode")
-    assert_state_parity(st, st_ref, torch.bfloat16, "cfg4")
+    assert_parity(y_dec, ref[:, T:], torch.bfloat16, "cfg4 decode (256 steps)")
+    assert_state_parity(st, st_ref, torch.bfloat16, "cfg4 after 256 steps")
 
 
 def test_decode_masked_rows_keep_state():
