@@ -33,6 +33,8 @@ HEADER_FUNCTIONS = (
     "flare_semi_ar_forward",
     "flare_semi_ar_backward_workspace_size",
     "flare_semi_ar_backward",
+    "flare_ar_forward_noalloc_max_bytes",
+    "flare_ar_forward_noalloc",
     "flare_device_faults",
     "flare_set_meet_spin_limit",
 )
@@ -86,6 +88,11 @@ def _declare(lib):
     lib.flare_semi_ar_backward_workspace_size.argtypes = [_i64] * 7
     lib.flare_semi_ar_backward.restype = _i
     lib.flare_semi_ar_backward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 7 + [_vp, _sz, _vp])
+    lib.flare_ar_forward_noalloc_max_bytes.restype = _sz
+    lib.flare_ar_forward_noalloc_max_bytes.argtypes = []
+    lib.flare_ar_forward_noalloc.restype = _i
+    lib.flare_ar_forward_noalloc.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 6
+                                             + [_vp, _i, _vp, _vp])
     lib.flare_device_faults.restype = _i
     lib.flare_device_faults.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint32), _i]
     lib.flare_set_meet_spin_limit.restype = _i

@@ -13,6 +13,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "flare_common.h"
 #include "flare_internal.h"
 
@@ -610,6 +612,75 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
                          cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws, redo);
+}
+
+// ---------------------------------------------------------------------------
+// flare_ar_forward_noalloc: flare_ar_forward_masked on a fixed device scratch
+// array instead of a caller workspace, for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace flare {
+// The workspace of flare_ar_forward_noalloc: chunk summaries, the output kernel's
+// redo flags and (separate decoder tensors) the decoder softmax.  One copy per
+// GPU, held until the process ends; every call on a GPU shares it.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices] = {};
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device, looked up once per device.
+static int scratch_ptr(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error("ar_forward_noalloc: no usable current device");
+        return FLARE_ERR_LAUNCH;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error("ar_forward_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return FLARE_ERR_LAUNCH;
+        }
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return FLARE_OK;
+}
+}  // namespace flare
+
+extern "C" {
+
+size_t flare_ar_forward_noalloc_max_bytes(void) { return flare::kScratchBytes; }
+
+int flare_ar_forward_noalloc(const void* Q, const void* K, const void* V, const void* Qdec,
+                             const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                             int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                             const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                             void* Y, int out_dtype, const int32_t* token_mask, void* stream) {
+    FLARE_REQUIRE(Q && K && V && Y, "ar_forward_noalloc: null pointer");
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0,
+                  "ar_forward_noalloc: sizes must be positive");
+    if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
+    // the separate-decoder workspace when it fits (MFMA path), else the plain one
+    size_t bytes = flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk);
+    FLARE_REQUIRE(bytes <= kScratchBytes,
+                  "ar_forward_noalloc: needs %zu bytes of scratch, the maximum is %zu "
+                  "(B*H*ceil(N/chunk)*M*(2+Dv)*4 bytes of chunk summaries)",
+                  bytes, kScratchBytes);
+    if (Qdec || Kdec) {
+        const size_t sep = flare_ar_forward_workspace_size_sep(B, N, H, M, Dv, chunk);
+        if (sep <= kScratchBytes) bytes = sep;
+    }
+    void* ws = nullptr;
+    const int rc = scratch_ptr(&ws);
+    if (rc) return rc;
+    return flare_ar_forward_masked(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, m0, d0, u0,
+                                   m_fin, d_fin, u_fin, Y, out_dtype, token_mask, ws, bytes, stream);
 }
 
 }  // extern "C"

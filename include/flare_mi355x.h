@@ -201,6 +201,27 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * flare_ar_forward_masked without a workspace argument: its chunk summaries, redo
+ * flags and (separate decoder tensors) decoder softmax live in a fixed device
+ * array of the library, one copy per GPU, held until the process ends.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it calls no allocating routine.  A call whose workspace
+ * (flare_ar_forward_workspace_size) exceeds flare_ar_forward_noalloc_max_bytes()
+ * (64 MiB) returns FLARE_ERR_INVALID before launching anything; separate decoder
+ * tensors use the MFMA path when flare_ar_forward_workspace_size_sep also fits,
+ * else the scalar kernels.  Every call on a GPU shares its array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be serialised
+ * by the caller.
+ */
+size_t flare_ar_forward_noalloc_max_bytes(void);
+int flare_ar_forward_noalloc(const void* Q, const void* K, const void* V, const void* Qdec,
+                             const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                             int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* m0,
+                             const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                             void* Y, int out_dtype, const int32_t* token_mask, void* stream);
+
+/*
  * Diagnostics (no counterpart in the reference, whose Triton kernels have no
  * bounded waits).  The producer waves of the bf16/fp16 output kernel meet once
  * per 32-token subtile at a workgroup-local counter; the wait is bounded.  A
