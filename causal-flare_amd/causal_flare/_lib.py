@@ -13,7 +13,8 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "_lib", "libflare_mi355x.so")
+# FLARE_LIB_PATH names another build of the same library (A/B comparisons of kernel variants).
+LIB_PATH = os.environ.get("FLARE_LIB_PATH") or os.path.join(_HERE, "_lib", "libflare_mi355x.so")
 HEADER_FUNCTIONS = (
     "flare_abi_version",
     "flare_last_error",

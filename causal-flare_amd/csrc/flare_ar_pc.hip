@@ -1106,6 +1106,9 @@ int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    if (output_tr_enabled())
+        return launch_output_tr(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, alpha,
+                                f16in, redo, g_spin_limit, stream);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
@@ -1179,7 +1182,12 @@ int flare_device_faults(void* stream, uint32_t* count, int reset) {
         flare::set_error("device_faults: %s", hipGetErrorString(hipGetLastError()));
         return FLARE_ERR_LAUNCH;
     }
-    *count = v;
+    unsigned int vt = 0;
+    if (flare::meet_timeouts_tr(st, &vt, reset != 0) != FLARE_OK) {
+        flare::set_error("device_faults: %s", hipGetErrorString(hipGetLastError()));
+        return FLARE_ERR_LAUNCH;
+    }
+    *count = v + vt;
     if (reset) {
         const unsigned int z = 0;
         if (hipMemcpyToSymbolAsync(HIP_SYMBOL(flare::mfma::g_meet_timeouts), &z, sizeof(z), 0, hipMemcpyHostToDevice,

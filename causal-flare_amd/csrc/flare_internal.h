@@ -44,6 +44,21 @@ inline bool output_pc_enabled() {
     }();
     return on;
 }
+// FLARE_OUTPUT_KERNEL=pc keeps the earlier producer / consumer phase-3 kernel
+// (partial G summed by the consumers) instead of chunk_output_tr (A/B checks).
+inline bool output_tr_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("FLARE_OUTPUT_KERNEL");
+        return !(e && e[0] == 'p');
+    }();
+    return on;
+}
+int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
+                     const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
+                     bool f16in, int* redo, int spin_limit, hipStream_t stream);
+// Meetings of chunk_output_tr that gave up waiting (optionally reset to 0).
+int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset);
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, bool f16in, hipStream_t stream);
