@@ -110,9 +110,9 @@ def bench_prefill(torch, flare, steps, warmup):
         "ms_per_step_eager": dt_eager * 1e3 / steps, "tok_s_eager_api_loop": B * N * steps / dt_eager,
         "phase_ms": phases, "alg_tflop_per_step": flops / 1e12,
         "roofline": {
-            "bound": "mfma", "kernel": "chunk_output_pc", "achieved": achieved,
+            "bound": "mfma", "kernel": "chunk_output_tr", "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": measured_traffic("traffic_cfg3_prefill.txt", "chunk_output_pc"),
+            "traffic": measured_traffic("traffic_cfg3_prefill.txt", "chunk_output_tr"),
             "kernel_ms": dom_ms, "alg_flop_per_launch": flops,
             "timing": f"mean of {steps} back-to-back launches, HIP events on the launch stream",
             "whole_pass_tflops": whole, "whole_pass_frac": whole / PEAK_BF16_TFLOPS,
@@ -328,6 +328,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--only", choices=("prefill", "decode"), default=None,
+                    help="run one workload alone (profiler passes); the JSON line then holds that part only")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a plain 1 GiB device-to-device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -338,6 +340,14 @@ def main():
     import torch
     import causal_flare as flare
 
+    if args.only is not None:
+        part = (bench_prefill(torch, flare, args.steps, args.warmup) if args.only == "prefill"
+                else bench_decode(torch, flare))
+        part.pop("final_state", None)
+        print(json.dumps({"only": args.only, **part}))
+        if args.calibration_copy:
+            calibration_copy(torch)
+        return
     pre = bench_prefill(torch, flare, args.steps, args.warmup)
     dec = None if args.no_decode else bench_decode(torch, flare)
     others = None if args.no_decode else bench_others(torch, flare)
@@ -369,10 +379,15 @@ def main():
     }
     print(json.dumps(out))
     if args.calibration_copy:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
+        calibration_copy(torch)
+
+
+def calibration_copy(torch):
+    """A plain 1 GiB device-to-device copy: the known-size kernel that scales the HBM byte counters."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 if __name__ == "__main__":

@@ -80,12 +80,46 @@ struct TrLayout {
     static constexpr int DC = 32;
     static constexpr int DTC = 2;
     static constexpr int KS = D / 32;            // k-steps of the scores
-    static constexpr int RP = M + 24;            // row pitch (halves) of E[tau][m] and W[t][m]
+    // Row pitch (halves) of E[tau][m] and W[t][m]: M + 48 keeps every read pattern used
+    // below at the LDS's full rate on gfx950 (measured: 16-byte reads down 16 rows, and the
+    // transposed 8-byte reads of 4 consecutive rows with either column pattern); pitches
+    // such as M + 24 or M + 36 cost 1.5x to 12x on one of them.
+    static constexpr int RPW = M + 48;
+    static constexpr int RPE = M + 48;
     static constexpr int VP = DC + 8;            // row pitch (halves) of a consumer's V[tau][d]
     static constexpr float kVCap = 2048.0f;      // bound on |V'| and |z'| (fp16 operands)
     static constexpr float kLazyE = 256.0f;      // 2^kLazy: an E above it moves the reference
     static constexpr float kTinyL = 0x1p-100f;   // smallest softmax partial of the common path
 };
+
+// Sum / max over the four 16-lane rows (lanes c, c+16, c+32, c+48) with the gfx950
+// lane swaps (rows 0<->1, 2<->3, then halves 0-31 <-> 32-63): VALU only, no LDS.
+// v_permlane16/32_swap exchange rows between their two operands; given x in two
+// distinct registers, each lane then holds x from itself and from its partner.  The
+// second operand is an opaque copy so that the two never share a register, and the
+// two results pass through an empty asm before they are combined: this compiler
+// otherwise folds the second result of the intrinsic into the first.
+__device__ __forceinline__ void lane_pair(unsigned& r0, unsigned& r1, unsigned x, bool rows32) {
+    unsigned xc = x;
+    asm volatile("" : "+v"(xc));
+    const auto p = rows32 ? __builtin_amdgcn_permlane32_swap(x, xc, false, false)
+                          : __builtin_amdgcn_permlane16_swap(x, xc, false, false);
+    r0 = p[0];
+    r1 = p[1];
+    asm volatile("" : "+v"(r0), "+v"(r1));
+}
+template <bool MAX>
+__device__ __forceinline__ float rows_reduce4(float x) {
+    unsigned r0, r1;
+    lane_pair(r0, r1, __builtin_bit_cast(unsigned, x), false);
+    const float y = MAX ? fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1))
+                        : __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+    lane_pair(r0, r1, __builtin_bit_cast(unsigned, y), true);
+    return MAX ? fmaxf(__builtin_bit_cast(float, r0), __builtin_bit_cast(float, r1))
+               : __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float rows_sum4_pl(float x) { return rows_reduce4<false>(x); }
+__device__ __forceinline__ float rows_max4_pl(float x) { return rows_reduce4<true>(x); }
 
 // (tau(g, e) <= t): the causal mask in operand slot order
 __device__ __forceinline__ int tau_slot(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
@@ -101,8 +135,8 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     // K rows of the even / odd subtiles (swizzled, filled by DMA)
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
     __shared__ __attribute__((aligned(16))) bf16 ksl1[T * D];
-    __shared__ __attribute__((aligned(16))) f16 erl[2][T * L::RP];            // E[tau][m] (fp16)
-    __shared__ __attribute__((aligned(16))) f16 wl[2][T * L::RP];             // W1[t][m] (fp16)
+    __shared__ __attribute__((aligned(16))) f16 erl[2][T * L::RPE];            // E[tau][m] (fp16)
+    __shared__ __attribute__((aligned(16))) f16 wl[2][T * L::RPW];             // W1[t][m] (fp16)
     __shared__ __attribute__((aligned(16))) f16 vrl[L::NC][T * L::VP];        // V'[tau][d], consumer-private
     __shared__ __attribute__((aligned(16))) f32x4 gpl[2][L::NP][3][64];       // general-path G^T tiles
     __shared__ __attribute__((aligned(16))) float2 lsep[2][L::NP][T];         // (reference, partial) per token
@@ -166,7 +200,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
             for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mx = fmaxf(mx, R[mi][r]);
-            Cw = rows_max4(mx);
+            Cw = rows_max4_pl(mx);
 #pragma unroll
             for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
@@ -231,19 +265,20 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 f32x4 acc[L::MTP][2];
 #pragma unroll
                 for (int mi = 0; mi < L::MTP; ++mi) acc[mi][0] = acc[mi][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                bf16x8 kb[L::KS][2];
 #pragma unroll
-                for (int kq = 0; kq < L::KS; ++kq) {
-                    bf16x8 kb[2];
+                for (int kq = 0; kq < L::KS; ++kq)
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
                         const int row = 16 * ti + c;
-                        kb[ti] = load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g));
+                        kb[kq][ti] = load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g));
                     }
+#pragma unroll
+                for (int kq = 0; kq < L::KS; ++kq)
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma_in<F16>(qa[mi][kq], kb[ti], acc[mi][ti]);
-                }
+                        for (int ti = 0; ti < 2; ++ti) acc[mi][ti] = mma_in<F16>(qa[mi][kq], kb[kq][ti], acc[mi][ti]);
                 bool valid[2];
 #pragma unroll
                 for (int ti = 0; ti < 2; ++ti) valid[ti] = t0 + 16 * ti + c < t_end && keep[ti];
@@ -340,8 +375,8 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
                                 for (int r = 0; r < 4; ++r) part[ti] = fmaf(e[mi][ti][r], A[mi][r], part[ti]);
-                        part[0] = rows_sum4(part[0]);
-                        part[1] = rows_sum4(part[1]);
+                        part[0] = rows_sum4_pl(part[0]);
+                        part[1] = rows_sum4_pl(part[1]);
                         slow = __any((valid[0] & (part[0] < L::kTinyL)) | (valid[1] & (part[1] < L::kTinyL)));
                     }
                     if (slow) {
@@ -355,7 +390,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                 sc[mi] = scores(mi, ti);
                                 mx = max3_raw(mx, max3_raw(sc[mi][0], sc[mi][1], sc[mi][2]), sc[mi][3]);
                             }
-                            const float lm = rows_max4(mx) * scale2;
+                            const float lm = rows_max4_pl(mx) * scale2;
                             float ls = 0.0f;
 #pragma unroll
                             for (int mi = 0; mi < L::MTP; ++mi)
@@ -363,7 +398,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                 for (int r = 0; r < 4; ++r)
                                     ls += lm == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[mi][r], scale2, -lm));
                             ref[ti] = lm;
-                            part[ti] = rows_sum4(ls);
+                            part[ti] = rows_sum4_pl(ls);
                         }
                     }
                     if (g == 0) {
@@ -375,9 +410,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
                         const float2 pr = g < L::NP ? lsep[buf][g][16 * ti + c] : float2{kNegInf, 0.0f};
-                        const float mm = rows_max4(pr.x);
+                        const float mm = rows_max4_pl(pr.x);
                         const float s = pr.y > 0.0f ? pr.y * exp2f_fast(pr.x - mm) : 0.0f;
-                        const float ss = rows_sum4(s);
+                        const float ss = rows_sum4_pl(s);
                         f[ti] = (ss > 0.0f && ref[ti] != kNegInf) ? exp2f_fast(ref[ti] - mm) * __builtin_amdgcn_rcpf(ss)
                                                                  : 0.0f;
                     }
@@ -393,15 +428,15 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                     for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                         for (int ti = 0; ti < 2; ++ti)
-                            *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RP + mp0 + 16 * mi + 4 * g) =
+                            *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RPE + mp0 + 16 * mi + 4 * g) =
                                 __builtin_convertvector((f32x4{e[mi][ti][0], e[mi][ti][1], e[mi][ti][2], e[mi][ti][3]}),
                                                         f16x4);
                     f32x4 dcum[L::MTP][2];
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi) {
                         const f16* col = er + mp0 + 16 * mi + 4 * (c & 3);
-                        const f16x8 ea = cat8<f16x8>(lds_tr4(col + (4 * g + (c >> 2)) * L::RP),
-                                                     lds_tr4(col + (16 + 4 * g + (c >> 2)) * L::RP));
+                        const f16x8 ea = cat8<f16x8>(lds_tr4(col + (4 * g + (c >> 2)) * L::RPE),
+                                                     lds_tr4(col + (16 + 4 * g + (c >> 2)) * L::RPE));
                         const f32x4 d0 = f32x4{dn[mi][0], dn[mi][1], dn[mi][2], dn[mi][3]};
 #pragma unroll
                         for (int ti = 0; ti < 2; ++ti) dcum[mi][ti] = mma(ea, tri[ti], d0);
@@ -416,7 +451,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                 const float p = SEP ? (float)af[mi][ti][r] : e[mi][ti][r] * (A[mi][r] * f[ti]);
                                 q[r] = p * __builtin_amdgcn_rcpf(dcum[mi][ti][r]);
                             }
-                            *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::RP + mp0 + 16 * mi + 4 * g) =
+                            *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::RPW + mp0 + 16 * mi + 4 * g) =
                                 __builtin_convertvector(q, f16x4);
                         }
 #pragma unroll
@@ -450,7 +485,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             f32x4 dcum[2];
 #pragma unroll
                             for (int ti = 0; ti < 2; ++ti)
-                                *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RP + mp0 + 16 * mi + 4 * g) =
+                                *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RPE + mp0 + 16 * mi + 4 * g) =
                                     __builtin_convertvector((f32x4{em[ti][0], em[ti][1], em[ti][2], em[ti][3]}), f16x4);
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {
@@ -472,7 +507,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                 }
                                 split_bf16x4(em[ti][0], em[ti][1], em[ti][2], em[ti][3], ehi[jb][ti], elo[jb][ti]);
                                 split_bf16x4(q[0], q[1], q[2], q[3], whi[jb][ti], wlo[jb][ti]);
-                                *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::RP + mp0 + 16 * mi + 4 * g) = w1;
+                                *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::RPW + mp0 + 16 * mi + 4 * g) = w1;
                             }
 #pragma unroll
                             for (int r = 0; r < 4; ++r) {
@@ -508,16 +543,20 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         // =========================== consumer ===========================
         const int cw = w - L::NP;
         const int dc0 = cw * L::DC;
-        f32x4 U[L::MTA][L::DTC];     // U[m = 16 mi + 4 g + r][d = dc0 + 16 di + c]
+        // U[mi][di][r] = U[m][d = dc0 + 16 di + c] for latent m = lat(mi, g) + r: lane row g holds
+        // the 8 consecutive latents 32 k + 8 g .. + 7 of each 32-latent k-step k in tiles 2 k and
+        // 2 k + 1, so that one 16-byte LDS read gives the matching W or E operand of the readout
+        auto lat = [](int mi, int gg) { return 32 * (mi >> 1) + 8 * gg + 4 * (mi & 1); };
+        f32x4 U[L::MTA][L::DTC];
 #pragma unroll
         for (int mi = 0; mi < L::MTA; ++mi)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float pd = pden[pbase + 16 * mi + 4 * g + r];
+                const float pd = pden[pbase + lat(mi, g) + r];
                 const float ip = pd > 0.0f ? 1.0f / pd : 0.0f;
 #pragma unroll
                 for (int di = 0; di < L::DTC; ++di)
-                    U[mi][di][r] = pnum[(pbase + 16 * mi + 4 * g + r) * D + dc0 + 16 * di + c] * ip;
+                    U[mi][di][r] = pnum[(pbase + lat(mi, g) + r) * D + dc0 + 16 * di + c] * ip;
             }
         // The wave keeps V' = V vs and U' = U vs with vs a power of two <= 1 chosen so
         // that |V'| and the prefix's |z'| stay below kVCap: every fp16 operand below is
@@ -612,12 +651,12 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
 #pragma unroll
                     for (int mt = 0; mt < L::MTP; ++mt) {
                         const int mi = w2 * L::MTP + mt;
-                        const f32x4 da = *reinterpret_cast<const f32x4*>(d0l[buf] + 16 * mi + 4 * g);
+                        const f32x4 da = *reinterpret_cast<const f32x4*>(d0l[buf] + lat(mi, g));
                         f32x4 gm;
                         if (back) {
                             gm = da;
                         } else {
-                            const f32x4 ga = *reinterpret_cast<const f32x4*>(gaml[buf] + 16 * mi + 4 * g);
+                            const f32x4 ga = *reinterpret_cast<const f32x4*>(gaml[buf] + lat(mi, g));
 #pragma unroll
                             for (int r = 0; r < 4; ++r) gm[r] = da[r] > 0.0f ? ga[r] / da[r] : 0.0f;
                         }
@@ -635,37 +674,49 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 for (int di = 0; di < L::DTC; ++di) yt[di][0] = yt[di][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int q3 = 0; q3 < 3; ++q3) gt[q3] = f32x4{0.f, 0.f, 0.f, 0.f};
+                // W rows (B operands: t = 16 ti + c, the k-step's latent slots) and E rows
+                // (A operands of G^T: tau = 16 ui + c) of k-step kk, fetched one step ahead.  The
+                // loop comes in two copies: without a general-path producer (the common case) it
+                // has no branch, so the loads of one step overlap the MFMAs of the previous one.
+                auto fused = [&](auto any_general) {
+                    constexpr bool AG = decltype(any_general)::value;
+                    f16x8 wbn[2], ean[2];
+                    auto fetch = [&](int kk) {
 #pragma unroll
-                for (int kk = 0; kk < L::MK; ++kk) {
-                    f16x8 wb[2];
-#pragma unroll
-                    for (int ti = 0; ti < 2; ++ti) {
-                        const f16* wr = wq + (16 * ti + c) * L::RP + 32 * kk + 4 * g;
-                        wb[ti] = cat8<f16x8>(load4<f16x4>(wr), load4<f16x4>(wr + 16));
-                    }
-#pragma unroll
-                    for (int di = 0; di < L::DTC; ++di) {
-                        f16x8 za;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            za[r] = (f16)U[2 * kk][di][r];
-                            za[4 + r] = (f16)U[2 * kk + 1][di][r];
+                        for (int q = 0; q < 2; ++q) {
+                            wbn[q] = load8<f16x8>(wq + (16 * q + c) * L::RPW + 32 * kk + 8 * g);
+                            ean[q] = load8<f16x8>(er + (16 * q + c) * L::RPE + 32 * kk + 8 * g);
                         }
+                    };
+                    fetch(0);
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) yt[di][ti] = mma(za, wb[ti], yt[di][ti]);
-                    }
-                    if (!(mv[kk / L::MKP] & 2)) {
-                        f16x8 ea[2];
+                    for (int kk = 0; kk < L::MK; ++kk) {
+                        const f16x8 wb[2] = {wbn[0], wbn[1]};
+                        const f16x8 ea[2] = {ean[0], ean[1]};
+                        if (kk + 1 < L::MK) fetch(kk + 1);
 #pragma unroll
-                        for (int ui = 0; ui < 2; ++ui) {
-                            const f16* erw = er + (16 * ui + c) * L::RP + 32 * kk + 4 * g;
-                            ea[ui] = cat8<f16x8>(load4<f16x4>(erw), load4<f16x4>(erw + 16));
+                        for (int di = 0; di < L::DTC; ++di) {
+                            f16x8 za;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                za[r] = (f16)U[2 * kk][di][r];
+                                za[4 + r] = (f16)U[2 * kk + 1][di][r];
+                            }
+#pragma unroll
+                            for (int ti = 0; ti < 2; ++ti) yt[di][ti] = mma(za, wb[ti], yt[di][ti]);
                         }
-                        gt[0] = mma(ea[0], wb[0], gt[0]);
-                        gt[1] = mma(ea[0], wb[1], gt[1]);
-                        gt[2] = mma(ea[1], wb[1], gt[2]);
+                        if (!AG || !(mv[kk / L::MKP] & 2)) {
+                            gt[0] = mma(ea[0], wb[0], gt[0]);
+                            gt[1] = mma(ea[0], wb[1], gt[1]);
+                            gt[2] = mma(ea[1], wb[1], gt[2]);
+                        }
                     }
-                }
+                };
+                int anyg = 0;
+#pragma unroll
+                for (int w2 = 0; w2 < L::NP; ++w2) anyg |= mv[w2];
+                if (anyg & 2) fused(std::true_type{});
+                else fused(std::false_type{});
 #pragma unroll
                 for (int w2 = 0; w2 < L::NP; ++w2) {
                     if (mv[w2] & 1) normalise(w2, true);    // back from z0 to the (rescaled) numerator
@@ -705,9 +756,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 // ---- U' += E^T V' (E^T read transposed from the E rows)
 #pragma unroll
                 for (int mi = 0; mi < L::MTA; ++mi) {
-                    const f16* col = er + 16 * mi + 4 * (c & 3);
-                    const f16x8 et = cat8<f16x8>(lds_tr4(col + (4 * g + (c >> 2)) * L::RP),
-                                                 lds_tr4(col + (16 + 4 * g + (c >> 2)) * L::RP));
+                    const f16* col = er + 32 * (mi >> 1) + 4 * (mi & 1) + 8 * (c & 3);   // latents lat(mi, .)
+                    const f16x8 et = cat8<f16x8>(lds_tr4(col + (4 * g + (c >> 2)) * L::RPE),
+                                                 lds_tr4(col + (16 + 4 * g + (c >> 2)) * L::RPE));
 #pragma unroll
                     for (int di = 0; di < L::DTC; ++di) U[mi][di] = mma(et, va[di], U[mi][di]);
                 }
