@@ -124,6 +124,40 @@ __device__ __forceinline__ float rows_max4_pl(float x) { return rows_reduce4<tru
 // (tau(g, e) <= t): the causal mask in operand slot order
 __device__ __forceinline__ int tau_slot(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
+// K rows of one subtile by DMA straight into swizzled LDS rows (global_load_lds, no
+// registers).  Each thread's NK 16-byte pieces keep their row and column from one
+// subtile to the next, so their global addresses are formed once and advanced by T rows.
+template <int D, int NTHR>
+struct KDma {
+    static constexpr int KC = D / 8;
+    static constexpr int NK = T * KC / NTHR;
+    static_assert(T * KC % NTHR == 0, "the producers' threads must divide the K pieces of a subtile");
+    const bf16* src[NK];
+    __device__ __forceinline__ void init(const bf16* K, size_t row0, size_t stride, int t_begin, int tid) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int e = tid + k * NTHR;
+            src[k] = K + row0 + (size_t)(t_begin + e / KC) * stride + 8 * swz<D>(e / KC, e % KC);
+        }
+    }
+    // Rows t0 .. t0+T of subtile j (t0 = t_begin + T j) into dst; rows at or past nrows read
+    // row nrows - 1 (the caller masks their scores).
+    __device__ __forceinline__ void issue(bf16* dst, int j, int t0, int nrows, size_t stride, int tid,
+                                          int lane) const {
+        const size_t adv = (size_t)j * T * stride;
+        if (t0 + T <= nrows) {
+#pragma unroll
+            for (int k = 0; k < NK; ++k) global_to_lds16(src[k] + adv, dst + (tid + k * NTHR - lane) * 8);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const int t = t0 + (tid + k * NTHR) / KC, tc = min(t, nrows - 1);
+                global_to_lds16(src[k] + adv - (size_t)(t - tc) * stride, dst + (tid + k * NTHR - lane) * 8);
+            }
+        }
+    }
+};
+
 template <int M, int D, bool SEP, bool F16>
 __global__ __launch_bounds__(64 * (M / 64 + D / 32), (512 / (64 * (M / 64 + D / 32))) > 0 ? 512 / (64 * (M / 64 + D / 32)) : 1)
 void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N,
@@ -180,6 +214,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         // reference starts at the prefix's log-sum-exp: den = 1, U = z.  R is the same on the
         // 16 lanes of a row (latent m = mp0 + 16 mi + 4 g + r).
         float R[L::MTP][4], dn[L::MTP][4], A[L::MTP][4];
+        f16x8 aph[L::MKP];
         float Cw = kNegInf;
         bool dnbig = false;
         bool rinf = false;   // some latent of this lane has no reference yet (R = -inf)
@@ -205,6 +240,12 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
             for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) A[mi][r] = Cw == kNegInf ? 0.0f : exp2f_fast(R[mi][r] - Cw);
+            // A in fp16 as the MFMA operand of the softmax partials, k-step slots
+            // m = 32 kk + 4 g + e and 32 kk + 16 + 4 g + e - 4 (the latent order of E's rows)
+#pragma unroll
+            for (int kk = 0; kk < L::MKP; ++kk)
+#pragma unroll
+                for (int e2 = 0; e2 < 8; ++e2) aph[kk][e2] = (f16)A[2 * kk + (e2 >> 2)][e2 & 3];
         };
         refresh();
         // The producers meet once per subtile at an LDS counter (consumers never take
@@ -224,7 +265,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 __builtin_amdgcn_s_sleep(1);
             }
         };
-        rows_to_lds<D, 64 * L::NP>(ksl0, K, row0, stride, t_begin, N, tid, lane);
+        KDma<D, 64 * L::NP> kdma;
+        kdma.init(K, row0, stride, t_begin, tid);
+        kdma.issue(ksl0, 0, t_begin, N, stride, tid, lane);
         FLARE_WAIT_VMCNT(0);
         __syncthreads();   // B0: K rows of subtile 0 visible
         auto subtile = [&](auto parity, int j) {
@@ -259,7 +302,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             af[mi][ti] = ok ? load4<f16x4>(arow + 16 * mi) : f16x4{0, 0, 0, 0};
                     }
                 }
-                if (j + 1 < NS) rows_to_lds<D, 64 * L::NP>(knext, K, row0, stride, t0 + T, N, 64 * w + lq, lq);
+                if (j + 1 < NS) kdma.issue(knext, j + 1, t0 + T, N, stride, 64 * w + lq, lq);
                 // ---- raw scores A = Q K^T: acc[mi][ti][r] = A[t = 16 ti + c][m = 16 mi + 4 g + r]
                 const bool ragged = t0 + T > t_end;
                 f32x4 acc[L::MTP][2];
@@ -310,6 +353,13 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                         e[mi][1][r] = exp2f_fast(fmaf(acc[mi][1][r], scale2, -R[mi][r]));
                         emax = fmaxf(emax, fmaxf(e[mi][0][r], e[mi][1][r]));
                     }
+                f16x4 e16[L::MTP][2];     // E in fp16: the MFMA operand of the partials, den and numerator
+#pragma unroll
+                for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                    for (int ti = 0; ti < 2; ++ti)
+                        e16[mi][ti] = __builtin_convertvector((f32x4{e[mi][ti][0], e[mi][ti][1], e[mi][ti][2], e[mi][ti][3]}),
+                                                              f16x4);
                 dnbig |= rinf;   // some latent has no reference yet (fully masked so far): general path
                 const bool moved = __any((emax > L::kLazyE) | dnbig);
                 if (moved) {
@@ -369,14 +419,23 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 if constexpr (!SEP) {
                     float part[2] = {0.0f, 0.0f};
                     if (!moved) {
+                        // sum_m E[t,m] A[m] over this wave's latents as MFMAs (every output row is the
+                        // same sum, column t = 16 ti + c), from the fp16 E that the numerator update
+                        // uses; the E rows then go to LDS at once (common path)
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) {
+                            f32x4 pl = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int kk = 0; kk < L::MKP; ++kk)
+                                pl = mma(aph[kk], cat8<f16x8>(e16[2 * kk][ti], e16[2 * kk + 1][ti]), pl);
+                            part[ti] = pl[0];
+                        }
 #pragma unroll
                         for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                             for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) part[ti] = fmaf(e[mi][ti][r], A[mi][r], part[ti]);
-                        part[0] = rows_sum4_pl(part[0]);
-                        part[1] = rows_sum4_pl(part[1]);
+                                *reinterpret_cast<f16x4*>(erl[buf] + (16 * ti + c) * L::RPE + mp0 + 16 * mi + 4 * g) =
+                                    e16[mi][ti];
                         slow = __any((valid[0] & (part[0] < L::kTinyL)) | (valid[1] & (part[1] < L::kTinyL)));
                     }
                     if (slow) {
@@ -424,13 +483,13 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                     // ---- common path: E rows to LDS (fp16), the cumulative den
                     //      d_t = d0 + sum_{tau<=t} E by MFMA against tri (E^T read transposed),
                     //      W = alpha / d_t (fp16) rows to LDS
+                    if constexpr (SEP) {     // (shared weights: stored with the softmax partials)
 #pragma unroll
-                    for (int mi = 0; mi < L::MTP; ++mi)
+                        for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti)
-                            *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RPE + mp0 + 16 * mi + 4 * g) =
-                                __builtin_convertvector((f32x4{e[mi][ti][0], e[mi][ti][1], e[mi][ti][2], e[mi][ti][3]}),
-                                                        f16x4);
+                            for (int ti = 0; ti < 2; ++ti)
+                                *reinterpret_cast<f16x4*>(er + (16 * ti + c) * L::RPE + mp0 + 16 * mi + 4 * g) = e16[mi][ti];
+                    }
                     f32x4 dcum[L::MTP][2];
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi) {
@@ -455,11 +514,12 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                 __builtin_convertvector(q, f16x4);
                         }
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) {      // den at the subtile end (column t = 31)
-                            dn[mi][r] = row_bcast15(dcum[mi][1][r]);
-                            dnbig |= dn[mi][r] > kDenMax;
-                        }
+                        for (int r = 0; r < 4; ++r) dn[mi][r] = row_bcast15(dcum[mi][1][r]);   // den at t = 31
                     }
+                    float dmx = 0.0f;
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi) dmx = fmaxf(dmx, fmaxf(fmaxf(dn[mi][0], dn[mi][1]), fmaxf(dn[mi][2], dn[mi][3])));
+                    dnbig = dmx > kDenMax;
                 } else {
                     // ---- general path: alpha = 2^(S - ref) f, guarded 1 / d_t, W1 = W d0 when a reference
                     //      moved (the consumers then read out z0 = U / d0), this wave's share of G^T in fp32
