@@ -32,6 +32,7 @@ HEADER_FUNCTIONS = (
     "flare_semi_ar_workspace_size",
     "flare_semi_ar_workspace_size_sep",
     "flare_semi_ar_forward",
+    "flare_semi_ar_forward_state",
     "flare_semi_ar_backward_workspace_size",
     "flare_semi_ar_backward",
     "flare_ar_forward_noalloc_max_bytes",
@@ -98,6 +99,9 @@ def _declare(lib):
     lib.flare_device_faults.argtypes = [_vp, ctypes.POINTER(ctypes.c_uint32), _i]
     lib.flare_set_meet_spin_limit.restype = _i
     lib.flare_set_meet_spin_limit.argtypes = [_i]
+    lib.flare_semi_ar_forward_state.restype = _i
+    lib.flare_semi_ar_forward_state.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp] * 6
+                                                + [_vp, _i, _vp, _sz, _vp])
     lib.flare_semi_ar_forward.restype = _i
     lib.flare_semi_ar_forward.argtypes = ([_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64] + [_vp, _i, _vp, _vp]
                                           + [_vp, _sz, _vp])

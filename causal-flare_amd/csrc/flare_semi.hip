@@ -21,11 +21,17 @@ int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype
 constexpr int kSemiNT = 256;
 constexpr int kSemiCols = 4;
 
-// grid = B*H*M workgroups of one wavefront; in place: num becomes z.
+// grid = B*H*M workgroups of one wavefront; in place: num becomes z.  The scan starts
+// from the cached state (m0, d0, u0) when given (earlier blocks: max, den and numerator
+// relative to the max, inference.py:66-120) and leaves the state after the last block in
+// (m_fin, d_fin, u_fin) when asked.
 __global__ __launch_bounds__(64) void semi_scan_z_kernel(float* __restrict__ bmax,
                                                          float* __restrict__ bden,
                                                          float* __restrict__ bnum, int NB, int M,
-                                                         int Dv, float* __restrict__ lse_enc) {
+                                                         int Dv, float* __restrict__ lse_enc,
+                                                         const float* __restrict__ m0, const float* __restrict__ d0,
+                                                         const float* __restrict__ u0, float* __restrict__ m_fin,
+                                                         float* __restrict__ d_fin, float* __restrict__ u_fin) {
     const int row = blockIdx.x;
     const int bh = row / M, m = row % M;
     const int lane = threadIdx.x;
@@ -33,6 +39,13 @@ __global__ __launch_bounds__(64) void semi_scan_z_kernel(float* __restrict__ bma
     float uc[kSemiCols];
 #pragma unroll
     for (int k = 0; k < kSemiCols; ++k) uc[k] = 0.0f;
+    if (m0 != nullptr) {
+        mc = m0[row];
+        dc = d0[row];
+#pragma unroll
+        for (int k = 0; k < kSemiCols; ++k)
+            if (lane + 64 * k < Dv) uc[k] = u0[(size_t)row * Dv + lane + 64 * k];
+    }
     for (int g = 0; g < NB; ++g) {
         const size_t si = ((size_t)bh * NB + g) * M + m;
         const float bm = bmax[si], bd = bden[si];
@@ -51,6 +64,15 @@ __global__ __launch_bounds__(64) void semi_scan_z_kernel(float* __restrict__ bma
                 bnum[si * Dv + col] = uc[k] * w;
             }
         }
+    }
+    if (m_fin != nullptr) {
+        if (lane == 0) {
+            m_fin[row] = mc;
+            d_fin[row] = dc;
+        }
+#pragma unroll
+        for (int k = 0; k < kSemiCols; ++k)
+            if (lane + 64 * k < Dv) u_fin[(size_t)row * Dv + lane + 64 * k] = uc[k];
     }
 }
 
@@ -153,11 +175,15 @@ size_t flare_semi_ar_workspace_size_sep(int64_t B, int64_t N, int64_t H, int64_t
     return semi_summary_bytes(B, N, H, M, Dv, block) + semi_alpha_bytes(B, N, H, M);
 }
 
-int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
-                          const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H,
-                          int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,
-                          void* Y, int out_dtype, float* lse_dec, float* lse_enc,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The block-causal forward with an optional cached state in (m0, d0, u0: the blocks
+// before this call) and out (m_fin, d_fin, u_fin: after its last block).
+static int semi_forward_impl(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec,
+                             int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
+                             float scale, int64_t block, const float* m0, const float* d0, const float* u0,
+                             float* m_fin, float* d_fin, float* u_fin, void* Y, int out_dtype, float* lse_dec,
+                             float* lse_enc, void* workspace, size_t workspace_bytes, void* stream) {
     FLARE_REQUIRE(Q && K && V && Y, "semi_ar_forward: null pointer");
     FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0, "semi_ar_forward: sizes must be positive");
     FLARE_REQUIRE(block > 0 && block % 16 == 0 && N % block == 0,
@@ -204,8 +230,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
         const int64_t NC = (N + chunk - 1) / chunk;
         int rc = launch_prepare_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, bmax, bden, bnum, dtype == FLARE_F16, s);
         if (rc) return rc;
-        rc = launch_prefix_public(bmax, bden, bnum, B * H, NC, M, Dv, nullptr, nullptr, nullptr, nullptr,
-                                  nullptr, nullptr, s);
+        rc = launch_prefix_public(bmax, bden, bnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
         if (rc) return rc;
         return launch_semi_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, block, bmax, bden, bnum, Y,
                                        out_dtype, lse_dec, lse_enc, alpha_ws, !shared, dtype == FLARE_F16, s);
@@ -213,7 +238,7 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
     int rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, block, bmax, bden, bnum, s);
     if (rc) return rc;
     hipLaunchKernelGGL(semi_scan_z_kernel, dim3((unsigned)(B * H * M)), dim3(64), 0, s, bmax, bden,
-                       bnum, (int)NB, (int)M, (int)Dv, lse_enc);
+                       bnum, (int)NB, (int)M, (int)Dv, lse_enc, m0, d0, u0, m_fin, d_fin, u_fin);
     rc = check_launch("semi_scan_z_kernel");
     if (rc) return rc;
     // Value tile so that z_block[g][:, tile] fits in 32 KB of LDS.
@@ -236,6 +261,31 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
     else FLARE_SEMI(float);
 #undef FLARE_SEMI
     return check_launch("semi_output_kernel");
+}
+
+extern "C" {
+
+int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const void* Qdec,
+                          const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H,
+                          int64_t M, int64_t Dk, int64_t Dv, float scale, int64_t block,
+                          void* Y, int out_dtype, float* lse_dec, float* lse_enc,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    return semi_forward_impl(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, block, nullptr, nullptr,
+                             nullptr, nullptr, nullptr, nullptr, Y, out_dtype, lse_dec, lse_enc, workspace,
+                             workspace_bytes, stream);
+}
+
+int flare_semi_ar_forward_state(const void* Q, const void* K, const void* V, const void* Qdec,
+                                const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                                int64_t Dk, int64_t Dv, float scale, int64_t block, const float* m0,
+                                const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                                void* Y, int out_dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    FLARE_REQUIRE((m0 == nullptr) == (d0 == nullptr) && (m0 == nullptr) == (u0 == nullptr),
+                  "semi_ar_forward_state: give all of m0, d0, u0 or none");
+    FLARE_REQUIRE((m_fin == nullptr) == (d_fin == nullptr) && (m_fin == nullptr) == (u_fin == nullptr),
+                  "semi_ar_forward_state: give all of m_fin, d_fin, u_fin or none");
+    return semi_forward_impl(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, block, m0, d0, u0, m_fin,
+                             d_fin, u_fin, Y, out_dtype, nullptr, nullptr, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -201,6 +201,25 @@ int flare_semi_ar_forward(const void* Q, const void* K, const void* V, const voi
                           void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Semi-autoregressive cached prefill / block decode: flare_semi_ar_forward over N
+ * tokens that continue a cached latent state.  m0 / d0 [B, H, M] and u0 [B, H, M, Dv]
+ * (fp32; all NULL for an empty cache) hold the earlier blocks as running max, den
+ * and numerator relative to the max -- the layout of the autoregressive cache
+ * (causal_flare/autoregressive/inference.py:66-120).  Every token of a block reads
+ * the state after its whole block.  m_fin / d_fin / u_fin (all NULL, or all given;
+ * they must not overlap m0 / d0 / u0) receive the state after the last block.  Same
+ * requirements and workspace as flare_semi_ar_forward; no LSE outputs.  The
+ * reference ships these entry points as stubs that raise NotImplementedError
+ * (causal_flare/semi_autoregressive/inference.py:5-36,
+ * flare_semi_autoregressive_prefill_trition / flare_semi_autoregressive_decode_trition).
+ */
+int flare_semi_ar_forward_state(const void* Q, const void* K, const void* V, const void* Qdec,
+                                const void* Kdec, int dtype, int64_t B, int64_t N, int64_t H, int64_t M,
+                                int64_t Dk, int64_t Dv, float scale, int64_t block, const float* m0,
+                                const float* d0, const float* u0, float* m_fin, float* d_fin, float* u_fin,
+                                void* Y, int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * flare_ar_forward_masked without a workspace argument: its chunk summaries, redo
  * flags and (separate decoder tensors) decoder softmax live in a fixed device
  * array of the library, one copy per GPU, held until the process ends.  No

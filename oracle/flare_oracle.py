@@ -18,6 +18,9 @@ Two layers:
     - ``brute_semi_ar``: the per-block two-SDPA oracle, ``semi_autoregressive/reference.py:560-597``
     - ``brute_ar_state``: the same definition continued from a cached state
       ``{m, d, u}`` (``inference.py:66-120``), with an optional token mask.
+    - ``brute_semi_ar_state``: the block-causal definition continued from a
+      cached state (the semi-AR cached prefill / block decode, which the
+      reference leaves as stubs).
   They are the pins for the C restatement (see tests/test_oracle.py).
 * ``ar_grads``: fp64 torch autograd of ``ar_forward_torch64`` (the same
   definition with cumulative sums), the ground truth of the backward; pinned
@@ -289,6 +292,51 @@ def brute_semi_ar(Q, K, V, block_size, scale=None, Q_dec=None, K_dec=None):
         alpha = _softmax(A[:, :, t0:t1, :], axis=-1)
         Y[:, :, t0:t1] = np.einsum("bhtm,bhmd->bhtd", alpha, Z)
     return Y.transpose(0, 2, 1, 3)
+
+
+def brute_semi_ar_state(Q, K, V, block_size, state=None, scale=None, Q_dec=None, K_dec=None):
+    """Block-causal FLARE continuing a cached state {m, d, u}, fp64 (semi-AR cached prefill).
+
+    The reference ships no implementation (its semi_autoregressive/inference.py:5-36 are
+    stubs); this is the block-level analogue of ``brute_ar_state``: the cached state
+    stands for earlier blocks with weights exp(m) d and exp(m) u (inference.py:66-120),
+    and every token of block g reads the latent state after the whole block, as in
+    ``brute_semi_ar`` (semi_autoregressive/reference.py:560-597).  Returns (Y, state)
+    with m the running max of all seen scores.  Pinned in tests/test_oracle.py by
+    ``brute_semi_ar`` (no state), by continuation (prefill(a + b) == prefill(b) after
+    prefill(a), split at a block end) and by ``brute_ar_state`` (the final state does
+    not depend on the blocking).
+    """
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    S = scale * np.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * np.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    Vt = V.transpose(0, 2, 1, 3)
+    if state is None:
+        mc = np.full((B, H, M), -np.inf)
+        dc = np.zeros((B, H, M))
+        uc = np.zeros((B, H, M, Dv))
+    else:
+        mc, dc, uc = (_f64(state[k]).copy() for k in ("m", "d", "u"))
+    Y = np.zeros((B, H, N, Dv))
+    for g in range(math.ceil(N / block_size)):
+        t0, t1 = g * block_size, min(N, (g + 1) * block_size)
+        s = S[:, :, t0:t1, :]                                     # [B, H, n, M]
+        mn = np.maximum(mc, s.max(axis=2))
+        mn_safe = np.where(np.isneginf(mn), 0.0, mn)
+        w_state = np.where(np.isneginf(mc), 0.0, np.exp(mc - mn_safe))
+        w_tok = np.exp(s - mn_safe[:, :, None, :])
+        dc = dc * w_state + w_tok.sum(axis=2)
+        uc = uc * w_state[..., None] + np.einsum("bhtm,bhtd->bhmd", w_tok, Vt[:, :, t0:t1])
+        mc = mn
+        z = uc / np.where(dc > 0, dc, 1.0)[..., None]
+        alpha = _softmax(A[:, :, t0:t1, :], axis=-1)
+        Y[:, :, t0:t1] = np.einsum("bhtm,bhmd->bhtd", alpha, z)
+    return Y.transpose(0, 2, 1, 3), {"m": mc, "d": dc, "u": uc}
 
 
 def allclose_rel(a, b, dtype_name: str):

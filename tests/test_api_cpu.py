@@ -87,12 +87,20 @@ def test_semi_ar_rejects_non_block_aligned_length_and_missing_args():
         causal_flare.flare_semi_autoregressive_trition(q, k[:, :32], v[:, :32], block_size=16, chunk_size=16)
 
 
-def test_semi_ar_stubs_raise():
-    q, k, v = torch.randn(2, 4, 16), torch.randn(1, 8, 2, 16), torch.randn(1, 8, 2, 16)
-    with pytest.raises(NotImplementedError):
-        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v)
-    with pytest.raises(NotImplementedError):
-        causal_flare.flare_semi_autoregressive_decode_trition(q, k, v)
+def test_semi_ar_cached_validation():
+    """The semi-AR cached prefill / block decode (stubs in the reference,
+    semi_autoregressive/inference.py:5-36) validate blocks before they need a GPU."""
+    q, k, v = torch.randn(2, 4, 16), torch.randn(1, 48, 2, 16), torch.randn(1, 48, 2, 16)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v, block_size=24)
+    with pytest.raises(ValueError, match="exact multiple of block_size"):
+        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v, block_size=32)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        causal_flare.flare_semi_autoregressive_decode_trition(q, k[:, :24], v[:, :24])
+    with pytest.raises(RuntimeError, match="requires CUDA tensors"):
+        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v, block_size=16)
+    with pytest.raises(NotImplementedError, match="attention_mask"):
+        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v, attention_mask=torch.zeros(1, 48))
 
 
 def test_recurrent_validation_messages():

@@ -174,6 +174,43 @@ def test_semi_ar_block_ends_equal_ar():
     assert np.abs(ys[:, 0] - ya[:, 0]).max() > 1e-3   # and not elsewhere
 
 
+@pytest.mark.parametrize("block", [1, 4, 16])
+def test_semi_state_oracle_without_state_is_block_causal(block):
+    """No cached state: the block-causal definition (semi_autoregressive/reference.py:560-597)."""
+    B, N, H, M, D = 2, 32, 2, 6, 8
+    q, k, v = seeded(30, B, N, H, M, D, D, torch.float32)
+    y, _ = O.brute_semi_ar_state(q, k, v, block)
+    _close(y, O.brute_semi_ar(q, k, v, block), 1e-12)
+
+
+def test_semi_state_oracle_continuation_and_final_state():
+    """prefill(a + b) == prefill(a) then prefill(b) from its state (split at a block end);
+    the state after the tokens is the autoregressive one (independent of the blocking);
+    one-token blocks reduce to the autoregressive prefill from the same state."""
+    B, N, H, M, D, blk = 2, 48, 2, 5, 8, 8
+    q, k, v = seeded(31, B, N, H, M, D, D, torch.float32)
+    # a random cached state, as a previous prefill leaves it
+    q0, k0, v0 = seeded(32, B, 11, H, M, D, D, torch.float32)
+    _, st0 = O.brute_ar_state(q0, k0, v0, scale=0.3)
+    y_all, st_all = O.brute_semi_ar_state(q, k, v, blk, state=st0, scale=0.3)
+    cut = 3 * blk
+    y_a, st_a = O.brute_semi_ar_state(q, k[:, :cut], v[:, :cut], blk, state=st0, scale=0.3)
+    y_b, st_b = O.brute_semi_ar_state(q, k[:, cut:], v[:, cut:], blk, state=st_a, scale=0.3)
+    _close(np.concatenate([y_a, y_b], axis=1), y_all, 1e-12)
+    for key in ("m", "d", "u"):
+        _close(st_b[key], st_all[key], 1e-12)
+    y_ar, st_ar = O.brute_ar_state(q, k, v, state=st0, scale=0.3)
+    for key in ("m", "d", "u"):
+        _close(st_all[key], st_ar[key], 1e-10)
+    y1, _ = O.brute_semi_ar_state(q, k, v, 1, state=st0, scale=0.3)
+    _close(y1, y_ar, 1e-10)
+    # closed form: constant values give y = that constant in every block
+    vc = torch.full_like(v, 0.75)
+    _, stc = O.brute_ar_state(q0, k0, torch.full_like(v0, 0.75), scale=0.3)
+    yc, _ = O.brute_semi_ar_state(q, k, vc, blk, state=stc, scale=0.3)
+    _close(yc, np.full(yc.shape, 0.75), 1e-12)
+
+
 def test_golden_fixtures():
     files = sorted(f for f in os.listdir(GOLDEN) if f.endswith(".npz"))
     assert files, "no golden fixtures"
