@@ -214,7 +214,6 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         // reference starts at the prefix's log-sum-exp: den = 1, U = z.  R is the same on the
         // 16 lanes of a row (latent m = mp0 + 16 mi + 4 g + r).
         float R[L::MTP][4], dn[L::MTP][4], A[L::MTP][4];
-        f16x8 aph[L::MKP];
         float Cw = kNegInf;
         bool dnbig = false;
         bool rinf = false;   // some latent of this lane has no reference yet (R = -inf)
@@ -240,12 +239,6 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
             for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) A[mi][r] = Cw == kNegInf ? 0.0f : exp2f_fast(R[mi][r] - Cw);
-            // A in fp16 as the MFMA operand of the softmax partials, k-step slots
-            // m = 32 kk + 4 g + e and 32 kk + 16 + 4 g + e - 4 (the latent order of E's rows)
-#pragma unroll
-            for (int kk = 0; kk < L::MKP; ++kk)
-#pragma unroll
-                for (int e2 = 0; e2 < 8; ++e2) aph[kk][e2] = (f16)A[2 * kk + (e2 >> 2)][e2 & 3];
         };
         refresh();
         // The producers meet once per subtile at an LDS counter (consumers never take
@@ -345,24 +338,69 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 // ---- E = 2^(S - R) against the current references
                 float e[L::MTP][2][4];
                 float emax = 0.0f;
-#pragma unroll
-                for (int mi = 0; mi < L::MTP; ++mi)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        e[mi][0][r] = exp2f_fast(fmaf(acc[mi][0][r], scale2, -R[mi][r]));
-                        e[mi][1][r] = exp2f_fast(fmaf(acc[mi][1][r], scale2, -R[mi][r]));
-                        emax = fmaxf(emax, fmaxf(e[mi][0][r], e[mi][1][r]));
-                    }
                 f16x4 e16[L::MTP][2];     // E in fp16: the MFMA operand of the partials, den and numerator
+                auto exps = [&]() __attribute__((always_inline)) {
+                    emax = 0.0f;
 #pragma unroll
-                for (int mi = 0; mi < L::MTP; ++mi)
+                    for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
-                    for (int ti = 0; ti < 2; ++ti)
-                        e16[mi][ti] = __builtin_convertvector((f32x4{e[mi][ti][0], e[mi][ti][1], e[mi][ti][2], e[mi][ti][3]}),
-                                                              f16x4);
+                        for (int r = 0; r < 4; ++r) {
+                            e[mi][0][r] = exp2f_fast(fmaf(acc[mi][0][r], scale2, -R[mi][r]));
+                            e[mi][1][r] = exp2f_fast(fmaf(acc[mi][1][r], scale2, -R[mi][r]));
+                            emax = fmaxf(emax, fmaxf(e[mi][0][r], e[mi][1][r]));
+                        }
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti)
+                            e16[mi][ti] = __builtin_convertvector(
+                                (f32x4{e[mi][ti][0], e[mi][ti][1], e[mi][ti][2], e[mi][ti][3]}), f16x4);
+                };
+                if (__any(rinf)) {
+                    // Some latent has no reference yet.  When no latent of the wave has one
+                    // (nothing accumulated: a chunk with no earlier tokens) the references
+                    // start at the subtile's log-sum-exp without a move, so there is nothing
+                    // to rescale and the subtile takes the common path -- provided every
+                    // E is at least 2^-12 (a token's den is then a sum of fp16 values with
+                    // their full 11 bits) and every token of the subtile is valid (a masked
+                    // token before the first valid one would have den 0).
+                    bool seen = false;
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) seen |= R[mi][r] != kNegInf;
+                    if (!__any(seen)) {
+                        bool tiny = false;
+#pragma unroll
+                        for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                float x = row_max16(fmaxf(acc[mi][0][r], acc[mi][1][r])) * scale2;
+                                tiny |= x == kNegInf;
+                                if (x != kNegInf)
+                                    x += __log2f(row_sum16(exp2f_fast(fmaf(acc[mi][0][r], scale2, -x)) +
+                                                           exp2f_fast(fmaf(acc[mi][1][r], scale2, -x))));
+#pragma unroll
+                                for (int ti = 0; ti < 2; ++ti)
+                                    tiny |= !valid[ti] | (fmaf(acc[mi][ti][r], scale2, -x) < -12.0f);
+                                R[mi][r] = x;
+                            }
+                        if (__any(tiny)) {
+#pragma unroll
+                            for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) R[mi][r] = kNegInf;
+                        } else {
+                            refresh();
+                            rinf = false;
+                        }
+                    }
+                }
+                exps();
                 dnbig |= rinf;   // some latent has no reference yet (fully masked so far): general path
-                const bool moved = __any((emax > L::kLazyE) | dnbig);
+                bool moved = __any((emax > L::kLazyE) | dnbig);
                 if (moved) {
+                    // every latent of the wave had den 0 so far (a chunk with no earlier tokens)
                     float gam[L::MTP][4];
                     bool jump = false;
 #pragma unroll
@@ -379,13 +417,21 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             const float s0 = acc[mi][0][r] * scale2, s1 = acc[mi][1][r] * scale2;
                             const float mn = -row_max16(fmaxf(s0 == kNegInf ? kNegInf : -s0, s1 == kNegInf ? kNegInf : -s1));
                             const float base = R[mi][r] == kNegInf ? mn : R[mi][r];
-                            jump |= Rn - base > kJumpMax;
                             float g1 = exp2f_fast(R[mi][r] - Rn);                  // 0 when R = -inf
-                            const float dd = dn[mi][r] * g1;
-                            if (dd > kDenMax) {
+                            // den at the subtile's end against Rn: the old den plus this
+                            // subtile's E.  Above 1 the reference rises to its log-sum-exp, so
+                            // the den restarts at 1 and one move covers the subtile's own growth
+                            // (a first subtile of flat scores would otherwise move again next).
+                            float ss = 0.0f;
+                            if (Rn != kNegInf)
+                                ss = row_sum16(exp2f_fast(fmaf(acc[mi][0][r], scale2, -Rn)) +
+                                               exp2f_fast(fmaf(acc[mi][1][r], scale2, -Rn)));
+                            const float dd = dn[mi][r] * g1 + ss;
+                            if (dd > 1.0f) {
                                 Rn += __log2f(dd);
                                 g1 = exp2f_fast(R[mi][r] - Rn);
                             }
+                            jump |= Rn - base > kJumpMax;
                             gam[mi][r] = Rn == R[mi][r] ? 1.0f : g1;
                             R[mi][r] = Rn;
                             dn[mi][r] *= gam[mi][r];     // E is recomputed on the general path
@@ -419,17 +465,20 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 if constexpr (!SEP) {
                     float part[2] = {0.0f, 0.0f};
                     if (!moved) {
-                        // sum_m E[t,m] A[m] over this wave's latents as MFMAs (every output row is the
-                        // same sum, column t = 16 ti + c), from the fp16 E that the numerator update
-                        // uses; the E rows then go to LDS at once (common path)
+                        // sum_m E[t,m] A[m] over this wave's latents in fp32 (16 latents per lane,
+                        // then the four lane rows): A spans the spread of the references, which
+                        // can run past the fp16 range; the E rows then go to LDS at once
+                        // (common path)
+                        float pt[2] = {0.0f, 0.0f};
 #pragma unroll
-                        for (int ti = 0; ti < 2; ++ti) {
-                            f32x4 pl = f32x4{0.f, 0.f, 0.f, 0.f};
+                        for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll
-                            for (int kk = 0; kk < L::MKP; ++kk)
-                                pl = mma(aph[kk], cat8<f16x8>(e16[2 * kk][ti], e16[2 * kk + 1][ti]), pl);
-                            part[ti] = pl[0];
-                        }
+                            for (int r = 0; r < 4; ++r) {
+                                pt[0] = fmaf(e[mi][0][r], A[mi][r], pt[0]);
+                                pt[1] = fmaf(e[mi][1][r], A[mi][r], pt[1]);
+                            }
+                        part[0] = rows_sum4_pl(pt[0]);
+                        part[1] = rows_sum4_pl(pt[1]);
 #pragma unroll
                         for (int mi = 0; mi < L::MTP; ++mi)
 #pragma unroll

@@ -160,6 +160,33 @@ def test_score_jump_within_subtile(M, D, dtype):
     assert_noise_model(y, ref, f"repeated outlier M={M} D={D}")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("nats", [4.0, 7.5, 8.8, 12.0])
+@pytest.mark.parametrize("tok", [9, 100])
+def test_key_outlier_spreads_references(M, D, nats, tok):
+    """A key at token `tok` sits `nats` above the others on 8 latents (and far off on
+    many more), so the latents' references then span up to ~45 powers of two within
+    one producer wave: the per-token softmax partials must keep every latent (they
+    are summed in fp32), and at token 9 the first subtile of a sequence with no state
+    starts its references at that subtile's log-sum-exp only when every E is at least
+    2^-12.  Against the tokenwise recurrence (training.py:1282-1393) for the AR path
+    and the block-causal forward (semi reference.py:308-536) for the semi-AR path."""
+    from causal_flare import flare_autoregressive_triton, flare_semi_autoregressive_trition
+    _print_case("key_outlier", M, D, nats, tok)
+    B, N, H = 2, 300, 2
+    q, k, v = seeded(505 + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    scale = D ** -0.5
+    kj = _jump_keys(q, k, [tok], lat=list(range(0, M, M // 8)), nats=[nats], scale=scale)
+    ref = O.ar_chunked(q, kj, v, scale=scale, nthreads=16)
+    for chunk in (None, 64):
+        y = flare_autoregressive_triton(q.to(DEV), kj.to(DEV), v.to(DEV), chunk_size=chunk)
+        assert_parity(y, ref, torch.bfloat16, f"key outlier M={M} D={D} nats={nats} tok={tok} chunk={chunk}")
+    ys, _ = flare_semi_autoregressive_trition(q.to(DEV), kj[:, :288].to(DEV), v[:, :288].to(DEV), block_size=96,
+                                              chunk_size=32)
+    refs, _, _ = O.semi_ar(q, kj[:, :288], v[:, :288], 96, 32)
+    assert_parity(ys, refs, torch.bfloat16, f"semi key outlier M={M} D={D} nats={nats} tok={tok}")
+
+
 def test_meeting_timeout_falls_back_to_tokenwise_replay():
     """The producer meeting of the output kernel is a bounded wait.  With the bound
     forced to zero from the host, waits give up: the kernel counts the faults and
