@@ -1145,6 +1145,8 @@ using namespace mfma;
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, bool f16in, hipStream_t stream) {
+    if (prepare_tr_enabled())
+        return launch_prepare_tr(Q, K, V, B, N, H, M, D, scale, chunk, cmax, cden, cnum, tmask, f16in, stream);
     FLARE_REQUIRE(chunk % T == 0, "chunk_prepare_pc: chunk must be a multiple of %d", T);
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_prepare_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);

@@ -1,0 +1,417 @@
+// flare_ar_prep.hip -- phase 1 of the chunked causal FLARE forward on gfx950:
+// the chunk summaries (max, den, num) of the reference's flare_chunk_prepare
+// (training.py:914-1018) for bf16 or fp16 inputs, M in {128, 256}, D in {64, 128}.
+//
+// One workgroup per (chunk, b, h) with M/32 waves; wave w owns latents
+// 32 w .. 32 w + 31 over every value column, so the waves never exchange data:
+// per 64-token tile each wave forms S^T = K Q^T (tokens as rows), moves its lazy
+// references when a score passes them by more than kLazy, takes
+// E = 2^(S - R) straight from the score registers as the B operand of
+// U^T += V^T E (the C layout of a 16x16 score tile is the B layout of the
+// 32-deep contraction, with token slots tau(g, e) = 4 g + e and 16 + 4 g + e - 4),
+// and reads V^T with transposed LDS reads.  K and V tiles reach LDS by DMA
+// (global_load_lds into XOR-swizzled rows), three tiles in flight, one barrier
+// per tile.
+//
+// Precision: S in fp32 from the bf16 / fp16 inputs; E (<= 2^kLazy) enters
+// U^T += V^T E as fp16 against fp16 V -- the fp16 inputs, or bf16 V converted
+// to fp16 in LDS one tile ahead (exact within the fp16 range).  A bf16 tile
+// holding a value outside that range takes E as a bf16 hi + lo pair against
+// bf16 V instead.  (A single bf16 rounding of E, as the reference's
+// p.to(v.dtype) in training.py:985-990, leaves state errors near 2e-2 where
+// sum E v cancels.)  den and the maxima in fp32.  The summary is returned
+// relative to the true chunk max: (max, den 2^(R - max), U 2^(R - max)) in
+// natural-log units, as chunk_prepare_pc writes it.
+#include <type_traits>
+
+#include "flare_common.h"
+#include "flare_internal.h"
+#include "flare_mfma.h"
+
+namespace flare {
+namespace mfma {
+
+typedef short s16x4p __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4p lds_s16x4p;
+
+namespace {
+
+constexpr int TT = 64;   // tokens per tile
+
+// Transposed 8-byte LDS read: with lane j of a 16-lane group pointing at row
+// base + j / 4, columns c0 + 4 (j % 4) .. + 3, lane i receives column c0 + i of
+// rows base .. base + 3.
+template <bool F16>
+__device__ __forceinline__ bf16x4 tr4(const bf16* p) {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4p*)p));
+}
+
+// global_load_lds of 16 bytes per lane (lane l's bytes land at LDS byte offset 16 l
+// from wave_dst) written as inline assembly: the compiler then does not track the
+// LDS write, and inserts no wait for it before LDS reads of the other tiles (it
+// cannot tell the three tile buffers apart there); the kernel orders the DMA with
+// explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const bf16* src, bf16* wave_dst) {
+    const unsigned lds = __builtin_amdgcn_readfirstlane(
+        (unsigned)(uintptr_t)((__attribute__((address_space(3))) bf16*)wave_dst));
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// The TT-row tiles of a [.., stride] 16-bit tensor (one (b,h)), one after another,
+// into XOR-swizzled LDS rows by DMA (no registers): piece e = tid + k NTHR of a
+// tile is row e / KC, LDS slot e % KC, and holds logical 16-byte column chunk
+// swz(row, slot).  Each thread keeps the global addresses of its pieces and
+// advances them by TT rows per tile.  Rows at or past `rows_end` repeat row
+// rows_end - 1 (their scores are masked).
+template <int D, int NTHR>
+struct TileDma {
+    static constexpr int KC = D / 8;
+    static constexpr int NK = TT * KC / NTHR;
+    static_assert(TT * KC % NTHR == 0, "the workgroup's threads must divide the pieces of a tile");
+    const bf16* p[NK];
+    __device__ __forceinline__ void init(const bf16* base, int t_first, size_t stride, int tid) {
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            const int e = tid + k * NTHR;
+            p[k] = base + (size_t)(t_first + e / KC) * stride + 8 * swz<D>(e / KC, e % KC);
+        }
+    }
+    // the next tile (rows t0 ..) into dst; wofs = 8 x (the wave's first thread index)
+    __device__ __forceinline__ void issue(bf16* dst, int wofs, int t0, int rows_end, size_t stride, int tid) {
+        if (t0 + TT <= rows_end) {
+#pragma unroll
+            for (int k = 0; k < NK; ++k) dma16(p[k], dst + wofs + k * NTHR * 8);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NK; ++k) {
+                const int t = t0 + (tid + k * NTHR) / KC, tc = min(t, rows_end - 1);
+                dma16(p[k] - (size_t)(t - tc) * stride, dst + wofs + k * NTHR * 8);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NK; ++k) p[k] += (size_t)TT * stride;
+    }
+};
+
+}  // namespace
+
+template <int M, int D, bool F16, bool MASK>
+__global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K,
+                                                          const bf16* __restrict__ V, int N, int H, float scale2,
+                                                          int chunk, float* __restrict__ cmax,
+                                                          float* __restrict__ cden, float* __restrict__ cnum,
+                                                          const int32_t* __restrict__ tmask) {
+    constexpr int NT = 2 * M;           // M / 32 waves
+    constexpr int KS = D / 32;          // k-steps of the scores
+    constexpr int DT = D / 16;          // value-column tiles
+    constexpr int TI = TT / 16;         // token tiles of a tile
+    constexpr int KK = TT / 32;         // k-steps of U^T += V^T E
+    constexpr int NCV = TT * D / 8 / NT;
+    using Dma = TileDma<D, NT>;
+    // K tiles j mod 3 and V tiles j mod 4 (DMA two tiles ahead; V of tile j is read
+    // until iteration j + 1); bf16 inputs: V tiles j mod 2 converted to fp16
+    __shared__ __attribute__((aligned(16))) bf16 ktl[3][TT * D];
+    __shared__ __attribute__((aligned(16))) bf16 vtl[4][TT * D];
+    __shared__ __attribute__((aligned(16))) f16 vhl[F16 ? 1 : 2][F16 ? 8 : TT * D];
+    __shared__ int redo_bf16;
+
+    const int c_idx = blockIdx.x, bh = blockIdx.y;
+    const int NC = gridDim.x;
+    const int b = bh / H, h = bh % H;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int m0 = 32 * w;
+    const int t_begin = c_idx * chunk;
+    const int t_end = min(N, t_begin + chunk);
+    const int NS = (t_end - t_begin + TT - 1) / TT;
+    const size_t stride = (size_t)H * D;
+    const bf16* Kb = K + (size_t)b * N * stride + (size_t)h * D;
+    const bf16* Vb = V + (size_t)b * N * stride + (size_t)h * D;
+
+    // this wave's Q rows as MFMA B operands (n = m, k = d)
+    bf16x8 qb[2][KS];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kq = 0; kq < KS; ++kq)
+            qb[mt][kq] = load8<bf16x8>(Q + ((size_t)h * M + m0 + 16 * mt + c) * D + 32 * kq + 8 * g);
+    // Q has arrived before the loop (the empty asm uses it), so that the compiler keeps
+    // no wait for these loads inside the loop, where it would also wait for the DMA
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int kq = 0; kq < KS; ++kq) asm volatile("" : "+v"(qb[mt][kq]));
+    const int wofs = 8 * __builtin_amdgcn_readfirstlane(tid - lane);
+    // per-lane LDS offsets (elements) of the swizzled operand reads: K rows 16 ti + c at
+    // chunk 4 kq + g (row & (KC - 1) = c & (KC - 1)), and the transposed V reads of rows
+    // 32 kk + 4 g + c / 4 (+ 16) at columns 16 di + 4 (c & 3) (row & (KC - 1) does not
+    // depend on kk); the tile-dependent parts are compile-time offsets
+    constexpr int KC = D / 8;
+    int kofs[KS], vofs[DT];
+#pragma unroll
+    for (int kq = 0; kq < KS; ++kq) kofs[kq] = c * D + 8 * ((4 * kq + g) ^ (c & (KC - 1)));
+#pragma unroll
+    for (int di = 0; di < DT; ++di) {
+        const int rl = 4 * g + (c >> 2);
+        vofs[di] = rl * D + 8 * ((2 * di + ((c & 3) >> 1)) ^ (rl & (KC - 1))) + 4 * (c & 1);
+    }
+    // U^T[d = 16 di + 4 g + r][m = m0 + 16 mt + c]
+    f32x4 U[DT][2];
+    // per latent m0 + 16 mt + c (replicated over g): reference R, this lane's max rt and den dl
+    float R[2], rt[2], dl[2];
+
+    // One pass over the chunk.  BF = false: fp16 E (<= 2^kLazy) against fp16 V (the fp16
+    // inputs, or bf16 V converted in LDS); BF = true (bf16 inputs only, a rerun when the
+    // first pass met a value outside the fp16 range): E as an exact bf16 hi + lo pair
+    // against the bf16 V.
+    auto pass = [&](auto bf_tag) __attribute__((always_inline)) {
+        constexpr bool BF = decltype(bf_tag)::value;
+        Dma kdma, vdma;
+        kdma.init(Kb, t_begin, stride, tid);
+        vdma.init(Vb, t_begin, stride, tid);
+        kdma.issue(ktl[0], wofs, t_begin, t_end, stride, tid);
+        vdma.issue(vtl[0], wofs, t_begin, t_end, stride, tid);
+        kdma.issue(ktl[1], wofs, t_begin + TT, t_end, stride, tid);
+        vdma.issue(vtl[1], wofs, t_begin + TT, t_end, stride, tid);
+#pragma unroll
+        for (int di = 0; di < DT; ++di) U[di][0] = U[di][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+            R[mt] = kNegInf;
+            rt[mt] = kNegInf;
+            dl[mt] = 0.0f;
+        }
+        // E of the previous tile in fp16, k-slot order tau(g, e): the B operand of U^T += V^T E
+        f16x8 eh[KK][2];
+        FLARE_WAIT_VMCNT((2 * Dma::NK));   // tile 0 has landed
+        lds_barrier();
+        auto value_product = [&](int jp) __attribute__((always_inline)) {
+            auto vread = [&](const bf16* base, int kk, int di) __attribute__((always_inline)) {
+                const bf16* p = base + vofs[di] + 32 * kk * D;
+                return cat8<bf16x8>(tr4<F16>(p), tr4<F16>(p + 16 * D));
+            };
+            if constexpr (!BF) {
+                const bf16* vf = F16 ? vtl[jp & 3] : reinterpret_cast<const bf16*>(vhl[jp & 1]);
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+                    for (int di = 0; di < DT; ++di) {
+                        const f16x8 va = __builtin_bit_cast(f16x8, vread(vf, kk, di));
+#pragma unroll
+                        for (int mt = 0; mt < 2; ++mt) U[di][mt] = mma(va, eh[kk][mt], U[di][mt]);
+                    }
+            } else {
+                bf16x8 hi[KK][2], lo[KK][2];
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) SPLIT2(bf16, (float)eh[kk][mt][i], hi[kk][mt][i], lo[kk][mt][i]);
+#pragma unroll
+                for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+                    for (int di = 0; di < DT; ++di) {
+                        const bf16x8 va = vread(vtl[jp & 3], kk, di);
+#pragma unroll
+                        for (int mt = 0; mt < 2; ++mt) {
+                            U[di][mt] = mma(va, hi[kk][mt], U[di][mt]);
+                            U[di][mt] = mma(va, lo[kk][mt], U[di][mt]);
+                        }
+                    }
+            }
+        };
+
+        for (int j = 0; j < NS; ++j) {
+            const int t0 = t_begin + TT * j;
+            // masked tokens of this lane (t = t0 + 16 ti + 4 g + r, bit 4 ti + r)
+            unsigned drop = 0;
+            if constexpr (MASK) {
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = t0 + 16 * ti + 4 * g + r;
+                        if (t < t_end && tmask[(size_t)b * N + t] == 0) drop |= 1u << (4 * ti + r);
+                    }
+            }
+            // tile j + 2 (past the chunk's last tile: copies of its last row, never read), so
+            // that every iteration issues the same number of DMA requests
+            kdma.issue(ktl[(j + 2) % 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+            vdma.issue(vtl[(j + 2) & 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+            // bf16 inputs, first pass: V of tile j (landed at the last barrier) to fp16 for
+            // iteration j + 1 (a value outside the fp16 range becomes inf and shows in U)
+            if constexpr (!F16 && !BF) {
+                const bf16* src = vtl[j & 3];
+                f16* dst = vhl[j & 1];
+#pragma unroll
+                for (int k = 0; k < NCV; ++k) {
+                    const int idx = tid + k * NT;
+                    const bf16x8 x = load8<bf16x8>(src + 8 * idx);
+                    f16x8 y;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) y[i] = (f16)(float)x[i];
+                    *reinterpret_cast<f16x8*>(dst + 8 * idx) = y;
+                }
+            }
+            // the previous tile's value product, before this tile may rescale U
+            if (j > 0) value_product(j - 1);
+            // ---- S^T = K Q^T: acc[ti][mt][r] = S[t = 16 ti + 4 g + r][m = 16 mt + c]
+            const bf16* kt = ktl[j % 3];
+            f32x4 acc[TI][2];
+#pragma unroll
+            for (int ti = 0; ti < TI; ++ti) acc[ti][0] = acc[ti][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kq = 0; kq < KS; ++kq) {
+                bf16x8 ka[TI];
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti) ka[ti] = load8<bf16x8>(kt + kofs[kq] + 16 * ti * D);
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) acc[ti][mt] = mma_in<F16>(ka[ti], qb[mt][kq], acc[ti][mt]);
+            }
+            // the ragged end of the chunk and masked tokens score -inf
+            if (t0 + TT > t_end || MASK) {
+                asm volatile("");   // a branch around this rare block, not selects on every tile
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (t0 + 16 * ti + 4 * g + r >= t_end || ((drop >> (4 * ti + r)) & 1))
+                            acc[ti][0][r] = acc[ti][1][r] = kNegInf;
+                    }
+            }
+            // ---- lazy references: checked per lane, moved to the exact max over the latent rarely
+            float mx[2];
+            bool need = false;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                float x = max3_raw(acc[0][mt][0], acc[0][mt][1], acc[0][mt][2]);
+                x = max3_raw(x, acc[0][mt][3], acc[1][mt][0]);
+                x = max3_raw(x, acc[1][mt][1], acc[1][mt][2]);
+                x = fmaxf(x, acc[1][mt][3]);
+#pragma unroll
+                for (int ti = 2; ti < TI; ++ti) {
+                    x = max3_raw(x, acc[ti][mt][0], acc[ti][mt][1]);
+                    x = max3_raw(x, acc[ti][mt][2], acc[ti][mt][3]);
+                }
+                mx[mt] = x * scale2;
+                rt[mt] = fmaxf(rt[mt], mx[mt]);
+                need |= mx[mt] > R[mt] + kLazy;
+            }
+            if (__any(need)) {
+                asm volatile("");   // a branch: the rescale of U is rare
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const float m4 = rows_max4(mx[mt]);
+                    const bool mv = m4 > R[mt] + kLazy;
+                    const float Rn = mv ? m4 : R[mt];
+                    const float gam = mv ? exp2f_fast(R[mt] - Rn) : 1.0f;   // 0 when R = -inf
+                    R[mt] = Rn;
+                    dl[mt] *= gam;
+#pragma unroll
+                    for (int di = 0; di < DT; ++di) U[di][mt] *= gam;
+                }
+            }
+            // ---- E = 2^(S - R) (<= 2^kLazy, fp16) and its den.  A latent with no reference
+            //      yet (every token so far masked) has E = 0.
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float nR = R[mt] == kNegInf ? kNegInf : -R[mt];
+                float es = 0.0f;
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float e = exp2f_fast(fmaf(acc[ti][mt][r], scale2, nR));
+                        es += e;
+                        eh[ti >> 1][mt][4 * (ti & 1) + r] = (f16)e;
+                    }
+                dl[mt] += es;
+            }
+            // tile j + 1 has landed (tile j + 2 may still be in flight); every wave is done
+            // with the buffers that iteration j + 1 refills
+            FLARE_WAIT_VMCNT((2 * Dma::NK));
+            lds_barrier();   // no memory fence: it would wait for the DMA of tile j + 2
+        }
+        if (NS > 0) value_product(NS - 1);
+        FLARE_WAIT_VMCNT(0);   // the DMA of the two tiles past the end has landed
+    };
+
+    if (tid == 0) redo_bf16 = 0;
+    __syncthreads();
+    pass(std::false_type{});
+    if constexpr (!F16) {
+        // a bf16 value outside the fp16 range (or a non-finite input) left U non-finite:
+        // the chunk is redone with bf16 V
+        bool bad = false;
+#pragma unroll
+        for (int di = 0; di < DT; ++di)
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bad |= !__builtin_isfinite(U[di][mt][r]);
+        if (__any(bad) && lane == 0) redo_bf16 = 1;
+        __syncthreads();
+        if (redo_bf16) pass(std::true_type{});
+    }
+    // ---- the summary relative to the true chunk max
+    const size_t sbase = ((size_t)bh * NC + c_idx) * M;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+        const float Rt = rows_max4(rt[mt]);
+        const float den = rows_sum4(dl[mt]);
+        const float f = Rt == kNegInf ? 0.0f : exp2f_fast(R[mt] - Rt);   // <= 1
+        const int m = m0 + 16 * mt + c;
+        if (g == 0) {
+            cmax[sbase + m] = Rt * kLn2;
+            cden[sbase + m] = den * f;
+        }
+#pragma unroll
+        for (int di = 0; di < DT; ++di)
+            *reinterpret_cast<f32x4*>(cnum + (sbase + m) * D + 16 * di + 4 * g) = U[di][mt] * f;
+    }
+}
+
+}  // namespace mfma
+}  // namespace flare
+
+namespace flare {
+using namespace mfma;
+
+int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                      int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
+                      const int32_t* tmask, bool f16in, hipStream_t stream) {
+    FLARE_REQUIRE(chunk > 0, "chunk_prepare_tr: chunk must be positive");
+    FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
+                  "chunk_prepare_tr: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    const int64_t NC = (N + chunk - 1) / chunk;
+    dim3 grid((unsigned)NC, (unsigned)(B * H));
+    const float s2 = scale * kLog2e;
+#define FLARE_PREP_TR_T(MM, DD, F)                                                                           \
+    do {                                                                                                     \
+        if (tmask != nullptr)                                                                                \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, true>), grid, dim3(2 * MM), 0, stream,           \
+                               (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
+                               cmax, cden, cnum, tmask);                                                     \
+        else                                                                                                 \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false>), grid, dim3(2 * MM), 0, stream,          \
+                               (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
+                               cmax, cden, cnum, tmask);                                                     \
+    } while (0)
+#define FLARE_PREP_TR(MM, DD)                        \
+    do {                                             \
+        if (f16in) FLARE_PREP_TR_T(MM, DD, true);    \
+        else FLARE_PREP_TR_T(MM, DD, false);         \
+    } while (0)
+    if (M == 128 && D == 64) FLARE_PREP_TR(128, 64);
+    else if (M == 128 && D == 128) FLARE_PREP_TR(128, 128);
+    else if (M == 256 && D == 64) FLARE_PREP_TR(256, 64);
+    else FLARE_PREP_TR(256, 128);
+#undef FLARE_PREP_TR
+#undef FLARE_PREP_TR_T
+    return check_launch("chunk_prepare_tr");
+}
+
+}  // namespace flare

@@ -62,6 +62,18 @@ int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset);
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, bool f16in, hipStream_t stream);
+// Phase 1 with wave-private latents (chunk_prepare_tr); FLARE_PREPARE_KERNEL=pc keeps
+// the producer / consumer kernel chunk_prepare_pc instead (A/B checks).
+int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                      int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
+                      const int32_t* tmask, bool f16in, hipStream_t stream);
+inline bool prepare_tr_enabled() {
+    static const bool on = [] {
+        const char* e = getenv("FLARE_PREPARE_KERNEL");
+        return !(e && e[0] == 'p');
+    }();
+    return on;
+}
 // alpha: NULL for shared decoder weights; else the decoder softmax [B*H, N, M]
 // (fp16) written by launch_decoder_alpha, for separate Qdec / Kdec.
 // redo: NULL, or [B*H, NC] ints; the kernel writes 1 for a chunk in which some
