@@ -16,6 +16,7 @@ recomputes the chunk statistics from the saved inputs and output.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 
 import torch
@@ -63,6 +64,28 @@ def _decoder_args(Q, K, Q_dec, K_dec, separate_q, separate_k):
 
 def _prep(t, dtype):
     return None if t is None else t.to(dtype).contiguous()
+
+
+_PHASES = ("flare_chunk_prepare", "flare_chunk_prefix", "flare_chunk_fwd")
+
+
+def forward_kernel_resources(dtype, M, Dk, Dv, shared, chunk):
+    """Per phase, the resources of the kernel the forward launches: waves per workgroup,
+    VGPRs per lane, spilled 4-byte slots per lane and LDS bytes per workgroup (the
+    reference's _maybe_record_kernel_resource, training.py:4-18, reads the same facts
+    from Triton's compiled kernels).  A phase whose kernel the library does not report
+    (scalar or earlier kernels) is left out."""
+    lib = _lib.lib()
+    out = (ctypes.c_int32 * 4)()
+    res = {}
+    for phase, name in enumerate(_PHASES):
+        rc = lib.flare_forward_kernel_resources(_lib.dtype_code(dtype), M, Dk, Dv, int(shared), chunk, phase,
+                                                ctypes.cast(out, ctypes.c_void_p))
+        if rc != 0:
+            continue
+        res[name] = {"num_waves": int(out[0]), "regs_per_thread": int(out[1]), "spills": int(out[2]) // 4,
+                     "shared_bytes": int(out[3])}
+    return res
 
 
 def run_chunked_forward(Q, K, V, qd, kd, *, scale, chunk, out_dtype, state=None,
@@ -199,6 +222,9 @@ class AutoRegressiveFLARE(autograd.Function):
                 Q, K, V, qd, kd, scale=scale, chunk=chunk, out_dtype=out_dtype,
                 timings=profile_data["forward"] if profile else None,
             )
+            if profile:
+                profile_data["forward_resources"] = forward_kernel_resources(
+                    _compute_dtype(Q, K, V, qd, kd), M, D_score, D_value, qd is None and kd is None, chunk)
         ctx.scale = scale
         ctx.sep = (qd is not None, kd is not None)
         ctx.save_for_backward(Q, K, V, qd, kd, Y)

@@ -546,6 +546,39 @@ int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64
     return default_chunk(B, N, H, M, Dv);
 }
 
+int flare_forward_kernel_resources(int dtype, int64_t M, int64_t Dk, int64_t Dv, int shared, int64_t chunk,
+                                   int phase, int32_t* out) {
+    FLARE_REQUIRE(out != nullptr && phase >= 0 && phase <= 2, "kernel_resources: bad arguments");
+    hipFuncAttributes attr{};
+    int threads = 0;
+    const bool f16in = dtype == FLARE_F16;
+    const bool tile_shape = Dk == Dv && (M == 128 || M == 256) && (Dk == 64 || Dk == 128);
+    if (phase == 1) {
+        FLARE_REQUIRE(hipFuncGetAttributes(&attr, (const void*)chunk_prefix_kernel) == hipSuccess,
+                      "kernel_resources: hipFuncGetAttributes failed");
+        threads = 256;
+    } else if (phase == 0) {
+        // the kernel launch_prepare picks for this call: chunk_prepare_tr, or none reported
+        FLARE_REQUIRE((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv) &&
+                          output_pc_enabled() && prepare_tr_enabled() && tile_shape,
+                      "kernel_resources: this call does not run chunk_prepare_tr");
+        const int rc = prepare_tr_attributes(M, Dk, f16in, &attr, &threads);
+        if (rc) return rc;
+    } else {
+        FLARE_REQUIRE((mfma_phase_mask() & 2) && chunk % 32 == 0 &&
+                          mfma_output_supported(dtype, dtype, true, M, Dk, Dv) && output_pc_enabled() &&
+                          output_tr_enabled() && tile_shape,
+                      "kernel_resources: this call does not run chunk_output_tr");
+        const int rc = output_tr_attributes(M, Dk, shared == 0, f16in, &attr, &threads);
+        if (rc) return rc;
+    }
+    out[0] = threads / 64;
+    out[1] = attr.numRegs;
+    out[2] = (int32_t)attr.localSizeBytes;
+    out[3] = (int32_t)attr.sharedSizeBytes;
+    return FLARE_OK;
+}
+
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Bytes of the chunk summaries (max, den, num) and the per-chunk redo flags of the

@@ -953,4 +953,20 @@ int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset) {
     return FLARE_OK;
 }
 
+int output_tr_attributes(int64_t M, int64_t D, bool sep, bool f16in, hipFuncAttributes* attr, int* threads) {
+    const void* f = nullptr;
+#define FLARE_OUT_TR_F(MM, DD)                                                                          \
+    f = sep ? (f16in ? (const void*)chunk_output_tr<MM, DD, true, true> : (const void*)chunk_output_tr<MM, DD, true, false>) \
+            : (f16in ? (const void*)chunk_output_tr<MM, DD, false, true> : (const void*)chunk_output_tr<MM, DD, false, false>)
+    if (M == 128 && D == 64) FLARE_OUT_TR_F(128, 64);
+    else if (M == 128 && D == 128) FLARE_OUT_TR_F(128, 128);
+    else if (M == 256 && D == 64) FLARE_OUT_TR_F(256, 64);
+    else if (M == 256 && D == 128) FLARE_OUT_TR_F(256, 128);
+#undef FLARE_OUT_TR_F
+    FLARE_REQUIRE(f != nullptr, "chunk_output_tr: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    *threads = (int)(64 * (M / 64 + D / 32));
+    FLARE_REQUIRE(hipFuncGetAttributes(attr, f) == hipSuccess, "chunk_output_tr: hipFuncGetAttributes failed");
+    return FLARE_OK;
+}
+
 }  // namespace flare

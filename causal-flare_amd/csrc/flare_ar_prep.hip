@@ -414,4 +414,19 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
     return check_launch("chunk_prepare_tr");
 }
 
+int prepare_tr_attributes(int64_t M, int64_t D, bool f16in, hipFuncAttributes* attr, int* threads) {
+    const void* f = nullptr;
+#define FLARE_PREP_TR_F(MM, DD)                                                                       \
+    f = f16in ? (const void*)chunk_prepare_tr<MM, DD, true, false> : (const void*)chunk_prepare_tr<MM, DD, false, false>
+    if (M == 128 && D == 64) FLARE_PREP_TR_F(128, 64);
+    else if (M == 128 && D == 128) FLARE_PREP_TR_F(128, 128);
+    else if (M == 256 && D == 64) FLARE_PREP_TR_F(256, 64);
+    else if (M == 256 && D == 128) FLARE_PREP_TR_F(256, 128);
+#undef FLARE_PREP_TR_F
+    FLARE_REQUIRE(f != nullptr, "chunk_prepare_tr: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    *threads = (int)(2 * M);
+    FLARE_REQUIRE(hipFuncGetAttributes(attr, f) == hipSuccess, "chunk_prepare_tr: hipFuncGetAttributes failed");
+    return FLARE_OK;
+}
+
 }  // namespace flare

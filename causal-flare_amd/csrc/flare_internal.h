@@ -67,6 +67,9 @@ int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, in
 int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, bool f16in, hipStream_t stream);
+// Register, scratch and LDS use of the kernels the forward launches (profile=True).
+int prepare_tr_attributes(int64_t M, int64_t D, bool f16in, hipFuncAttributes* attr, int* threads);
+int output_tr_attributes(int64_t M, int64_t D, bool sep, bool f16in, hipFuncAttributes* attr, int* threads);
 inline bool prepare_tr_enabled() {
     static const bool on = [] {
         const char* e = getenv("FLARE_PREPARE_KERNEL");

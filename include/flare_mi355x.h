@@ -131,6 +131,19 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
 int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 
 /*
+ * Resources of a forward kernel this library launches for the given call
+ * (phase 0: chunk summaries, 1: prefix scan, 2: token replay), for the
+ * profile=True record: out[0] waves per workgroup, out[1] VGPRs per lane,
+ * out[2] scratch (spill) bytes per lane, out[3] LDS bytes per workgroup.
+ * Replaces the reference's _maybe_record_kernel_resource
+ * (autoregressive/training.py:4-18), which reads the same facts from Triton's
+ * compiled kernels.  Phases 0 and 2 answer FLARE_ERR_INVALID when the call
+ * would run another kernel than chunk_prepare_tr / chunk_output_tr.
+ */
+int flare_forward_kernel_resources(int dtype, int64_t M, int64_t Dk, int64_t Dv, int shared, int64_t chunk,
+                                   int phase, int32_t* out);
+
+/*
  * Backward of the chunked forward (flare_ar_forward without initial state or
  * mask): from the forward's inputs, its output Y and dY (all in `dtype`,
  * Y and dY [B, N, H, Dv]) write dQ [H, M, Dk], dK [B, N, H, Dk], dV [B, N, H, Dv]

@@ -725,3 +725,31 @@ def test_semi_ar_mfma_fp16(M, D, block):
     assert_parity(y, y_ref, torch.float16, f"semi mfma fp16 M={M} D={D} block={block}")
     np.testing.assert_allclose(to_np(aux["LSE_dec"]), lse_dec, rtol=1e-4, atol=1e-4)
     np.testing.assert_allclose(to_np(aux["LSE_enc"]), lse_enc, rtol=1e-4, atol=1e-4)
+
+
+# --------------------------------------------------------------------------
+# profile=True: per-phase timings and kernel resources
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("M,D,waves", [(128, 64, 4), (256, 128, 8)])
+def test_profile_reports_timings_and_kernel_resources(M, D, waves):
+    """profile=True returns (Y, dict) with per-phase forward timings and totals
+    (reference training.py:4-50) and, per phase, the launched kernel's waves per
+    workgroup, VGPRs, spills and LDS bytes (the reference's backward_resources
+    record, training.py:4-18, 4418); Y equals the call without profile."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("profile_resources", M, D)
+    q, k, v = seeded(9, 1, 700, 2, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    y, prof = flare_autoregressive_triton(qd, kd, vd, profile=True)
+    assert torch.equal(y, flare_autoregressive_triton(qd, kd, vd))
+    assert set(prof["forward"]) == {"flare_chunk_prepare", "flare_chunk_prefix", "flare_chunk_fwd"}
+    assert all(t > 0 for t in prof["forward"].values())
+    assert prof["total_ms"] == pytest.approx(prof["forward_total_ms"] + prof["backward_total_ms"])
+    res = prof["forward_resources"]
+    assert set(res) == {"flare_chunk_prepare", "flare_chunk_prefix", "flare_chunk_fwd"}
+    for name, r in res.items():
+        assert 0 < r["regs_per_thread"] <= 512 and r["spills"] >= 0, (name, r)
+    assert res["flare_chunk_prepare"]["num_waves"] == M // 32
+    assert res["flare_chunk_fwd"]["num_waves"] == M // 64 + D // 32
+    assert res["flare_chunk_fwd"]["shared_bytes"] > 32 * 1024 and res["flare_chunk_prepare"]["shared_bytes"] > 0
+    assert waves == M // 32
