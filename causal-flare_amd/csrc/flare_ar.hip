@@ -39,7 +39,9 @@ template <typename T>
 __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, int N, int H,
     int M, int Dk, int Dv, float scale, int chunk, float* __restrict__ cmax,
-    float* __restrict__ cden, float* __restrict__ cnum, const int32_t* __restrict__ tmask) {
+    float* __restrict__ cden, float* __restrict__ cnum, const int32_t* __restrict__ tmask, float power) {
+    // power > 0: the stablemax encoder (E = stablemax_transform(s), no running max:
+    // the summary's max stays 0, so the prefix merges are plain sums)
     extern __shared__ float smem[];
     float* k_tile = smem;                       // [TT][Dk]
     float* v_tile = k_tile + kPrepTT * Dk;      // [TT][Dv]
@@ -52,7 +54,7 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
     const int m = mbase + ml;
     const T* q_h = Q + (size_t)h * M * Dk;
 
-    float mx = kNegInf, den = 0.0f;
+    float mx = power > 0.0f ? 0.0f : kNegInf, den = 0.0f;
     float num[kPrepCols];
 #pragma unroll
     for (int i = 0; i < kPrepCols; ++i) num[i] = 0.0f;
@@ -86,9 +88,9 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
         for (int i = 0; i < nt; ++i) {
             const float s = s_tile[i * kPrepMT + ml];
             if (s == kNegInf) continue;     // a masked token (no update; keeps mx = -inf safe)
-            const float m_new = fmaxf(mx, s);
-            const float r = __expf(mx - m_new);     // mx = -inf on the first token -> 0
-            const float e = __expf(s - m_new);
+            const float m_new = power > 0.0f ? mx : fmaxf(mx, s);
+            const float r = power > 0.0f ? 1.0f : __expf(mx - m_new);     // mx = -inf on the first token -> 0
+            const float e = power > 0.0f ? stablemax_transform(s, power) : __expf(s - m_new);
             den = den * r + e;
             const float* vr = v_tile + i * Dv;
 #pragma unroll
@@ -201,9 +203,12 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     const T* __restrict__ Qdec, const T* __restrict__ Kdec, int N, int H, int M, int Dk, int Dv,
     int DT, int TT, float scale, int chunk, bool shared, const float* __restrict__ pmax,
     const float* __restrict__ pden, const float* __restrict__ pnum, void* __restrict__ Y,
-    int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask, const int* __restrict__ only) {
+    int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask, const int* __restrict__ only,
+    float power) {
     // only: when given, [B*H, NC] flags; chunks whose flag is 0 are left alone (the
-    // tokenwise replay of the chunks an MFMA output kernel could not resolve)
+    // tokenwise replay of the chunks an MFMA output kernel could not resolve).
+    // power > 0: the stablemax encoder (den += stablemax_transform(s), no rescale);
+    // the decoder weights stay a softmax over the latents.
     if (only != nullptr && only[(size_t)blockIdx.y * gridDim.x + blockIdx.x] == 0) return;
     extern __shared__ float smem[];
     const int R = kNT / DT;
@@ -296,7 +301,14 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
             const float li = lse[i];
             for (int m = tid; m < M; m += kNT) {
                 const float s = s_tile[i * M + m];
-                const MergeScales ts = token_scales(mstate[m], s);
+                MergeScales ts;
+                if (power > 0.0f) {
+                    ts.m_new = mstate[m];
+                    ts.sa = 1.0f;
+                    ts.sb = stablemax_transform(s, power);
+                } else {
+                    ts = token_scales(mstate[m], s);
+                }
                 const float dn = dstate[m] * ts.sa + ts.sb;
                 mstate[m] = ts.m_new;
                 dstate[m] = dn;
@@ -335,8 +347,8 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
 static int launch_prepare(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum,
-                          hipStream_t stream, const int32_t* tmask = nullptr) {
-    if ((mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv)) {
+                          hipStream_t stream, const int32_t* tmask = nullptr, float power = 0.0f) {
+    if (power <= 0.0f && (mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv)) {
         if (output_pc_enabled() && (M == 128 || M == 256))
             return launch_prepare_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, tmask,
                                      dtype == FLARE_F16, stream);
@@ -352,7 +364,7 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
 #define FLARE_PREP(TY)                                                                          \
     hipLaunchKernelGGL(chunk_prepare_kernel<TY>, grid, dim3(kNT), sm, stream,                   \
                        (const TY*)Q, (const TY*)K, (const TY*)V, (int)N, (int)H, (int)M,         \
-                       (int)Dk, (int)Dv, scale, (int)chunk, cmax, cden, cnum, tmask)
+                       (int)Dk, (int)Dv, scale, (int)chunk, cmax, cden, cnum, tmask, power)
     if (dtype == FLARE_BF16) FLARE_PREP(__hip_bfloat16);
     else if (dtype == FLARE_F16) FLARE_PREP(__half);
     else FLARE_PREP(float);
@@ -391,7 +403,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
                          const float* pden, const float* pnum, void* Y, int out_dtype,
                          float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr,
-                         void* alpha_ws = nullptr, int* redo = nullptr) {
+                         void* alpha_ws = nullptr, int* redo = nullptr, float power = 0.0f) {
     const bool shared = Qdec == nullptr && Kdec == nullptr;
     // A launch of the scalar kernel restricted to the chunks flagged in `only` (or all).
     auto scalar = [&](const int* only) -> int {
@@ -415,7 +427,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
     hipLaunchKernelGGL((chunk_output_kernel<TY, RW>), grid, dim3(kNT), sm, stream, (const TY*)Q, \
                        (const TY*)K, (const TY*)V, (const TY*)qd, (const TY*)kd, (int)N, (int)H,  \
                        (int)M, (int)Dk, (int)Dv, DT, TT, scale, (int)chunk, shared, pmax, pden,   \
-                       pnum, Y, out_dtype, lse_dec, tmask, only)
+                       pnum, Y, out_dtype, lse_dec, tmask, only, power)
 #define FLARE_OUT_ROWS(TY)                   \
     if (rows <= 8) FLARE_OUT(TY, 8);         \
     else if (rows <= 16) FLARE_OUT(TY, 16);  \
@@ -429,7 +441,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
         return check_launch("chunk_output_kernel");
     };
     // the MFMA kernels run with the redo flags (the chunks they hand back to the scalar kernel)
-    if ((mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr && redo != nullptr) {
+    if (power <= 0.0f && (mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr && redo != nullptr) {
         int rc = -1;
         if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled())) {
             rc = launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
@@ -610,6 +622,36 @@ int flare_ar_forward(const void* Q, const void* K, const void* V, const void* Qd
                      void* stream) {
     return flare_ar_forward_masked(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, m0, d0, u0,
                                    m_fin, d_fin, u_fin, Y, out_dtype, nullptr, workspace, workspace_bytes, stream);
+}
+
+int flare_stablemax_forward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec,
+                            int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
+                            float scale, int64_t chunk, float power, void* Y, int out_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+    FLARE_REQUIRE(Q && K && V && Y, "stablemax_forward: null pointer");
+    FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0,
+                  "stablemax_forward: sizes must be positive");
+    FLARE_REQUIRE(power > 0.0f && power < 1e30f, "stablemax_forward: power must be positive and finite");
+    if (chunk <= 0) chunk = default_chunk(B, N, H, M, Dv);
+    const size_t need = flare_ar_forward_workspace_size(B, N, H, M, Dv, chunk);
+    if (!workspace || workspace_bytes < need) {
+        set_error("stablemax_forward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+        return FLARE_ERR_WORKSPACE;
+    }
+    const int64_t NC = (N + chunk - 1) / chunk;
+    const size_t per = (size_t)B * H * NC * M;
+    char* ws = (char*)workspace;
+    float* cmax = (float*)ws;
+    float* cden = (float*)(ws + align256(per * sizeof(float)));
+    float* cnum = (float*)(ws + 2 * align256(per * sizeof(float)));
+    hipStream_t s = (hipStream_t)stream;
+    int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s, nullptr, power);
+    if (rc) return rc;
+    // the summaries' maxima are 0: the online-softmax merges of the scan are plain sums
+    rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, s);
+    if (rc) return rc;
+    return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, Y,
+                         out_dtype, nullptr, s, nullptr, nullptr, nullptr, power);
 }
 
 int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const void* Qdec,

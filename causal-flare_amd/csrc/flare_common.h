@@ -56,6 +56,23 @@ __device__ __forceinline__ MergeScales token_scales(float m, float s) {
     return r;
 }
 
+// The stablemax score transform (reference autoregressive/stablemax.py:45-52,
+// stablemax_triton.py:137-170): (1 + x)^p for x >= 0 and (1 - x)^-p for x < 0,
+// positive and monotone; x = -inf gives 0.  Powers 1-4 by products, others as
+// exp2(p log2 base).
+__device__ __forceinline__ float stablemax_transform(float x, float p) {
+    const float base = x >= 0.0f ? 1.0f + x : 1.0f - x;
+    float r;
+    if (p == 1.0f) r = base;
+    else if (p == 2.0f) r = base * base;
+    else if (p == 3.0f) r = base * base * base;
+    else if (p == 4.0f) {
+        const float b2 = base * base;
+        r = b2 * b2;
+    } else r = exp2f(p * log2f(base));
+    return x >= 0.0f ? r : 1.0f / r;
+}
+
 // ---------------------------------------------------------------------------
 // Wavefront (64-lane) and workgroup reductions.
 // ---------------------------------------------------------------------------

@@ -127,6 +127,21 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
                             void* Y, int out_dtype, const int32_t* token_mask, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/*
+ * Stablemax FLARE forward, the non-write-gated path of
+ * flare_autoregressive_stablemax_triton (autoregressive/stablemax_triton.py:
+ * 1707-2055, 2423-2468; PyTorch form stablemax.py:482-635):
+ *   y_t = sum_m softmax_m(scale qd_t . kd_m) *
+ *         (sum_{tau<=t} s(a_tau,m) v_tau) / (sum_{tau<=t} s(a_tau,m)),
+ *   a_tau,m = scale k_tau . q_m,  s(x) = (1+x)^power (x >= 0), (1-x)^-power (x < 0).
+ * Qdec / Kdec may be NULL (K and Q).  Runs the fp32 chunk kernels with the
+ * stablemax encoder; workspace of flare_ar_forward_workspace_size bytes.
+ */
+int flare_stablemax_forward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec,
+                            int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
+                            float scale, int64_t chunk, float power, void* Y, int out_dtype, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* The chunk length flare_ar_forward uses when called with chunk <= 0. */
 int64_t flare_ar_default_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv);
 

@@ -21,6 +21,9 @@ Two layers:
     - ``brute_semi_ar_state``: the block-causal definition continued from a
       cached state (the semi-AR cached prefill / block decode, which the
       reference leaves as stubs).
+    - ``brute_stablemax``: the stablemax variant's per-token definition
+      (``autoregressive/stablemax_triton.py:1718-1731``), and
+      ``stablemax_chunked``, its chunked form (``stablemax.py:578-635``).
   They are the pins for the C restatement (see tests/test_oracle.py).
 * ``ar_grads``: fp64 torch autograd of ``ar_forward_torch64`` (the same
   definition with cumulative sums), the ground truth of the backward; pinned
@@ -224,6 +227,73 @@ def brute_ar(Q, K, V, scale=None, Q_dec=None, K_dec=None):
         alpha = _softmax(A[:, :, t, :], axis=-1)
         Y[:, :, t] = np.einsum("bhm,bhmd->bhd", alpha, Z)
     return Y.transpose(0, 2, 1, 3)
+
+
+def stablemax_transform(x, power):
+    """The stablemax score transform (stablemax.py:45-52): (1 + x)^p for x >= 0,
+    (1 - x)^-p for x < 0.  fp64."""
+    x = np.asarray(x, np.float64)
+    return np.where(x >= 0, np.power(np.where(x >= 0, 1.0 + x, 1.0), power),
+                    np.power(np.where(x < 0, 1.0 - x, 1.0), -power))
+
+
+def brute_stablemax(Q, K, V, power=2.0, scale=None, Q_dec=None, K_dec=None):
+    """Stablemax FLARE by its per-token definition (stablemax_triton.py:1718-1731,
+    stablemax.py:595-603): z_t[m] = sum_{tau<=t} s(a_tau,m) v_tau / sum_{tau<=t} s(a_tau,m),
+    y_t = sum_m softmax_m(scale qd_t . kd_m) z_t[m].  fp64, one token at a time."""
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    W = stablemax_transform(scale * np.einsum("bnhd,hmd->bhnm", K, Q), power)   # [B,H,N,M]
+    A = scale * np.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    Vt = V.transpose(0, 2, 1, 3)
+    Y = np.empty((B, H, N, Dv))
+    for t in range(N):
+        den = W[:, :, : t + 1].sum(axis=2)                                       # [B,H,M]
+        num = np.einsum("bhtm,bhtd->bhmd", W[:, :, : t + 1], Vt[:, :, : t + 1])
+        alpha = _softmax(A[:, :, t, :], axis=-1)
+        Y[:, :, t] = np.einsum("bhm,bhmd->bhd", alpha, num / den[..., None])
+    return Y.transpose(0, 2, 1, 3)
+
+
+def stablemax_chunked(Q, K, V, power=2.0, scale=None, chunk_size=64, Q_dec=None, K_dec=None):
+    """Stablemax FLARE in the chunked form of the reference's PyTorch path
+    (stablemax.py:578-635): per-chunk encoder den / num, strict chunk prefixes,
+    the decoder softmax over latents, then prefix_out + tril(R W^T) V inside each
+    chunk with R = p_dec / total_den.  fp64; a different summation from
+    brute_stablemax, against which tests/test_oracle.py pins it."""
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = _f64(Q_dec) if Q_dec is not None else K
+    Kd = _f64(K_dec) if K_dec is not None else Q
+    C = int(chunk_size)
+    NC = -(-N // C)
+    pad = NC * C - N
+    Kp = np.concatenate([K, np.zeros((B, pad, H, Dk))], axis=1)
+    Vp = np.concatenate([V, np.zeros((B, pad, H, Dv))], axis=1)
+    Qdp = np.concatenate([Qd, np.zeros((B, pad, H, Dk))], axis=1)
+    Kc = Kp.reshape(B, NC, C, H, Dk).transpose(0, 3, 1, 2, 4)                   # [B,H,NC,C,Dk]
+    Vc = Vp.reshape(B, NC, C, H, Dv).transpose(0, 3, 1, 2, 4)
+    Qdc = Qdp.reshape(B, NC, C, H, Dk).transpose(0, 3, 1, 2, 4)
+    W = stablemax_transform(scale * np.einsum("bhncd,hmd->bhncm", Kc, Q), power)
+    if pad:
+        W[:, :, -1, C - pad:, :] = 0.0      # padded tokens carry no weight
+    cden = W.sum(axis=3)                                                          # [B,H,NC,M]
+    cnum = np.einsum("bhncm,bhncd->bhnmd", W, Vc)
+    prev_den = np.cumsum(cden, axis=2) - cden
+    prev_num = np.cumsum(cnum, axis=2) - cnum
+    p_dec = _softmax(scale * np.einsum("bhncd,hmd->bhncm", Qdc, Kd), axis=-1)
+    total = prev_den[:, :, :, None, :] + np.cumsum(W, axis=3)
+    R = p_dec / np.where(total > 0, total, 1.0)
+    prefix_out = np.einsum("bhncm,bhnmd->bhncd", R, prev_num)
+    mix = np.einsum("bhncm,bhnsm->bhncs", R, W) * np.tril(np.ones((C, C)))
+    Yc = prefix_out + np.einsum("bhncs,bhnsd->bhncd", mix, Vc)
+    return Yc.reshape(B, H, NC * C, Dv)[:, :, :N].transpose(0, 2, 1, 3)
 
 
 def brute_ar_state(Q, K, V, state=None, scale=1.0, attention_mask=None, Q_dec=None, K_dec=None):

@@ -207,3 +207,25 @@ def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_stablemax_validation():
+    """flare_autoregressive_stablemax_triton keeps the reference's refusals
+    (stablemax_triton.py:2441-2452, 1754-1758) and its module export."""
+    from causal_flare.autoregressive import flare_autoregressive_stablemax_triton as smx
+    from causal_flare.autoregressive import FLAREAutoregressiveStablemaxTriton  # noqa: F401
+    q, k, v = torch.randn(2, 16, 16), torch.randn(1, 32, 2, 16), torch.randn(1, 32, 2, 16)
+    for kw, msg in ((dict(eps=1e-6), "does not use eps"), (dict(profile=True), "profile=True"),
+                    (dict(state={}), "recurrent state"), (dict(attention_mask=torch.ones(1, 32)), "attention_mask"),
+                    (dict(return_state=True), "return_state=True"), (dict(write_gate=True), "non-write-gated")):
+        with pytest.raises(NotImplementedError, match=re.escape(msg)):
+            smx(q, k, v, **kw)
+    with pytest.raises(ValueError, match="chunk size divisible by 16"):
+        smx(q, k, v, chunk_size=24)
+    with pytest.raises(ValueError, match="power must be positive"):
+        smx(q, k, v, power=0.0)
+    with pytest.raises(RuntimeError, match="requires GPU tensors"):
+        smx(q, k, v)
+    # N = 0 needs no kernel
+    y = smx(q, k[:, :0], v[:, :0])
+    assert y.shape == (1, 0, 2, 16) and y.dtype == v.dtype

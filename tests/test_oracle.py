@@ -316,3 +316,61 @@ def test_semi_grad_oracle_matches_finite_differences(sep_q, sep_k):
                 vals.append(float((O.brute_semi_ar(xs[0], xs[1], xs[2], 2, 0.8, xs[3], xs[4]) * Gn).sum()))
             fd.reshape(-1)[j] = (vals[0] - vals[1]) / (2 * h)
         np.testing.assert_allclose(gx, fd, rtol=1e-6, atol=1e-8)
+
+
+# --------------------------------------------------------------------------
+# Stablemax variant (reference autoregressive/stablemax.py, stablemax_triton.py)
+# --------------------------------------------------------------------------
+def test_stablemax_transform_closed_forms():
+    """s(x) = (1+x)^p (x >= 0), (1-x)^-p (x < 0): s(0) = 1, s(1) = 2^p, s(-1) = 2^-p,
+    s(3) = 4^p, s(-3) = 4^-p; positive and increasing."""
+    for p in (1.0, 2.0, 3.0, 4.0, 2.5):
+        s = O.stablemax_transform(np.array([0.0, 1.0, -1.0, 3.0, -3.0]), p)
+        np.testing.assert_allclose(s, [1.0, 2.0 ** p, 2.0 ** -p, 4.0 ** p, 4.0 ** -p], rtol=1e-14)
+        x = np.linspace(-20, 20, 4001)
+        sx = O.stablemax_transform(x, p)
+        assert (sx > 0).all() and (np.diff(sx) > 0).all()
+
+
+@pytest.mark.parametrize("power", [1.0, 2.0, 3.0, 4.0, 2.5])
+@pytest.mark.parametrize("chunk", [16, 32, 48])
+def test_stablemax_chunked_equals_per_token_definition(power, chunk):
+    """The chunked form (stablemax.py:578-635: chunk sums, strict prefixes,
+    tril(R W^T) V inside a chunk) equals the per-token definition, ragged N,
+    with shared and with separate decoder tensors."""
+    rng = np.random.default_rng(11)
+    H, M, D, B, N = 2, 24, 16, 2, 77
+    q = rng.standard_normal((H, M, D))
+    k = rng.standard_normal((B, N, H, D))
+    v = rng.standard_normal((B, N, H, D))
+    np.testing.assert_allclose(O.stablemax_chunked(q, k, v, power=power, chunk_size=chunk),
+                               O.brute_stablemax(q, k, v, power=power), rtol=1e-10, atol=1e-12)
+    qd = rng.standard_normal((B, N, H, D))
+    kd = rng.standard_normal((H, M, D))
+    np.testing.assert_allclose(
+        O.stablemax_chunked(q, k, v, power=power, chunk_size=chunk, Q_dec=qd, K_dec=kd, scale=0.3),
+        O.brute_stablemax(q, k, v, power=power, Q_dec=qd, K_dec=kd, scale=0.3), rtol=1e-10, atol=1e-12)
+
+
+def test_stablemax_zero_scores_give_the_causal_mean():
+    """Q = 0: every score is 0, s = 1 for every (token, latent), so z_t is the mean of
+    v over tau <= t for every latent and y_t (a convex combination of the z) is that
+    mean, whatever the power and the decoder."""
+    rng = np.random.default_rng(12)
+    H, M, D, B, N = 2, 8, 4, 1, 30
+    q = np.zeros((H, M, D))
+    k = rng.standard_normal((B, N, H, D))
+    v = rng.standard_normal((B, N, H, D))
+    mean = np.cumsum(v, axis=1) / np.arange(1, N + 1)[None, :, None, None]
+    for p in (1.0, 3.0):
+        np.testing.assert_allclose(O.brute_stablemax(q, k, v, power=p), mean, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(O.stablemax_chunked(q, k, v, power=p, chunk_size=16), mean, rtol=1e-12, atol=1e-12)
+
+
+def test_stablemax_first_token_is_its_value():
+    """N = 1: z_0 = v_0 for every latent, so y_0 = v_0."""
+    rng = np.random.default_rng(13)
+    q = rng.standard_normal((3, 16, 8))
+    k = rng.standard_normal((2, 1, 3, 8))
+    v = rng.standard_normal((2, 1, 3, 8))
+    np.testing.assert_allclose(O.brute_stablemax(q, k, v, power=2.0), v, rtol=1e-13)
