@@ -21,6 +21,7 @@ Two layers:
     - ``brute_semi_ar_state``: the block-causal definition continued from a
       cached state (the semi-AR cached prefill / block decode, which the
       reference leaves as stubs).
+    - ``chunk_summaries``: phase 1's per-chunk (max, den, num), fp64.
     - ``brute_stablemax``: the stablemax variant's per-token definition
       (``autoregressive/stablemax_triton.py:1718-1731``), and
       ``stablemax_chunked``, its chunked form (``stablemax.py:578-635``).
@@ -227,6 +228,29 @@ def brute_ar(Q, K, V, scale=None, Q_dec=None, K_dec=None):
         alpha = _softmax(A[:, :, t, :], axis=-1)
         Y[:, :, t] = np.einsum("bhm,bhmd->bhd", alpha, Z)
     return Y.transpose(0, 2, 1, 3)
+
+
+def chunk_summaries(Q, K, V, chunk, scale=None):
+    """Per-chunk encoder summaries of the chunked forward's phase 1
+    (flare_chunk_prepare, training.py:914-1018; reference.py:240-300): for chunk c
+    and latent m, max_c = max over the chunk's tokens of s = scale k . q_m (natural
+    log units), den_c = sum exp(s - max_c), num_c = sum exp(s - max_c) v.  fp64;
+    returns (max [B*H, NC, M], den, num [B*H, NC, M, Dv])."""
+    Q, K, V = _f64(Q), _f64(K), _f64(V)
+    H, M, Dk = Q.shape
+    B, N, _, Dv = V.shape
+    scale = resolve_scale(scale, Dk)
+    NC = -(-N // chunk)
+    S = scale * np.einsum("bnhd,hmd->bhnm", K, Q)          # [B,H,N,M]
+    Vt = V.transpose(0, 2, 1, 3)                            # [B,H,N,Dv]
+    mx = np.empty((B, H, NC, M)); den = np.empty((B, H, NC, M)); num = np.empty((B, H, NC, M, Dv))
+    for c in range(NC):
+        sl = slice(c * chunk, min(N, (c + 1) * chunk))
+        m = S[:, :, sl].max(axis=2)
+        e = np.exp(S[:, :, sl] - m[:, :, None])
+        mx[:, :, c], den[:, :, c] = m, e.sum(axis=2)
+        num[:, :, c] = np.einsum("bhtm,bhtd->bhmd", e, Vt[:, :, sl])
+    return mx.reshape(B * H, NC, M), den.reshape(B * H, NC, M), num.reshape(B * H, NC, M, Dv)
 
 
 def stablemax_transform(x, power):

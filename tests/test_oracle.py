@@ -374,3 +374,26 @@ def test_stablemax_first_token_is_its_value():
     k = rng.standard_normal((2, 1, 3, 8))
     v = rng.standard_normal((2, 1, 3, 8))
     np.testing.assert_allclose(O.brute_stablemax(q, k, v, power=2.0), v, rtol=1e-13)
+
+
+def test_chunk_summaries_merge_to_the_whole_sequence_state():
+    """Phase 1's per-chunk (max, den, num), merged over all chunks with the
+    inf-safe online-softmax merge (reference.py:160-187), equal the state
+    {m, d, u} of the whole sequence from the per-token definition
+    (brute_ar_state); with chunk = N they are that state directly."""
+    rng = np.random.default_rng(21)
+    H, M, D, B, N = 2, 16, 8, 2, 70
+    q = rng.standard_normal((H, M, D)) * 0.7
+    k = rng.standard_normal((B, N, H, D))
+    v = rng.standard_normal((B, N, H, D))
+    _, st = O.brute_ar_state(q, k, v, scale=D ** -0.5)
+    for chunk in (16, 24, 70):
+        mx, den, num = O.chunk_summaries(q, k, v, chunk, scale=D ** -0.5)
+        m, d, u = mx[:, 0], den[:, 0], num[:, 0]
+        for c in range(1, mx.shape[1]):
+            mn = np.maximum(m, mx[:, c])
+            a, b = np.exp(m - mn), np.exp(mx[:, c] - mn)
+            d, u, m = d * a + den[:, c] * b, u * a[..., None] + num[:, c] * b[..., None], mn
+        np.testing.assert_allclose(m.reshape(B, H, M), st["m"], rtol=1e-12)
+        np.testing.assert_allclose(d.reshape(B, H, M), st["d"], rtol=1e-10)
+        np.testing.assert_allclose(u.reshape(B, H, M, D), st["u"], rtol=1e-9, atol=1e-12)
