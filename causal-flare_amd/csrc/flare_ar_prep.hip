@@ -222,7 +222,8 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
             }
         };
 
-        for (int j = 0; j < NS; ++j) {
+        // S^T of tile j into acc (the ragged end and masked tokens score -inf)
+        auto scores = [&](int j, f32x4 (&acc)[TI][2]) __attribute__((always_inline)) {
             const int t0 = t_begin + TT * j;
             // masked tokens of this lane (t = t0 + 16 ti + 4 g + r, bit 4 ti + r)
             unsigned drop = 0;
@@ -235,30 +236,8 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                         if (t < t_end && tmask[(size_t)b * N + t] == 0) drop |= 1u << (4 * ti + r);
                     }
             }
-            // tile j + 2 (past the chunk's last tile: copies of its last row, never read), so
-            // that every iteration issues the same number of DMA requests
-            kdma.issue(ktl[(j + 2) % 3], wofs, t0 + 2 * TT, t_end, stride, tid);
-            vdma.issue(vtl[(j + 2) & 3], wofs, t0 + 2 * TT, t_end, stride, tid);
-            // bf16 inputs, first pass: V of tile j (landed at the last barrier) to fp16 for
-            // iteration j + 1 (a value outside the fp16 range becomes inf and shows in U)
-            if constexpr (!F16 && !BF) {
-                const bf16* src = vtl[j & 3];
-                f16* dst = vhl[j & 1];
-#pragma unroll
-                for (int k = 0; k < NCV; ++k) {
-                    const int idx = tid + k * NT;
-                    const bf16x8 x = load8<bf16x8>(src + 8 * idx);
-                    f16x8 y;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) y[i] = (f16)(float)x[i];
-                    *reinterpret_cast<f16x8*>(dst + 8 * idx) = y;
-                }
-            }
-            // the previous tile's value product, before this tile may rescale U
-            if (j > 0) value_product(j - 1);
             // ---- S^T = K Q^T: acc[ti][mt][r] = S[t = 16 ti + 4 g + r][m = 16 mt + c]
             const bf16* kt = ktl[j % 3];
-            f32x4 acc[TI][2];
 #pragma unroll
             for (int ti = 0; ti < TI; ++ti) acc[ti][0] = acc[ti][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -282,6 +261,9 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                             acc[ti][0][r] = acc[ti][1][r] = kNegInf;
                     }
             }
+        };
+        // the lazy references, then E = 2^(S - R) of the tile in acc into eh and its den
+        auto exps = [&](f32x4 (&acc)[TI][2]) __attribute__((always_inline)) {
             // ---- lazy references: checked per lane, moved to the exact max over the latent rarely
             float mx[2];
             bool need = false;
@@ -330,11 +312,59 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                     }
                 dl[mt] += es;
             }
-            // tile j + 1 has landed (tile j + 2 may still be in flight); every wave is done
-            // with the buffers that iteration j + 1 refills
-            FLARE_WAIT_VMCNT((2 * Dma::NK));
-            lds_barrier();   // no memory fence: it would wait for the DMA of tile j + 2
-        }
+        };
+        // Iteration j issues the DMA of tile j + 2, converts V of tile j and runs, per wave,
+        // ... S(j) E(j) | P(j) S(j+1) E(j+1) | ... (S scores, E exponentials, P the value
+        // product).  The waves of the second half of a 256-latent workgroup place the
+        // barrier one step later, after S(j) instead of after E(j): a SIMD then holds one
+        // wave in its MFMA-heavy part (P, S) while the other is in its VALU-heavy part (E),
+        // instead of both in the same part at once.
+        auto loop = [&](auto late_tag) __attribute__((always_inline)) {
+            constexpr bool LATE = decltype(late_tag)::value;
+            f32x4 acc[TI][2];
+            for (int j = 0; j < NS; ++j) {
+                const int t0 = t_begin + TT * j;
+                // tile j + 2 (past the chunk's last tile: copies of its last row, never read), so
+                // that every iteration issues the same number of DMA requests
+                kdma.issue(ktl[(j + 2) % 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+                vdma.issue(vtl[(j + 2) & 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+                // bf16 inputs, first pass: V of tile j (landed at the last barrier) to fp16 for
+                // iteration j + 1 (a value outside the fp16 range becomes inf and shows in U)
+                if constexpr (!F16 && !BF) {
+                    const bf16* src = vtl[j & 3];
+                    f16* dst = vhl[j & 1];
+#pragma unroll
+                    for (int k = 0; k < NCV; ++k) {
+                        const int idx = tid + k * NT;
+                        const bf16x8 x = load8<bf16x8>(src + 8 * idx);
+                        f16x8 y;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) y[i] = (f16)(float)x[i];
+                        *reinterpret_cast<f16x8*>(dst + 8 * idx) = y;
+                    }
+                }
+                if constexpr (LATE) {
+                    if (j > 0) {
+                        exps(acc);
+                        value_product(j - 1);
+                    }
+                    scores(j, acc);
+                } else {
+                    if (j > 0) value_product(j - 1);
+                    scores(j, acc);
+                    exps(acc);
+                }
+                // tile j + 1 has landed (tile j + 2 may still be in flight); every wave is done
+                // with the buffers that iteration j + 1 refills
+                FLARE_WAIT_VMCNT((2 * Dma::NK));
+                lds_barrier();   // no memory fence: it would wait for the DMA of tile j + 2
+            }
+            if constexpr (LATE) {
+                if (NS > 0) exps(acc);
+            }
+        };
+        if (M >= 256 && w >= M / 64) loop(std::true_type{});
+        else loop(std::false_type{});
         if (NS > 0) value_product(NS - 1);
         FLARE_WAIT_VMCNT(0);   // the DMA of the two tiles past the end has landed
     };
