@@ -82,6 +82,8 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
         *reinterpret_cast<bf16x8*>(qs + m * L::QP + 8 * d8) = load8<bf16x8>(Q + ((size_t)h * M + m) * D + 8 * d8);
     }
     const size_t pbase = ((size_t)bh * NC + c_idx) * M;
+    // R is the same on the 16 lanes of a latent's row; dn[mi][r] is this lane's partial den
+    // (its tokens' E, the prefix's den on lane c = 0), summed over the row at block ends
     float R[L::MT][4], dn[L::MT][4];
 #pragma unroll
     for (int mi = 0; mi < L::MT; ++mi)
@@ -89,7 +91,7 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
         for (int r = 0; r < 4; ++r) {
             const int m = mw0 + 16 * mi + 4 * g + r;
             R[mi][r] = pmax[pbase + m] * kLog2e;
-            dn[mi][r] = pden[pbase + m];
+            dn[mi][r] = c == 0 ? pden[pbase + m] : 0.0f;   // this lane's share of the den
         }
     f32x4 U[L::MTA][L::DTW];
 #pragma unroll
@@ -148,30 +150,43 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 #pragma unroll
                         for (int r = 0; r < 4; ++r) s[mi][ti][r] = acc[mi][ti][r] * scale2;
             }
-            // ---- lazy reference max, E (fp16 -> LDS), den
+            // ---- lazy reference max (checked per lane; moved rarely), E (fp16 -> LDS), den
             bool need = false;
 #pragma unroll
             for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
+                for (int r = 0; r < 4; ++r) need |= fmaxf(s[mi][0][r], s[mi][1][r]) > R[mi][r] + kLazy;
+            const bool wave_moved = __any(need);
+            if (wave_moved) {
+                asm volatile("");   // a branch: reference moves are rare
+#pragma unroll
+                for (int mi = 0; mi < L::MT; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
+                        const bool mv = mx > R[mi][r] + kLazy;
+                        const float Rn = mv ? mx : R[mi][r];
+                        const float gam = mv ? exp2f_fast(R[mi][r] - Rn) : 1.0f;   // 0 when R = -inf
+                        R[mi][r] = Rn;
+                        dn[mi][r] *= gam;
+                        if (c == 0) gaml[mw0 + 16 * mi + 4 * g + r] = gam;
+                    }
+            }
+#pragma unroll
+            for (int mi = 0; mi < L::MT; ++mi)
+#pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float mx = row_max16(fmaxf(s[mi][0][r], s[mi][1][r]));
-                    const bool mv = mx > R[mi][r] + kLazy;
-                    need |= mv;
-                    const float Rn = mv ? mx : R[mi][r];
-                    const float gam = mv ? exp2f_fast(R[mi][r] - Rn) : 1.0f;   // 0 when R = -inf
-                    R[mi][r] = Rn;
-                    const float e0 = exp2f_fast(s[mi][0][r] - Rn);
-                    const float e1 = exp2f_fast(s[mi][1][r] - Rn);
-                    dn[mi][r] = dn[mi][r] * gam + row_sum16(e0 + e1);
-                    const int m = mw0 + 16 * mi + 4 * g + r;
-                    if (c == 0) gaml[m] = gam;
-                    f16* er = etl + m * L::EP;
+                    const float e0 = exp2f_fast(s[mi][0][r] - R[mi][r]);
+                    const float e1 = exp2f_fast(s[mi][1][r] - R[mi][r]);
+                    dn[mi][r] += e0 + e1;
+                    f16* er = etl + (mw0 + 16 * mi + 4 * g + r) * L::EP;
                     er[c] = (f16)e0;
                     er[16 + c] = (f16)e1;
                 }
-            const bool wave_moved = __any(need);
             if (lane == 0) moved[w] = wave_moved ? 1 : 0;
-            // ---- decoder log-sum-exp partials per token
+            // ---- decoder log-sum-exp partials per token; the exponentials against the wave's
+            //      maximum lm are kept for alpha = 2^(s - lm) 2^(lm - lse)
+            float ex[L::MT][2][4], lmv[2];
 #pragma unroll
             for (int ti = 0; ti < (SEP ? 0 : 2); ++ti) {
                 float lm = kNegInf;
@@ -184,8 +199,12 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 #pragma unroll
                 for (int mi = 0; mi < L::MT; ++mi)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) ls += exp2f_fast(s[mi][ti][r] - lm);
+                    for (int r = 0; r < 4; ++r) {
+                        ex[mi][ti][r] = exp2f_fast(s[mi][ti][r] - lm);
+                        ls += ex[mi][ti][r];
+                    }
                 ls = rows_sum4(ls);
+                lmv[ti] = lm;
                 if (g == 0) {
                     lsep[(w * T + 16 * ti + c) * 2 + 0] = lm;
                     lsep[(w * T + 16 * ti + c) * 2 + 1] = ls;
@@ -216,22 +235,20 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
                 for (int w2 = 0; w2 < NW; ++w2) ss += lsep[(w2 * T + t) * 2 + 1] * exp2f_fast(lsep[(w2 * T + t) * 2] - mm);
                 const float lse2 = mm + __log2f(ss);
                 if (lse_dec && w == 0 && g == 0) lse_dec[(size_t)bh * N + t0 + t] = lse2 * kLn2;
+                const float sc = exp2f_fast(lmv[ti] - lse2);   // <= 1
 #pragma unroll
                 for (int mi = 0; mi < L::MT; ++mi) {
                     f16x4 a4;
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) a4[r] = (f16)exp2f_fast(s[mi][ti][r] - lse2);
+                    for (int r = 0; r < 4; ++r) a4[r] = (f16)(ex[mi][ti][r] * sc);
                     f16* dst = GA ? grow(blk0, j * T + t) : al + (j * T + t) * L::AP;
                     *reinterpret_cast<f16x4*>(dst + mw0 + 16 * mi + 4 * g) = a4;
                 }
             }
             // ---- numerator: move to new reference maxima (rare), then U += E^T V
-            bool any_moved = false;
 #pragma unroll
-            for (int w2 = 0; w2 < NW; ++w2) any_moved |= moved[w2] != 0;
-            if (any_moved) {
-#pragma unroll
-                for (int mi = 0; mi < L::MTA; ++mi) {
+            for (int mi = 0; mi < L::MTA; ++mi) {
+                if (moved[(16 * mi) / L::MW]) {   // the rows of a wave that moved its references
                     const f32x4 gm = *reinterpret_cast<const f32x4*>(gaml + 16 * mi + 4 * g);
 #pragma unroll
                     for (int di = 0; di < L::DTW; ++di)
@@ -276,9 +293,10 @@ __global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = mw0 + 16 * mi + 4 * g + r;
+                const float den = row_sum16(dn[mi][r]);
                 if (c == 0) {
-                    invd[m] = __builtin_amdgcn_rcpf(dn[mi][r]);
-                    if (lse_enc) lse_enc[((size_t)bh * NB + gblk) * M + m] = (R[mi][r] + __log2f(dn[mi][r])) * kLn2;
+                    invd[m] = __builtin_amdgcn_rcpf(den);
+                    if (lse_enc) lse_enc[((size_t)bh * NB + gblk) * M + m] = (R[mi][r] + __log2f(den)) * kLn2;
                 }
             }
         __syncthreads();   // S3: 1/d visible
