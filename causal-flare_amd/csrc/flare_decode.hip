@@ -17,6 +17,7 @@ namespace flare {
 
 constexpr int kDecNT = 256;
 constexpr int kDecBatchRows = 8;   // float4 rows loaded before any is stored
+constexpr int kDecKPT = 2;         // k / v elements per thread in the fast step (Dk, Dv <= 512)
 
 __device__ __forceinline__ void store_out_dec(void* Y, size_t idx, float v, int out_dtype) {
     if (out_dtype == FLARE_BF16) reinterpret_cast<__hip_bfloat16*>(Y)[idx] = __float2bfloat16(v);
@@ -156,9 +157,14 @@ __global__ __launch_bounds__(kDecNT) void decode_step_kernel(
 
 // Fast step for the common shapes: M = RG * ROWS latents and Dv = 4 * NT4 value
 // columns with RG = 256 / NT4, so every thread owns ROWS rows of one float4
-// column of u.  Those rows, and m / d of the thread's latent, are loaded at the
-// very start; their HBM latency overlaps the scores and the softmax, and the
-// update is applied from registers.  Q rows are read with 16-byte loads.
+// column of u.  Every workgroup of the grid runs its (b,h) at once, so the step
+// is one short chain per workgroup: all reads are issued at the start, the
+// small ones (k, the Q row of thread m, m / d, v) ahead of the u rows, since
+// loads complete in issue order; thread m then forms its score from k read
+// straight from global memory (the same 16 bytes in every thread, scalar
+// loads), so no barrier stands before the scores.  Three barriers follow: the
+// merge scales and per-wave softmax partials published, the weights
+// published, the y partials published.
 template <typename T, int ROWS, int NT4>
 __global__ __launch_bounds__(kDecNT) void decode_step_fast(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
@@ -166,59 +172,95 @@ __global__ __launch_bounds__(kDecNT) void decode_step_fast(
     int H, int M, int Dk, int Dv, float scale, bool shared, float* __restrict__ mst,
     float* __restrict__ dst, float* __restrict__ ust, void* __restrict__ Y, int out_dtype) {
     constexpr int RG = kDecNT / NT4;
+    constexpr int NWV = kDecNT / 64;
+    constexpr int CH = 16 / sizeof(T);   // Q elements per 16-byte load
+    constexpr int QPF = 8;               // 16-byte pieces of the Q row prefetched
     extern __shared__ float smem[];
-    float* kv = smem;                 // [Dk]
-    float* qd = kv + Dk;              // [Dk]
-    float* vv = qd + Dk;              // [Dv]
+    float* vv = smem + 2 * Dk;        // [Dv]
     float* av = vv + Dv;              // [M] decoder scores
     float* gam = av + M;              // [M]
     float* eta = gam + M;             // [M]
     float* wts = eta + M;             // [M]
-    float* red = wts + M;             // [8]
+    float* red = wts + M;             // [2 NWV] per-wave (max, sum) of the decoder softmax
     float4* ypart = reinterpret_cast<float4*>(smem + ((2 * Dk + Dv + 4 * M + 8 + 3) & ~3));  // [RG][NT4]
 
     const int bh = blockIdx.x;
     const int b = bh / H, h = bh % H;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int jt = tid % NT4, rg = tid / NT4;
     if (mask != nullptr && mask[b] == 0) {
         for (int j = tid; j < Dv; j += kDecNT) store_out_dec(Y, (size_t)bh * Dv + j, 0.0f, out_dtype);
         return;
     }
-    // prefetch: this thread's rows of u and the state of latent m = tid
+    // ---- every read of the step, issued up front, the small ones first: loads return
+    //      in issue order, so the scores wait only for k, q and m / d while the u rows
+    //      (the bulk of the step's traffic) are still in flight.  Thread m reads k (and
+    //      the token's decoder query) straight from global memory, the same 16-byte
+    //      pieces for every thread, so no barrier stands before the scores.
+    //      (Clamped indices, no branches: a branch around a load makes the compiler
+    //      wait for it.)
+    const size_t kvoff = (size_t)bh * Dk;
+    const T* qdsrc = shared ? K : Qdec;
+    const int npieces = Dk / CH;
+    typedef unsigned u32v4 __attribute__((ext_vector_type(4)));
+    const u32v4* k4 = reinterpret_cast<const u32v4*>(K + kvoff);
+    const u32v4* qd4 = reinterpret_cast<const u32v4*>(qdsrc + kvoff);
+    u32v4 kpf[QPF], qdpf[QPF], qpf[QPF];
+    const T* qrow = Q + ((size_t)h * M + min(tid, M - 1)) * Dk;
+#pragma unroll
+    for (int p = 0; p < QPF; ++p) {
+        kpf[p] = k4[min(p, npieces - 1)];
+        qpf[p] = reinterpret_cast<const u32v4*>(qrow)[min(p, npieces - 1)];
+    }
+    if (!shared) {
+#pragma unroll
+        for (int p = 0; p < QPF; ++p) qdpf[p] = qd4[min(p, npieces - 1)];
+    }
+    const size_t si = (size_t)bh * M + tid;
+    const bool own = tid < M;
+    const size_t sc = (size_t)bh * M + min(tid, M - 1);
+    float m_old = mst[sc];
+    float d_old = dst[sc];
+    float vr[kDecKPT];
+#pragma unroll
+    for (int i = 0; i < kDecKPT; ++i) vr[i] = to_f32(V[(size_t)bh * Dv + min(tid + i * kDecNT, Dv - 1)]);
     float4* u4 = reinterpret_cast<float4*>(ust + (size_t)bh * M * Dv);
     float4 ur[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) ur[r] = u4[(size_t)(rg + r * RG) * NT4 + jt];
-    const size_t si = (size_t)bh * M + tid;
-    const bool own = tid < M;
-    const float m_old = own ? mst[si] : 0.0f;
-    const float d_old = own ? dst[si] : 0.0f;
-    const size_t kvoff = (size_t)bh * Dk;
-    for (int j = tid; j < Dk; j += kDecNT) {
-        kv[j] = to_f32(K[kvoff + j]);
-        if (!shared) qd[j] = to_f32(Qdec[kvoff + j]);
-    }
-    for (int j = tid; j < Dv; j += kDecNT) vv[j] = to_f32(V[(size_t)bh * Dv + j]);
-    __syncthreads();
-
-    // scores: thread m dots its Q row (16-byte loads; Q[h] is shared by the batch, L2-resident)
-    constexpr int CH = 16 / sizeof(T);
-    float amax = kNegInf;
-    if (own) {
-        auto dot = [&](const T* row, const float* x) {
-            float acc = 0.0f;
-#pragma unroll 4
-            for (int d0 = 0; d0 < Dk; d0 += CH) {
-                union { uint4 raw; T el[CH]; } qv;
-                qv.raw = *reinterpret_cast<const uint4*>(row + d0);
+    // every load above is issued before the scores wait for k and q (the empty asm
+    // statements keep the compiler from moving that wait, or the dot product, above the
+    // u loads)
+    asm volatile("" ::: "memory");
 #pragma unroll
-                for (int e = 0; e < CH; ++e) acc += to_f32(qv.el[e]) * x[d0 + e];
-            }
-            return acc;
-        };
-        const float s = dot(Q + ((size_t)h * M + tid) * Dk, kv) * scale;
-        const float a = shared ? s : dot(Kdec + ((size_t)h * M + tid) * Dk, qd) * scale;
+    for (int p = 0; p < QPF; ++p) asm volatile("" : "+v"(kpf[p]), "+v"(qpf[p]));
+    asm volatile("" : "+v"(m_old), "+v"(d_old));
+
+    // ---- scores (thread m); the decoder softmax partials of each wave
+    auto dot = [&](u32v4 x, u32v4 y) {
+        union { u32v4 raw; T el[CH]; } xa, ya;
+        xa.raw = x;
+        ya.raw = y;
+        float acc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < CH; ++e) acc += to_f32(xa.el[e]) * to_f32(ya.el[e]);
+        return acc;
+    };
+    float a = kNegInf;
+    if (own) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int p = 0; p < QPF; ++p)
+            if (p < npieces) acc += dot(qpf[p], kpf[p]);
+        for (int p = QPF; p < npieces; ++p) acc += dot(reinterpret_cast<const u32v4*>(qrow)[p], k4[p]);
+        const float s = acc * scale;
+        a = s;
+        if (!shared) {
+            const u32v4* kd4 = reinterpret_cast<const u32v4*>(Kdec + ((size_t)h * M + tid) * Dk);
+            float acc2 = 0.0f;
+            for (int p = 0; p < npieces; ++p) acc2 += dot(kd4[p], p < QPF ? qdpf[p] : qd4[p]);
+            a = acc2 * scale;
+        }
         const MergeScales ts = token_scales(m_old, s);
         const float dn = d_old * ts.sa + ts.sb;
         mst[si] = ts.m_new;
@@ -227,15 +269,27 @@ __global__ __launch_bounds__(kDecNT) void decode_step_fast(
         eta[tid] = ts.sb;
         wts[tid] = dn > 0.0f ? dn : 1.0f;
         av[tid] = a;
-        amax = a;
     }
-    amax = block_max<kDecNT>(amax, red);
-    const float ea = own ? __expf(av[tid] - amax) : 0.0f;
-    const float asum = block_sum<kDecNT>(ea, red);
-    if (own) wts[tid] = ea / (asum * wts[tid]);
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kDecKPT; ++i) vv[min(tid + i * kDecNT, Dv - 1)] = vr[i];   // (past the end: the last value again)
+    const float wmax = wave_max(a);
+    const float wsum = wave_sum(own && wmax != kNegInf ? __expf(a - wmax) : 0.0f);
+    if (lane == 0) {
+        red[2 * wv] = wmax;
+        red[2 * wv + 1] = wsum;
+    }
+    __syncthreads();   // (1) v, the merge scales and the softmax partials visible
+    float amax = kNegInf;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i) amax = fmaxf(amax, red[2 * i]);
+    float asum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NWV; ++i)
+        if (red[2 * i] != kNegInf) asum += red[2 * i + 1] * __expf(red[2 * i] - amax);
+    if (own) wts[tid] = __expf(a - amax) / (asum * wts[tid]);
+    __syncthreads();   // (2) weights visible
 
-    // numerator update and readout from the prefetched rows
+    // ---- numerator update and readout from the prefetched rows
     const float4 vj = reinterpret_cast<const float4*>(vv)[jt];
     float4 y4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -254,7 +308,7 @@ __global__ __launch_bounds__(kDecNT) void decode_step_fast(
         y4.w += w * x.w;
     }
     ypart[rg * NT4 + jt] = y4;
-    __syncthreads();
+    __syncthreads();   // (3) y partials visible
     if (tid < NT4) {
         float4 acc = ypart[tid];
         for (int g2 = 1; g2 < RG; ++g2) {
@@ -298,8 +352,10 @@ extern "C" int flare_decode_step(const void* Q, const void* K, const void* V, co
         const bool pow2 = D4 > 0 && D4 <= kDecNT && (D4 & (D4 - 1)) == 0;
         const int64_t RG = pow2 ? kDecNT / D4 : 0;
         const int64_t rows = RG ? M / RG : 0;
-        const bool aligned = ((uintptr_t)Q & 15) == 0 && (!Kdec || ((uintptr_t)Kdec & 15) == 0);
+        const bool aligned = ((uintptr_t)Q & 15) == 0 && ((uintptr_t)K & 15) == 0 &&
+                             (!Kdec || ((uintptr_t)Kdec & 15) == 0) && (!Qdec || ((uintptr_t)Qdec & 15) == 0);
         if (pow2 && M <= kDecNT && rows * RG == M && (Dk * esz) % 16 == 0 && aligned &&
+            Dk <= kDecKPT * kDecNT && Dv <= kDecKPT * kDecNT &&
             (rows == 1 || rows == 2 || rows == 4 || rows == 8 || rows == 16)) {
 #define FLARE_DEC_FAST(TY, RW, N4)                                                                         \
     hipLaunchKernelGGL((decode_step_fast<TY, RW, N4>), dim3((unsigned)(B * H)), dim3(kDecNT), sm, s,        \
