@@ -15,7 +15,7 @@ import pytest
 import torch
 
 import flare_oracle as O
-from _util import assert_noise_model, assert_parity, assert_state_parity, seeded, to_np
+from _util import assert_noise_model, assert_parity, assert_state_parity, assert_state_rowwise, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -374,6 +374,35 @@ def test_cfg4_decode_bf16():
     assert_parity(y, ref[:, :T], torch.bfloat16, "cfg4 prefill")
     assert_parity(y_dec, ref[:, T:], torch.bfloat16, "cfg4 decode (256 steps)")
     assert_state_parity(st, st_ref, torch.bfloat16, "cfg4 after 256 steps")
+
+
+@pytest.mark.parametrize("M,D,dtype,sep", [(256, 64, torch.bfloat16, False), (256, 64, torch.float16, True),
+                                            (64, 128, torch.bfloat16, True), (128, 32, torch.float32, False),
+                                            (32, 256, torch.bfloat16, False)])
+def test_decode_fast_step_shapes(M, D, dtype, sep):
+    """The fast decode step over its template range (rows of u per thread 1..16, 16-byte
+    pieces of the Q row above and below the 8 it prefetches, separate decoder tensors):
+    a few steps after a prefill, outputs and the in-place state against the oracle (the
+    state row-wise: 40 tokens leave single entries of z cancelling to near zero)."""
+    from causal_flare import flare_autoregressive_decode_triton, flare_autoregressive_prefill_triton
+    _print_case("decode_fast", M, D, dtype, sep)
+    B, T, H, steps = 3, 40, 2, 4
+    q, k, v = seeded(77 + M + D, B, T + steps, H, M, D, D, dtype, q_std=D ** -0.5)
+    g = torch.Generator().manual_seed(78)
+    qd = torch.randn((B, T + steps, H, D), generator=g).to(dtype) if sep else None
+    kd = (torch.randn((H, M, D), generator=g) * D ** -0.5).to(dtype) if sep else None
+    dev = lambda x: None if x is None else x.to(DEV)
+    y, st = flare_autoregressive_prefill_triton(dev(q), dev(k[:, :T]), dev(v[:, :T]),
+                                                Q_dec=dev(None if qd is None else qd[:, :T]), K_dec=dev(kd))
+    ys = []
+    for t in range(T, T + steps):
+        y_t, st = flare_autoregressive_decode_triton(dev(q), dev(k[:, t]), dev(v[:, t]), state=st,
+                                                     Q_dec=dev(None if qd is None else qd[:, t]), K_dec=dev(kd))
+        ys.append(y_t)
+    ref, st_ref = O.ar_recurrent(q, k, v, Q_dec=qd, K_dec=kd, nthreads=16)
+    assert_parity(torch.cat(ys, dim=1), ref[:, T:], dtype, f"decode M={M} D={D} {dtype} sep={sep}")
+    assert_state_rowwise((st["m"], st["d"], st["u"]), (st_ref["m"], st_ref["d"], st_ref["u"]), dtype,
+                         f"decode state M={M} D={D} {dtype} sep={sep}")
 
 
 def test_decode_masked_rows_keep_state():

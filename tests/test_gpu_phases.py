@@ -4,15 +4,8 @@ otherwise) against the fp64 chunk summaries of the oracle (``chunk_summaries``,
 pinned in tests/test_oracle.py), and flare_chunk_prefix against the exclusive
 online-softmax scan of those summaries (reference training.py:914-1103).
 
-Bar for one chunk's summary (stated here, used by every test in this file):
-  max:  |m - m_ref| <= 1e-5                    (natural-log units)
-  den:  |d - d_ref| <= 1e-5 * d_ref
-  num:  compared through z = num / den, row by row (one latent's D_v vector):
-        max_j |z_j - zref_j| <= tol * max_j |zref_j|, tol 2e-3 for bf16/fp16
-        inputs (half a bf16 ulp), 2e-5 for fp32 inputs.
-A chunk sum is dominated by a few tokens, so single entries of z cancel to
-near zero while the row scale is set by the large terms; an element-wise
-relative bar would measure that cancellation, not the kernel."""
+Summaries are compared with the row-wise state bar of tests/_util.py
+(assert_state_rowwise)."""
 import sys
 
 import numpy as np
@@ -20,7 +13,7 @@ import pytest
 import torch
 
 import flare_oracle as O
-from _util import seeded, to_np
+from _util import assert_state_rowwise as assert_summary_parity, seeded, to_np
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -29,22 +22,6 @@ DEV = "cuda"
 def _case(*args):
     print("CASE", *args, flush=True)
     sys.stdout.flush()
-
-
-def assert_summary_parity(got, ref, dtype, what):
-    m, d, u = (to_np(t) for t in got)
-    mr, dr, ur = (np.asarray(t, np.float64) for t in ref)
-    assert np.isfinite(m).all() and np.isfinite(d).all() and np.isfinite(u).all(), f"{what}: non-finite"
-    fin = np.isfinite(mr)
-    assert (np.isneginf(m) == ~fin).all(), f"{what}: empty-summary pattern differs"
-    assert np.abs(m[fin] - mr[fin]).max(initial=0) <= 1e-5, f"{what}: max err {np.abs(m[fin] - mr[fin]).max()}"
-    assert (np.abs(d - dr) <= 1e-5 * dr + 1e-30).all(), f"{what}: den rel err {(np.abs(d - dr) / dr).max()}"
-    pos = dr > 0
-    z, zr = u[pos] / d[pos][..., None], ur[pos] / dr[pos][..., None]
-    tol = 2e-5 if dtype == torch.float32 else 2e-3
-    err = (np.abs(z - zr).max(-1) / np.abs(zr).max(-1).clip(1e-30)).max(initial=0)
-    assert err <= tol, f"{what}: z row-norm-wise err {err:.3e} > {tol}"
-    return err
 
 
 def _prepare(q, k, v, chunk, scale):
