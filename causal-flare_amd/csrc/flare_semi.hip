@@ -219,10 +219,14 @@ static int semi_forward_impl(const void* Q, const void* K, const void* V, const 
         // Chunks of whole blocks: prefix of every chunk from phases 1-2, then the
         // block-causal MFMA readout.  The summaries fit in the workspace since
         // chunks are never shorter than blocks.
-        // ~512 chunk workgroups (one round at two per compute unit), whole blocks each:
-        // measured on config 5 (B*H = 32), 2048 / 1024 / 512 / 256 workgroups take
-        // 151 / 126 / 119 / 168 us, the shorter chunks paying in summary traffic
-        const int64_t target = (512 + B * H - 1) / (B * H);
+        // One round of chunk workgroups, whole blocks each: ~512 (two per compute unit),
+        // or ~768 where three fit (M = 128, Dv = 64 with the block's softmax in LDS for
+        // blocks up to 64, or in the workspace: <= 168 VGPRs and <= 53 KiB of LDS).
+        // Measured on config 5 (B*H = 32) at two per CU, 2048 / 1024 / 512 / 256
+        // workgroups take 151 / 126 / 119 / 168 us, the shorter chunks paying in summary
+        // traffic; three per CU over 704 workgroups: 104 us.
+        const bool three = M == 128 && Dv == 64 && block != 128;
+        const int64_t target = ((three ? 768 : 512) + B * H - 1) / (B * H);
         int64_t chunk = (N + target - 1) / target;
         if (chunk > 2048) chunk = 2048;
         chunk = ((chunk + block - 1) / block) * block;

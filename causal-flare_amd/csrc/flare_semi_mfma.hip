@@ -49,7 +49,10 @@ struct SemiLayout {
 // LDS one subtile at a time for the readout; the block is nsub = block / 32
 // subtiles at run time and NSUB is unused.
 template <int M, int D, int NW, int NSUB, bool SEP, bool GA, bool F16>
-__global__ __launch_bounds__(64 * NW, 1) void semi_output_mfma(
+// (at least 3 workgroups per CU where the registers allow it: the 128 x 64 instances with
+// the block's softmax in LDS for blocks up to 64 fit in 168 VGPRs; the compiler keeps the
+// larger instances at their own count)
+__global__ __launch_bounds__(64 * NW, 3) void semi_output_mfma(
     const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N, int H,
     float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype, float* __restrict__ lse_dec,
