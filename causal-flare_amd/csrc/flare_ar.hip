@@ -126,7 +126,7 @@ __global__ __launch_bounds__(kNT) void chunk_prepare_kernel(
 // before their serial merges run, so one memory latency covers kScanBatch
 // merges.
 // ---------------------------------------------------------------------------
-constexpr int kScanBatch = 8;
+constexpr int kScanBatch = 16;   // chunk summaries loaded before the first merge (config 3 has 16 chunks)
 
 __global__ __launch_bounds__(256) void chunk_prefix_kernel(
     float* __restrict__ cmax, float* __restrict__ cden, float* __restrict__ cnum, int NC, int M,
