@@ -176,13 +176,13 @@ __global__ __launch_bounds__(kDecNT) void decode_step_fast(
     constexpr int CH = 16 / sizeof(T);   // Q elements per 16-byte load
     constexpr int QPF = 8;               // 16-byte pieces of the Q row prefetched
     extern __shared__ float smem[];
-    float* vv = smem + 2 * Dk;        // [Dv]
+    float* vv = smem;                 // [Dv]
     float* av = vv + Dv;              // [M] decoder scores
     float* gam = av + M;              // [M]
     float* eta = gam + M;             // [M]
     float* wts = eta + M;             // [M]
     float* red = wts + M;             // [2 NWV] per-wave (max, sum) of the decoder softmax
-    float4* ypart = reinterpret_cast<float4*>(smem + ((2 * Dk + Dv + 4 * M + 8 + 3) & ~3));  // [RG][NT4]
+    float4* ypart = reinterpret_cast<float4*>(smem + ((Dv + 4 * M + 8 + 3) & ~3));  // [RG][NT4]
 
     const int bh = blockIdx.x;
     const int b = bh / H, h = bh % H;
