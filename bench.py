@@ -199,87 +199,106 @@ def bench_decode(torch, flare, steps=256):
             "alg_bytes_per_step": bytes_step,
             "note": "graph replay of 256 back-to-back steps; per-step time includes launch gaps",
         },
-        "final_state": {kk: vv.cpu() for kk, vv in st.items()},
+        # the prefill state (before any decode step): the CPU baseline's decode starts from it
+        "prefill_state": {kk: vv.cpu() for kk, vv in base.items()},
     }
 
 
-def bench_others(torch, flare):
-    """Informational timings of configs 2 and 5 (their parity is tested, they are not the headline)."""
-    def inputs(seed, B, N, H, M, D):
-        torch.manual_seed(seed)
-        q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16).cuda()
-        return q, torch.randn(B, N, H, D).to(torch.bfloat16).cuda(), torch.randn(B, N, H, D).to(torch.bfloat16).cuda()
+def _inputs(torch, seed, B, N, H, M, D):
+    torch.manual_seed(seed)
+    q = (torch.randn(H, M, D) / math.sqrt(D)).to(torch.bfloat16).cuda()
+    return q, torch.randn(B, N, H, D).to(torch.bfloat16).cuda(), torch.randn(B, N, H, D).to(torch.bfloat16).cuda()
 
-    def timed(fn, reps=20, warm=1):
-        for _ in range(warm):
-            fn()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            fn()
-        torch.cuda.synchronize()
-        return (time.perf_counter() - t0) / reps
 
-    def replayed(fn, reps=20):
-        """`reps` calls captured once in a HIP graph and replayed back to back (as the
-        prefill line): the kernels of the eager calls without the host's enqueue time.
-        Every replayed output must equal the eager one bit for bit, else None."""
-        first = lambda r: r[0] if isinstance(r, tuple) else r
-        try:
-            ref = first(fn()).clone()
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                for _ in range(2):
-                    fn()
-            torch.cuda.current_stream().wait_stream(side)
-            graph = torch.cuda.CUDAGraph()
-            outs = []
-            with torch.cuda.graph(graph):
-                for _ in range(reps):
-                    outs.append(first(fn()))
+def _timed(torch, fn, reps=20, warm=1):
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps
+
+
+def _replayed(torch, fn, reps=20):
+    """`reps` calls captured once in a HIP graph and replayed back to back (as the
+    prefill line): the kernels of the eager calls without the host's enqueue time.
+    Every replayed output must equal the eager one bit for bit, else None."""
+    first = lambda r: r[0] if isinstance(r, tuple) else r
+    try:
+        ref = first(fn()).clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        outs = []
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                outs.append(first(fn()))
+        graph.replay()
+        torch.cuda.synchronize()
+        if not all(bool(torch.equal(o, ref)) for o in outs):
+            return None
+        best = None
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
             graph.replay()
             torch.cuda.synchronize()
-            if not all(bool(torch.equal(o, ref)) for o in outs):
-                return None
-            best = None
-            for _ in range(3):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                graph.replay()
-                torch.cuda.synchronize()
-                dt = (time.perf_counter() - t0) / reps
-                best = dt if best is None else min(best, dt)
-            del graph, outs
-            return best
-        except Exception as exc:   # capture unavailable: the eager loop stands
-            print(f"graph replay unavailable: {exc}", file=sys.stderr)
-            return None
+            dt = (time.perf_counter() - t0) / reps
+            best = dt if best is None else min(best, dt)
+        del graph, outs
+        return best
+    except Exception as exc:   # capture unavailable: the eager loop stands
+        print(f"graph replay unavailable: {exc}", file=sys.stderr)
+        return None
 
-    out = {}
-    def hbm_roofline(B, N, H, D, dt):
-        # algorithmic bytes: K and V read, Y written, bf16: 6 D bytes per token-head
-        alg = 6.0 * D * B * N * H
-        gbs = alg / dt / 1e9
-        return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": gbs / PEAK_HBM_GBS, "alg_bytes": alg, "scope": "whole forward (all kernels)"}
 
-    # forward timings: graph replay (the kernels back to back) where its outputs are
-    # bit-identical to the eager calls', with the eager API loop's host-clock time beside it
-    for name, seed, (B, N), fn_of in (
-            ("config2_prefill", 1, (4, 4096), lambda q, k, v: lambda: flare.flare_autoregressive_triton(q, k, v)),
-            ("config5_semi_ar", 4, (2, 8192),
-             lambda q, k, v: lambda: flare.flare_semi_autoregressive_trition(q, k, v, block_size=64, chunk_size=64))):
-        q, k, v = inputs(seed, B, N, 16, 128, 64)
-        fn = fn_of(q, k, v)
-        dt_eager = timed(fn)
-        dt_graph = replayed(fn)
-        dt = dt_graph if dt_graph is not None else dt_eager
-        out[name] = {"ms": dt * 1e3, "tok_s": B * N / dt,
-                     "tflops_alg": 6 * 128 * 64 * B * N * 16 / dt / 1e12,
-                     "roofline": hbm_roofline(B, N, 16, 64, dt),
-                     "timing": "graph replay (bit-identical to eager)" if dt_graph is not None else "eager API loop",
-                     "ms_eager_api_loop": dt_eager * 1e3}
+def _hbm_roofline(B, N, H, D, dt):
+    # algorithmic bytes: K and V read, Y written, bf16: 6 D bytes per token-head
+    alg = 6.0 * D * B * N * H
+    gbs = alg / dt / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": gbs / PEAK_HBM_GBS, "alg_bytes": alg, "scope": "whole forward (all kernels)"}
+
+
+# configs 2 and 5: (seed, B, N) and the forward call
+FWD_CONFIGS = {
+    "config2_prefill": (1, 4, 4096, lambda flare, q, k, v: lambda: flare.flare_autoregressive_triton(q, k, v)),
+    "config5_semi_ar": (4, 2, 8192, lambda flare, q, k, v: lambda: flare.flare_semi_autoregressive_trition(
+        q, k, v, block_size=64, chunk_size=64)),
+}
+
+
+def bench_forward_config(torch, flare, name):
+    """One of configs 2 / 5 (H=16, M=128, D=64, bf16): graph replay (the kernels back to
+    back) where its outputs are bit-identical to the eager calls', with the eager API
+    loop's host-clock time beside it."""
+    seed, B, N, fn_of = FWD_CONFIGS[name]
+    q, k, v = _inputs(torch, seed, B, N, 16, 128, 64)
+    fn = fn_of(flare, q, k, v)
+    dt_eager = _timed(torch, fn)
+    dt_graph = _replayed(torch, fn)
+    dt = dt_graph if dt_graph is not None else dt_eager
+    return {"ms": dt * 1e3, "tok_s": B * N / dt,
+            "tflops_alg": 6 * 128 * 64 * B * N * 16 / dt / 1e12,
+            "roofline": _hbm_roofline(B, N, 16, 64, dt),
+            "timing": "graph replay (bit-identical to eager)" if dt_graph is not None else "eager API loop",
+            "ms_eager_api_loop": dt_eager * 1e3}
+
+
+def bench_others(torch, flare):
+    """Informational timings of configs 2 and 5 (their parity is tested, they are not the headline),
+    config 3 with score jumps, and the backward of configs 2, 3 and 5."""
+    inputs = lambda *a: _inputs(torch, *a)
+    timed = lambda fn, reps=20, warm=1: _timed(torch, fn, reps, warm)
+    replayed = lambda fn, reps=20: _replayed(torch, fn, reps)
+    out = {name: bench_forward_config(torch, flare, name) for name in FWD_CONFIGS}
+    out["config3_score_jump"] = bench_score_jump(torch, flare, replayed, timed)
     # backward (autograd through flare_autoregressive_triton) on configs 2 and 3
     for name, shape, reps in (("config2_backward", (4, 4096, 16, 128, 64), 5),
                               ("config3_backward", (1, 65536, 16, 256, 128), 3)):
@@ -296,6 +315,47 @@ def bench_others(torch, flare):
     dt = timed(lambda: y.backward(dy, retain_graph=True), 5, warm=2)
     out["config5_semi_ar_backward"] = {"ms": dt * 1e3, "tok_s": 2 * 8192 / dt}
     return out
+
+
+def _jump_keys(torch, q, k, tokens, lat, nats, scale):
+    """Key outliers (as the GPU parity tests build them): at tokens[i] the key of every
+    head points along the sum of the latent directions `lat`, scaled so that the
+    smallest of those latents' scores is nats[i] -- a reference jump far past the fp32
+    range within one 32-token subtile."""
+    qf = q.float()
+    for h in range(q.shape[0]):
+        u = sum(qf[h, m] / qf[h, m].norm() for m in lat)
+        s = torch.stack([qf[h, m] @ u for m in lat]).min() * scale
+        for t, n in zip(tokens, nats):
+            k[:, t, h] = (u * (n / float(s))).to(k.dtype)
+    return k
+
+
+def bench_score_jump(torch, flare, replayed, timed):
+    """Config 3 with score jumps: one outlier key in one chunk, and one in every chunk
+    (rising, so each one jumps).  The output kernel flags the jumping subtile and the
+    tokenwise fp32 kernel replays that subtile only; the cost is the clean forward's
+    plus the replay."""
+    dev = torch.device("cuda:0")
+    (B, N, H, M, D), q, k, v = _cfg3_inputs(torch, dev)
+    chunk = int(flare._lib.lib().flare_ar_default_chunk(B, N, H, M, D))
+    lat = list(range(0, M, M // 8))
+    res = {"chunk": chunk}
+    cases = (("clean", [], []),
+             ("one_chunk", [5 * chunk + 1000 + 17], [150.0]),
+             ("every_chunk", [c * chunk + 1000 + 17 for c in range(N // chunk)],
+              [150.0 * (c + 1) for c in range(N // chunk)]))
+    for name, toks, nats in cases:
+        kj = _jump_keys(torch, q, k.clone(), toks, lat, nats, D ** -0.5) if toks else k
+        fn = lambda: flare.flare_autoregressive_triton(q, kj, v)
+        dt = replayed(fn)
+        how = "graph replay (bit-identical to eager)"
+        if dt is None:
+            dt, how = timed(fn), "eager API loop"
+        res[name] = {"ms": dt * 1e3, "outliers": len(toks), "timing": how}
+    for name in ("one_chunk", "every_chunk"):
+        res[name]["vs_clean"] = res[name]["ms"] / res["clean"]["ms"]
+    return res
 
 
 def measured_traffic(fname, kernel):
@@ -370,7 +430,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=("prefill", "decode"), default=None,
+    ap.add_argument("--only", choices=("prefill", "decode", "config2", "config5", "jump"), default=None,
                     help="run one workload alone (profiler passes); the JSON line then holds that part only")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="finish with a plain 1 GiB device-to-device copy (HBM counter calibration)")
@@ -383,9 +443,16 @@ def main():
     import causal_flare as flare
 
     if args.only is not None:
-        part = (bench_prefill(torch, flare, args.steps, args.warmup) if args.only == "prefill"
-                else bench_decode(torch, flare))
-        part.pop("final_state", None)
+        if args.only == "prefill":
+            part = bench_prefill(torch, flare, args.steps, args.warmup)
+        elif args.only == "decode":
+            part = bench_decode(torch, flare)
+        elif args.only == "jump":
+            part = bench_score_jump(torch, flare, lambda fn, reps=20: _replayed(torch, fn, reps),
+                                    lambda fn: _timed(torch, fn))
+        else:
+            part = bench_forward_config(torch, flare, {"config2": "config2_prefill", "config5": "config5_semi_ar"}[args.only])
+        part.pop("prefill_state", None)
         print(json.dumps({"only": args.only, **part}))
         if args.calibration_copy:
             calibration_copy(torch)
@@ -393,7 +460,7 @@ def main():
     pre = bench_prefill(torch, flare, args.steps, args.warmup)
     dec = None if args.no_decode else bench_decode(torch, flare)
     others = None if args.no_decode else bench_others(torch, flare)
-    dstate = dec.pop("final_state", None) if dec else None
+    dstate = dec.pop("prefill_state", None) if dec else None
     cpu = None if args.no_cpu else cpu_baseline(dstate)
     out = {
         "metric": "prefill tok/s (N=64k) & decode tok/s (B=64) on 1 MI355X; % of roofline",

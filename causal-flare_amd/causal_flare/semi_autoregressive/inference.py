@@ -5,10 +5,13 @@ The reference ships these entry points as stubs that raise
 Here they are implemented with the same names and keyword arguments, plus a
 ``block_size`` keyword:
 
-* The tokens of a call form whole blocks of ``block_size`` tokens (default: the
-  whole call is one block).  Every token of a block reads the latent state after
-  its whole block, as in the block-causal forward
-  (``semi_autoregressive/reference.py:560-597``).
+* The tokens of a prefill form whole blocks of ``block_size`` tokens.  As in
+  ``flare_semi_autoregressive_trition`` (semi ``training.py:4082-4088``),
+  ``block_size`` is required: a prefill without it raises ``ValueError`` (a
+  default of one block per call would let every prompt token read later tokens).
+  Every token of a block reads the latent state after its whole block, as in the
+  block-causal forward (``semi_autoregressive/reference.py:560-597``).  A block
+  decode step is one block: the ``T`` tokens of the call.
 * The state is the autoregressive cache ``{"m": [B,H,M], "d": [B,H,M],
   "u": [B,H,M,Dv]}`` (fp32; ``autoregressive/inference.py:66-120``): it stands for
   every earlier block, so a semi-AR prefill can continue an autoregressive one and
@@ -37,7 +40,9 @@ from ..autoregressive.inference import _canonicalize_flare_state, flare_autoregr
 def _semi_cached(Q, K, V, *, state, scale, Q_dec, K_dec, block_size, name):
     """One launch of flare_semi_ar_forward_state; returns (Y, canonical input state, state after)."""
     B, N, H, M, D_score, D_value = validate_flare_qkv_layouts(Q, K, V, name=name)
-    block = N if block_size is None else int(block_size)
+    if block_size is None:
+        raise ValueError(f"{name} requires block_size (tokens per block).")
+    block = int(block_size)
     if block <= 0 or block % 16 != 0:
         raise ValueError(f"{name} requires block_size to be a positive multiple of 16. Got block_size={block}.")
     if N % block != 0:
@@ -104,7 +109,7 @@ def flare_semi_autoregressive_decode_trition(Q, K, V, *, state=None, scale=None,
         D = K.shape[-1]
         return flare_autoregressive_decode_triton(Q, K, V, state=state, scale=_resolve_attn_scale(scale, D),
                                                   Q_dec=Q_dec, K_dec=K_dec)
-    Y, st, out = _semi_cached(Q, K, V, state=state, scale=scale, Q_dec=Q_dec, K_dec=K_dec, block_size=None,
+    Y, st, out = _semi_cached(Q, K, V, state=state, scale=scale, Q_dec=Q_dec, K_dec=K_dec, block_size=K.shape[1],
                               name=name)
     if st is None:
         return Y, out
@@ -115,9 +120,10 @@ def flare_semi_autoregressive_decode_trition(Q, K, V, *, state=None, scale=None,
 
 class SemiAutoRegressivePrefillFLARE(autograd.Function):
     @staticmethod
-    def forward(ctx, Q, K, V, state=None, scale=None, attention_mask=None, Q_dec=None, K_dec=None):
+    def forward(ctx, Q, K, V, state=None, scale=None, attention_mask=None, Q_dec=None, K_dec=None, block_size=None):
         return flare_semi_autoregressive_prefill_trition(Q, K, V, state=state, scale=scale,
-                                                         attention_mask=attention_mask, Q_dec=Q_dec, K_dec=K_dec)
+                                                         attention_mask=attention_mask, Q_dec=Q_dec, K_dec=K_dec,
+                                                         block_size=block_size)
 
     @staticmethod
     def backward(ctx, dY, dState=None):

@@ -206,10 +206,16 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     int out_dtype, float* __restrict__ lse_dec, const int32_t* __restrict__ tmask, const int* __restrict__ only,
     float power) {
     // only: when given, [B*H, NC] flags; chunks whose flag is 0 are left alone (the
-    // tokenwise replay of the chunks an MFMA output kernel could not resolve).
+    // tokenwise replay of the chunks an MFMA output kernel could not resolve).  A
+    // narrow flag replays 32-token subtiles j1 .. j2 of the chunk only, from the
+    // state at subtile j1's start (which then stands in the chunk's prefix slot).
     // power > 0: the stablemax encoder (den += stablemax_transform(s), no rescale);
     // the decoder weights stay a softmax over the latents.
-    if (only != nullptr && only[(size_t)blockIdx.y * gridDim.x + blockIdx.x] == 0) return;
+    int flag = kRedoWhole;
+    if (only != nullptr) {
+        flag = only[(size_t)blockIdx.y * gridDim.x + blockIdx.x];
+        if (flag == 0) return;
+    }
     extern __shared__ float smem[];
     const int R = kNT / DT;
     float* k_tile = smem;                                   // [TT][Dk]
@@ -244,8 +250,12 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
         U[r] = m < M ? pnum[(pbase + m) * Dv + dt0 + col] : 0.0f;
     }
 
-    const int t_begin = c * chunk;
-    const int t_end = min(N, t_begin + chunk);
+    int t_begin = c * chunk;
+    int t_end = min(N, t_begin + chunk);
+    if (redo_is_narrow(flag)) {
+        t_end = min(t_end, t_begin + 32 * (redo_j2(flag) + 1));
+        t_begin += 32 * redo_j1(flag);
+    }
     for (int t0 = t_begin; t0 < t_end; t0 += TT) {
         const int nt = min(TT, t_end - t0);
         __syncthreads();
@@ -260,26 +270,47 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
             v_tile[e] = i < nt ? to_f32(V[(((size_t)b * N + t0 + i) * H + h) * Dv + dt0 + d]) : 0.0f;
         }
         __syncthreads();
-        for (int p = tid; p < nt * M; p += kNT) {
-            const int i = p / M, m = p % M;
-            if (tmask != nullptr && tmask[(size_t)b * N + t0 + i] == 0) {
-                // a masked token: s = a = -inf leaves the state unchanged and gives y = 0
-                // (inference.py:395-397, 476-478)
-                s_tile[p] = kNegInf;
-                if (!shared) a_tile[p] = kNegInf;
-                continue;
-            }
+        // Scores of the tile: thread m reads its latent's Q (and K_dec) row once per tile, four
+        // columns at a time, against the TT token rows in LDS (the same address in every lane:
+        // broadcast reads); the sums run over d in order, per token.
+        for (int m = tid; m < M; m += kNT) {
             const T* qrow = q_h + (size_t)m * Dk;
-            const float* kr = k_tile + i * Dk;
-            float acc = 0.0f;
-            for (int d = 0; d < Dk; ++d) acc += kr[d] * to_f32(qrow[d]);
-            s_tile[p] = acc * scale;
-            if (!shared) {
-                const T* krow = kd_h + (size_t)m * Dk;
-                const float* qr = qd_tile + i * Dk;
-                float acc2 = 0.0f;
-                for (int d = 0; d < Dk; ++d) acc2 += qr[d] * to_f32(krow[d]);
-                a_tile[p] = acc2 * scale;
+            const T* kdrow = kd_h + (size_t)m * Dk;
+            float acc[16], acc2[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[i] = acc2[i] = 0.0f;
+            auto cols = [&](int d, int nd) {
+                float qv[4], kv[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[e] = e < nd ? to_f32(qrow[d + e]) : 0.0f;
+                    kv[e] = (!shared && e < nd) ? to_f32(kdrow[d + e]) : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    if (i < nt) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if (e < nd) {
+                                acc[i] += k_tile[i * Dk + d + e] * qv[e];
+                                if (!shared) acc2[i] += qd_tile[i * Dk + d + e] * kv[e];
+                            }
+                        }
+                    }
+                }
+            };
+            int d = 0;
+            for (; d + 4 <= Dk; d += 4) cols(d, 4);
+            if (d < Dk) cols(d, Dk - d);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                if (i < nt) {
+                    // a masked token: s = a = -inf leaves the state unchanged and gives y = 0
+                    // (inference.py:395-397, 476-478)
+                    const bool masked = tmask != nullptr && tmask[(size_t)b * N + t0 + i] == 0;
+                    s_tile[i * M + m] = masked ? kNegInf : acc[i] * scale;
+                    if (!shared) a_tile[i * M + m] = masked ? kNegInf : acc2[i] * scale;
+                }
             }
         }
         __syncthreads();
@@ -403,7 +434,10 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                          int64_t Dk, int64_t Dv, float scale, int64_t chunk, const float* pmax,
                          const float* pden, const float* pnum, void* Y, int out_dtype,
                          float* lse_dec, hipStream_t stream, const int32_t* tmask = nullptr,
-                         void* alpha_ws = nullptr, int* redo = nullptr, float power = 0.0f) {
+                         void* alpha_ws = nullptr, int* redo = nullptr, float power = 0.0f,
+                         bool record = false) {
+    // record: pmax / pden / pnum are this call's own scratch (the forward's workspace), so
+    // the output kernel may overwrite a chunk's slot with a replay record
     const bool shared = Qdec == nullptr && Kdec == nullptr;
     // A launch of the scalar kernel restricted to the chunks flagged in `only` (or all).
     auto scalar = [&](const int* only) -> int {
@@ -445,7 +479,7 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
         int rc = -1;
         if (mfma_output_supported(dtype, out_dtype, shared, M, Dk, Dv) && (tmask == nullptr || output_pc_enabled())) {
             rc = launch_output_mfma(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype,
-                                    tmask, dtype == FLARE_F16, redo, stream);
+                                    tmask, dtype == FLARE_F16, redo, stream, record);
         } else if (!shared && alpha_ws != nullptr && output_pc_enabled() &&
                    mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
             // separate decoder tensors: the decoder softmax first (alpha_ws, [B*H, N, M] fp16),
@@ -540,13 +574,20 @@ int flare_chunk_output(const void* Q, const void* K, const void* V, const void* 
     FLARE_REQUIRE(B > 0 && N > 0 && H > 0 && M > 0 && Dk > 0 && Dv > 0 && chunk > 0,
                   "chunk_output: sizes must be positive");
     // the MFMA output kernels report the chunks they hand back to the scalar kernel in
-    // [B*H, NC] flags: a stream-ordered allocation of them for this call
+    // [B*H, NC] flags: a stream-ordered allocation of them for this call.  If it fails the
+    // call fails (the MFMA kernels need the flags; there is no silent fallback).  The
+    // prefix arrays are the caller's, so replays here always cover whole chunks.
     hipStream_t st = (hipStream_t)stream;
     int* redo = nullptr;
     const int64_t NC = (N + chunk - 1) / chunk;
-    if (lse_dec == nullptr && hipMallocAsync((void**)&redo, (size_t)B * H * NC * sizeof(int), st) != hipSuccess) {
-        (void)hipGetLastError();
-        redo = nullptr;     // the scalar kernels alone
+    if (lse_dec == nullptr) {
+        const hipError_t e = hipMallocAsync((void**)&redo, (size_t)B * H * NC * sizeof(int), st);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            set_error("chunk_output: hipMallocAsync of %lld redo flags failed: %s", (long long)(B * H * NC),
+                      hipGetErrorString(e));
+            return FLARE_ERR_LAUNCH;
+        }
     }
     const int rc = launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, prefix_max,
                                  prefix_den, prefix_num, Y, out_dtype, lse_dec, st, nullptr, nullptr, redo);
@@ -686,7 +727,7 @@ int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const v
     rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, m0, d0, u0, m_fin, d_fin, u_fin, s);
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden,
-                         cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws, redo);
+                         cnum, Y, out_dtype, nullptr, s, token_mask, alpha_ws, redo, 0.0f, true);
 }
 
 // ---------------------------------------------------------------------------
@@ -703,27 +744,42 @@ constexpr size_t kScratchBytes = (size_t)64 << 20;
 __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
-static void* g_scratch_ptr[kMaxDevices] = {};
+// Per device: the device address of `scratch`, and the order of the calls that use it
+// (an event recorded after the last call's kernels, on the stream they ran on).
+struct ScratchSlot {
+    void* ptr = nullptr;
+    hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;
+    bool pending = false;
+};
+static ScratchSlot g_scratch[kMaxDevices];
+// Held from the device lookup to the end of a call's enqueue: calls from several host
+// threads enqueue one after the other, so the event order below is the call order.
 static std::mutex g_scratch_mu;
 
-// Device address of `scratch` on the current device, looked up once per device.
-static int scratch_ptr(void** out) {
+// The current device's slot, set up once per device (symbol address, order event).
+static int scratch_slot(ScratchSlot** out) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
         set_error("ar_forward_noalloc: no usable current device");
         return FLARE_ERR_LAUNCH;
     }
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (g_scratch_ptr[dev] == nullptr) {
+    ScratchSlot& sl = g_scratch[dev];
+    if (sl.ptr == nullptr) {
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || p == nullptr) {
             set_error("ar_forward_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
             return FLARE_ERR_LAUNCH;
         }
-        g_scratch_ptr[dev] = p;
+        e = hipEventCreateWithFlags(&sl.done, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            set_error("ar_forward_noalloc: hipEventCreateWithFlags failed: %s", hipGetErrorString(e));
+            return FLARE_ERR_LAUNCH;
+        }
+        sl.ptr = p;
     }
-    *out = g_scratch_ptr[dev];
+    *out = &sl;
     return FLARE_OK;
 }
 }  // namespace flare
@@ -751,11 +807,28 @@ int flare_ar_forward_noalloc(const void* Q, const void* K, const void* V, const 
         const size_t sep = flare_ar_forward_workspace_size_sep(B, N, H, M, Dv, chunk);
         if (sep <= kScratchBytes) bytes = sep;
     }
-    void* ws = nullptr;
-    const int rc = scratch_ptr(&ws);
+    std::lock_guard<std::mutex> lock(flare::g_scratch_mu);
+    flare::ScratchSlot* sl = nullptr;
+    int rc = flare::scratch_slot(&sl);
     if (rc) return rc;
-    return flare_ar_forward_masked(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, m0, d0, u0,
-                                   m_fin, d_fin, u_fin, Y, out_dtype, token_mask, ws, bytes, stream);
+    // Calls share the scratch array: one enqueued on another stream than the previous
+    // call first waits for that call's kernels (same-stream calls are in stream order).
+    // Under graph capture the order is the graph's; a replay that overlaps a call on
+    // another stream is not ordered by this.
+    hipStream_t st = (hipStream_t)stream;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    FLARE_REQUIRE(hipStreamIsCapturing(st, &cap) == hipSuccess, "ar_forward_noalloc: hipStreamIsCapturing failed");
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    if (eager && sl->pending && sl->last != st)
+        FLARE_REQUIRE(hipStreamWaitEvent(st, sl->done, 0) == hipSuccess, "ar_forward_noalloc: hipStreamWaitEvent failed");
+    rc = flare_ar_forward_masked(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, m0, d0, u0, m_fin,
+                                 d_fin, u_fin, Y, out_dtype, token_mask, sl->ptr, bytes, stream);
+    if (rc == FLARE_OK && eager) {
+        FLARE_REQUIRE(hipEventRecord(sl->done, st) == hipSuccess, "ar_forward_noalloc: hipEventRecord failed");
+        sl->last = st;
+        sl->pending = true;
+    }
+    return rc;
 }
 
 }  // extern "C"

@@ -810,10 +810,10 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
-                       bool f16in, int* redo, hipStream_t stream) {
+                       bool f16in, int* redo, hipStream_t stream, bool record) {
     if (output_pc_enabled())
         return launch_output_pc(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, nullptr,
-                                f16in, redo, stream);
+                                f16in, redo, stream, record);
     FLARE_REQUIRE(!f16in, "chunk_output_mfma: fp16 inputs need the producer/consumer kernel");
     FLARE_REQUIRE(tmask == nullptr, "chunk_output_mfma: token masks need the producer/consumer kernel");
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_mfma: chunk must be a multiple of %d", T);

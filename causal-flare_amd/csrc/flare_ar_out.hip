@@ -161,10 +161,14 @@ struct KDma {
 template <int M, int D, bool SEP, bool F16>
 __global__ __launch_bounds__(64 * (M / 64 + D / 32), (512 / (64 * (M / 64 + D / 32))) > 0 ? 512 / (64 * (M / 64 + D / 32)) : 1)
 void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N,
-                     int H, float scale2, int chunk, const float* __restrict__ pmax, const float* __restrict__ pden,
-                     const float* __restrict__ pnum, void* __restrict__ Y, int out_dtype,
+                     int H, float scale2, int chunk, const float* pmax, const float* pden,
+                     const float* pnum, void* __restrict__ Y, int out_dtype,
                      const int32_t* __restrict__ tmask, const f16* __restrict__ alpha, int* __restrict__ redo,
-                     int spin_limit) {
+                     int spin_limit, int record) {
+    // record (shared decoder weights only): the prefix slot of this chunk (pmax, pden,
+    // pnum, read once at the start) may be overwritten with the state at the start of
+    // the first subtile whose reference jumped, so that the tokenwise fp32 replay only
+    // covers the flagged subtiles (a narrow redo flag) instead of the whole chunk.
     using L = TrLayout<M, D>;
     // K rows of the even / odd subtiles (swizzled, filled by DMA)
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
@@ -178,7 +182,13 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     __shared__ __attribute__((aligned(16))) float d0l[2][M];                  // den at the subtile start
     __shared__ int movedl[2][L::NP];    // bit 0: a reference moved; bit 1: general path
     __shared__ int psync;               // producer arrivals (monotonic)
-    __shared__ int redol;               // a reference jumped past kJumpMax
+    __shared__ int redol;               // separate decoder: a reference jumped past kJumpMax
+    // shared weights: subtile j + 1 in jumpl[j & 1] when a reference jumped past kJumpMax
+    // in subtile j (read by the other producers after their meeting); the references and
+    // dens at the start of such a subtile (rare: written only then)
+    __shared__ int jumpl[2];
+    __shared__ float rsvl[SEP ? 1 : 2][SEP ? 1 : M];
+    __shared__ float dsvl[SEP ? 1 : 2][SEP ? 1 : M];
 
     const int c_idx = blockIdx.x, bh = blockIdx.y;
     const int nchunks = gridDim.x;
@@ -194,7 +204,13 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     if (tid == 0) {
         psync = 0;
         redol = 0;
+        jumpl[0] = jumpl[1] = 0;
     }
+    // the replay decision, taken by every consumer wave alike from the subtile flags
+    // (movedl bit 2: a reference jumped, bit 3: a producer meeting gave up):
+    // the whole chunk (a meeting gave up before any record), else subtiles rj1 .. rj2
+    bool rwhole = false;
+    int rj1 = -1, rj2 = -1;
 
     if (w < L::NP) {
         // =========================== producer ===========================
@@ -246,16 +262,35 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         // producer runs the same subtiles, so the count always arrives; past spin_limit
         // sleeps the wave gives up, counts a fault and flags the chunk for the tokenwise
         // replay, which rewrites its outputs.
-        auto meet = [&](int n) {
+        auto meet = [&](int n, bool& gave_up) {
             if (lane == 0) __hip_atomic_fetch_add(&psync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             int spins = 0;
             while (__hip_atomic_load(&psync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < L::NP * n) {
                 if (spins++ >= spin_limit) {
-                    redol = 1;
+                    gave_up = true;
                     if (lane == 0) atomicAdd(&g_meet_timeouts_tr, 1u);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
+            }
+        };
+        // references and dens at a subtile's start to rsvl / dsvl (lanes c = 0..3 store rows r = c)
+        // (one exec-masked store per latent: lane c = r of each row writes latent r; lane-derived
+        // values from an opaque copy of the lane id, so that none becomes a loop invariant)
+        auto stash = [&](int bf) {
+            if constexpr (!SEP) {
+                int ls = lane;
+                asm volatile("" : "+v"(ls));
+                const int cs = ls & 15;
+                const int m0 = mp0 + 4 * (ls >> 4);
+#pragma unroll
+                for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (cs == r) {
+                            rsvl[bf][m0 + 16 * mi + r] = R[mi][r];
+                            dsvl[bf][m0 + 16 * mi + r] = dn[mi][r];
+                        }
             }
         };
         KDma<D, 64 * L::NP> kdma;
@@ -399,7 +434,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 exps();
                 dnbig |= rinf;   // some latent has no reference yet (fully masked so far): general path
                 bool moved = __any((emax > L::kLazyE) | dnbig);
+                bool jumped = false, gave_up = false;   // (flags of this subtile, wave-uniform)
                 if (moved) {
+                    stash(buf);     // the state before the move, for a replay record
                     // every latent of the wave had den 0 so far (a chunk with no earlier tokens)
                     float gam[L::MTP][4];
                     bool jump = false;
@@ -436,7 +473,11 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             R[mi][r] = Rn;
                             dn[mi][r] *= gam[mi][r];     // E is recomputed on the general path
                         }
-                    if (jump) redol = 1;
+                    if (jump) {
+                        if constexpr (SEP) redol = 1;
+                        else jumpl[buf] = j + 1;
+                    }
+                    jumped = __any(jump);
                     refresh();
                     rinf = false;
 #pragma unroll
@@ -513,7 +554,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                         lsep[buf][w][c] = float2{ref[0], part[0]};
                         lsep[buf][w][16 + c] = float2{ref[1], part[1]};
                     }
-                    meet(j + 1);
+                    meet(j + 1, gave_up);
+                    // a jump in another producer's latents: this wave's (unmoved) state too
+                    if (jumpl[buf] == j + 1 && !moved) stash(buf);
                     // merge: lane row g reads producer g's pair
 #pragma unroll
                     for (int ti = 0; ti < 2; ++ti) {
@@ -642,7 +685,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                     for (int q3 = 0; q3 < 3; ++q3) gpl[buf][w][q3][lq] = gacc[q3];
                 }
                 __builtin_amdgcn_s_setprio(0);
-                if (lq == 0) movedl[buf][w] = (moved ? 1 : 0) | (slow ? 2 : 0);
+                if (lq == 0) movedl[buf][w] = (moved ? 1 : 0) | (slow ? 2 : 0) | (jumped ? 4 : 0) | (gave_up ? 8 : 0);
                 FLARE_WAIT_VMCNT(0);     // this wave's K rows of the next subtile have landed
             }
             __syncthreads();   // hand-off: subtile j's operands visible, subtile j-1's consumed
@@ -722,6 +765,58 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 int mv[L::NP];
 #pragma unroll
                 for (int w2 = 0; w2 < L::NP; ++w2) mv[w2] = movedl[buf][w2];
+                if constexpr (!SEP) {
+                    // A reference jumped in subtile j (or a meeting gave up): the first such
+                    // subtile's starting state -- U here, before this subtile's rescales, and
+                    // the producers' stashed references and dens -- goes to the chunk's prefix
+                    // slot, and the replay covers subtiles rj1 .. rj2.  A meeting that gave up
+                    // before any record leaves the prefix intact for a whole-chunk replay.
+                    int fl = 0;
+#pragma unroll
+                    for (int w2 = 0; w2 < L::NP; ++w2) fl |= mv[w2];
+                    const bool tj = (fl & 8) != 0, jj = (fl & 4) != 0;
+                    if (fl & 12) {
+                        if (tj) {
+                            if (rj1 < 0) rwhole = true;
+                            else rj2 = NS - 1;
+                        }
+                        if (jj && !rwhole) {
+                            if (!record) {
+                                rwhole = true;
+                            } else {
+                                if (rj1 < 0) {
+                                    rj1 = j;
+                                    // buffer stores: one per-lane offset, the per-entry offsets
+                                    // are constants (plain addresses would be loop invariants that
+                                    // the compiler keeps live across the subtile loop)
+                                    const __amdgpu_buffer_rsrc_t nres =
+                                        buffer_rsrc(pnum + pbase * D, (unsigned)(M * D * 4));
+                                    const unsigned voff = (unsigned)((8 * g * D + dc0 + c) * 4);
+                                    const float iv = 1.0f / vs;
+#pragma unroll
+                                    for (int mi = 0; mi < L::MTA; ++mi)
+#pragma unroll
+                                        for (int di = 0; di < L::DTC; ++di)
+#pragma unroll
+                                            for (int r = 0; r < 4; ++r)
+                                                __builtin_amdgcn_raw_buffer_store_b32(
+                                                    __builtin_bit_cast(unsigned, U[mi][di][r] * iv), nres, voff,
+                                                    ((32 * (mi >> 1) + 4 * (mi & 1) + r) * D + 16 * di) * 4, 0);
+                                    if (cw == 0) {
+                                        float* rmax = const_cast<float*>(pmax);
+                                        float* rden = const_cast<float*>(pden);
+                                        for (int m = lane; m < M; m += 64) {
+                                            const float rr = rsvl[buf][m];
+                                            rmax[pbase + m] = rr == kNegInf ? kNegInf : rr * kLn2;
+                                            rden[pbase + m] = dsvl[buf][m];
+                                        }
+                                    }
+                                }
+                                rj2 = max(rj2, j);
+                            }
+                        }
+                    }
+                }
                 // ---- V' rows of subtile j (fp16) to this wave's LDS region
                 float vv[2][8];
                 float vlane = 0.0f;
@@ -905,7 +1000,11 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     }
     if (redo != nullptr) {
         __syncthreads();
-        if (tid == 0) redo[(size_t)bh * nchunks + c_idx] = redol;
+        if constexpr (SEP) {
+            if (tid == 0) redo[(size_t)bh * nchunks + c_idx] = redol;
+        } else if (tid == 64 * L::NP) {
+            redo[(size_t)bh * nchunks + c_idx] = rwhole ? kRedoWhole : rj1 >= 0 ? redo_narrow(rj1, rj2) : 0;
+        }
     }
 }
 
@@ -916,8 +1015,10 @@ using namespace mfma;
 int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, int spin_limit, hipStream_t stream) {
+                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_tr: chunk must be a multiple of %d", T);
+    // a narrow redo flag holds subtile indices below kRedoMaxSubtiles
+    const int rec = record && alpha == nullptr && chunk / T < kRedoMaxSubtiles ? 1 : 0;
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_tr: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     FLARE_REQUIRE((uint64_t)chunk * H * D * 4 < (1ull << 31), "chunk_output_tr: chunk too long for 32-bit offsets");
@@ -927,7 +1028,7 @@ int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int
 #define FLARE_OUT_TR_T(MM, DD, SP, F)                                                                          \
     hipLaunchKernelGGL((chunk_output_tr<MM, DD, SP, F>), grid, dim3(64 * (MM / 64 + DD / 32)), 0, stream,      \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, \
-                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit)
+                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit, rec)
 #define FLARE_OUT_TR(MM, DD)                                     \
     do {                                                         \
         if (f16in) {                                             \

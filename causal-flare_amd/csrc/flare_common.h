@@ -27,6 +27,21 @@ template <> __device__ __forceinline__ __half from_f32<__half>(float x) { return
 __device__ __forceinline__ bool is_neg_inf(float x) { return x == kNegInf; }
 
 // ---------------------------------------------------------------------------
+// Per-chunk replay flags of the MFMA output kernels ([B*H, NC] ints), read by the
+// tokenwise fp32 kernel: 0 leaves the chunk alone, kRedoWhole replays the whole
+// chunk from its prefix state, and a narrow flag replays the 32-token subtiles
+// j1 .. j2 only, starting from the state at subtile j1's start, which the output
+// kernel then wrote over the chunk's prefix slot.
+// ---------------------------------------------------------------------------
+constexpr int kRedoWhole = 1;
+constexpr int kRedoNarrowBit = 1 << 30;
+constexpr int kRedoMaxSubtiles = 1 << 15;    // j1, j2 < kRedoMaxSubtiles
+__host__ __device__ __forceinline__ int redo_narrow(int j1, int j2) { return kRedoNarrowBit | (j1 << 15) | j2; }
+__host__ __device__ __forceinline__ bool redo_is_narrow(int f) { return (f & kRedoNarrowBit) != 0; }
+__host__ __device__ __forceinline__ int redo_j1(int f) { return (f >> 15) & (kRedoMaxSubtiles - 1); }
+__host__ __device__ __forceinline__ int redo_j2(int f) { return f & (kRedoMaxSubtiles - 1); }
+
+// ---------------------------------------------------------------------------
 // Online-softmax monoid on one latent: (max, den, num).  The inf-safe forms
 // follow causal_flare/autoregressive/reference.py:160-187 (merge) and
 // :461-473 (single-token update).

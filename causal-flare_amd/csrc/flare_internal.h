@@ -20,7 +20,7 @@ int launch_prepare_mfma(const void* Q, const void* K, const void* V, int64_t B, 
 int launch_output_mfma(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H,
                        int64_t M, int64_t D, float scale, int64_t chunk, const float* pmax,
                        const float* pden, const float* pnum, void* Y, int out_dtype, const int32_t* tmask,
-                       bool f16in, int* redo, hipStream_t stream);
+                       bool f16in, int* redo, hipStream_t stream, bool record = false);
 
 // FLARE_DISABLE_MFMA=1 routes every shape to the scalar-fp32 kernels (A/B checks);
 // FLARE_MFMA_PHASES=<bits> keeps the MFMA kernel only for phase 1 (bit 0) and/or
@@ -56,7 +56,7 @@ inline bool output_tr_enabled() {
 int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, int spin_limit, hipStream_t stream);
+                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record = false);
 // Meetings of chunk_output_tr that gave up waiting (optionally reset to 0).
 int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset);
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
@@ -79,13 +79,16 @@ inline bool prepare_tr_enabled() {
 }
 // alpha: NULL for shared decoder weights; else the decoder softmax [B*H, N, M]
 // (fp16) written by launch_decoder_alpha, for separate Qdec / Kdec.
-// redo: NULL, or [B*H, NC] ints; the kernel writes 1 for a chunk in which some
-// latent's reference jumped past kJumpMax within a subtile (else 0), and the
-// caller replays those chunks with the tokenwise fp32 kernel.
+// redo: NULL, or [B*H, NC] ints; the kernel writes kRedoWhole for a chunk in which
+// some latent's reference jumped past kJumpMax within a subtile (else 0), and the
+// caller replays those chunks with the tokenwise fp32 kernel.  record: the prefix
+// arrays are the caller's own scratch, so chunk_output_tr (shared weights) may write
+// the state at the first flagged subtile over a chunk's prefix slot and flag only
+// the subtiles to replay (redo_narrow).
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, hipStream_t stream);
+                     bool f16in, int* redo, hipStream_t stream, bool record = false);
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
                          float scale, const int32_t* tmask, void* alpha, float* lse, bool f16in, hipStream_t stream);
 }  // namespace flare

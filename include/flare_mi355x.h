@@ -257,9 +257,12 @@ int flare_semi_ar_forward_state(const void* Q, const void* K, const void* V, con
  * (flare_ar_forward_workspace_size) exceeds flare_ar_forward_noalloc_max_bytes()
  * (64 MiB) returns FLARE_ERR_INVALID before launching anything; separate decoder
  * tensors use the MFMA path when flare_ar_forward_workspace_size_sep also fits,
- * else the scalar kernels.  Every call on a GPU shares its array: calls that
- * overlap on one GPU (other streams, other threads) race and must be serialised
- * by the caller.
+ * else the scalar kernels.  Every call on a GPU shares its array.  Calls are
+ * ordered on the device: a call enqueued on another stream than the previous
+ * call's first waits for that call's kernels (an event recorded after them;
+ * calls from several host threads enqueue under one lock).  Under HIP graph
+ * capture this ordering is not recorded: a replay of a captured call that
+ * overlaps another call on another stream races on the array.
  */
 size_t flare_ar_forward_noalloc_max_bytes(void);
 int flare_ar_forward_noalloc(const void* Q, const void* K, const void* V, const void* Qdec,

@@ -91,6 +91,11 @@ def test_semi_ar_cached_validation():
     """The semi-AR cached prefill / block decode (stubs in the reference,
     semi_autoregressive/inference.py:5-36) validate blocks before they need a GPU."""
     q, k, v = torch.randn(2, 4, 16), torch.randn(1, 48, 2, 16), torch.randn(1, 48, 2, 16)
+    # block_size is required for a prefill (no whole-call default block)
+    with pytest.raises(ValueError, match="requires block_size"):
+        causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v)
+    with pytest.raises(ValueError, match="requires block_size"):
+        causal_flare.semi_autoregressive.SemiAutoRegressivePrefillFLARE.apply(q, k, v)
     with pytest.raises(ValueError, match="multiple of 16"):
         causal_flare.flare_semi_autoregressive_prefill_trition(q, k, v, block_size=24)
     with pytest.raises(ValueError, match="exact multiple of block_size"):

@@ -161,6 +161,26 @@ def test_score_jump_within_subtile(M, D, dtype):
 
 
 @pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_score_jumps_replay_flagged_subtiles(M, D):
+    """Two jumps in one chunk (subtiles 2 and 5 of a 512-token chunk) and one in the
+    first subtile of another chunk: the output kernel records the state at the first
+    flagged subtile's start over the chunk's prefix slot, and the tokenwise fp32 kernel
+    replays subtiles 2 .. 5 (and 0 .. 0) only, from that state.  Tokens after the
+    replayed range come from the MFMA kernel with the jumped references."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("score_jump_narrow", M, D)
+    B, N, H = 1, 2048, 2
+    q, k, v = seeded(808 + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    scale = D ** -0.5
+    lat = list(range(0, M, M // 8))
+    kj = _jump_keys(q, k, [512 + 64 + 5, 512 + 160 + 20, 1536 + 3], lat=lat, nats=[150.0, 300.0, 450.0],
+                    scale=scale)
+    ref = O.ar_chunked(q, kj, v, scale=scale, nthreads=16)
+    y = flare_autoregressive_triton(q.to(DEV), kj.to(DEV), v.to(DEV), chunk_size=512)
+    assert_parity(y, ref, torch.bfloat16, f"narrow replay M={M} D={D}")
+
+
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
 @pytest.mark.parametrize("nats", [4.0, 7.5, 8.8, 12.0])
 @pytest.mark.parametrize("tok", [9, 100])
 def test_key_outlier_spreads_references(M, D, nats, tok):

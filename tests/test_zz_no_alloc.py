@@ -1,7 +1,9 @@
 """The allocation-free forward flare_ar_forward_noalloc (static device scratch)
 against flare_ar_forward with a caller workspace, through the C ABI: two calls in
 a row on one device, the second with a smaller input, each bit-identical to the
-workspace entry point; plus the size limit."""
+workspace entry point; calls on two streams without a host synchronisation in
+between (the entry point orders them); plus the size limit."""
+import ctypes
 import math
 import sys
 
@@ -89,3 +91,34 @@ def test_noalloc_separate_decoder_and_limit():
     rc = fn(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), None, None, _lib.BF16, 64, 1 << 20, 64, 256, 128, 128, 0.1, 64,
             None, None, None, None, None, None, _lib.ptr(y), _lib.BF16, None, _lib.stream_of(torch.device(DEV)))
     assert rc == -1 and b"maximum is" in lib.flare_last_error()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Back-to-back calls on one stream, then on a second stream with no host
+    synchronisation in between: the entry point makes the second stream wait for
+    the first call's kernels, so both outputs equal the workspace entry point's."""
+    lib, fn = _fn()
+    P = _lib.ptr
+    print("CASE no_alloc two streams", flush=True)
+    shapes = [(11, 1, 8192, 8, 128, 64), (12, 2, 2048, 4, 128, 64), (13, 1, 4096, 8, 128, 64)]
+    ins, refs = [], []
+    for seed, B, N, H, M, D in shapes:
+        q, k, v, _ = _inputs(seed, B, N, H, M, D, torch.bfloat16, False)
+        nb = lib.flare_ar_forward_workspace_size(B, N, H, M, D, 0)
+        ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+        y = torch.empty_like(v)
+        _lib.check(lib.flare_ar_forward(P(q), P(k), P(v), None, None, _lib.BF16, B, N, H, M, D, D, D ** -0.5, 0,
+                                        None, None, None, None, None, None, P(y), _lib.BF16, P(ws), nb,
+                                        _lib.stream_of(torch.device(DEV))), "ws")
+        ins.append((q, k, v, B, N, H, M, D))
+        refs.append(y)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = [torch.full_like(r, float("nan")) for r in refs]
+    torch.cuda.synchronize()
+    for (q, k, v, B, N, H, M, D), y, s in zip(ins, outs, (s1, s1, s2)):
+        rc = fn(P(q), P(k), P(v), None, None, _lib.BF16, B, N, H, M, D, D, D ** -0.5, 0, None, None, None,
+                None, None, None, P(y), _lib.BF16, None, ctypes.c_void_p(s.cuda_stream))
+        _lib.check(rc, "noalloc")
+    torch.cuda.synchronize()
+    for i, (y, r) in enumerate(zip(outs, refs)):
+        assert torch.equal(y, r), f"call {i}: noalloc output differs from the workspace entry point"
