@@ -188,12 +188,16 @@ __global__ __launch_bounds__(256) void chunk_prefix_kernel(
 // of TT: scores and decoder log-sum-exps for the tile first, then the
 // tokenwise recurrence and the readout, two barriers per token.
 // ---------------------------------------------------------------------------
+// The per-token factors gam / eta / wts come first (16-byte aligned) and are padded to
+// Mp = R * ROWS latents (gam 1, eta and wts 0 past M): a thread's ROWS consecutive latents
+// are then read four at a time with no bounds branch.  The token rows follow, also
+// 16-byte aligned when Dk is a multiple of 4.
 struct OutSmem {
-    int TT, Dk, DT, M, R;
+    int TT, Dk, DT, M, R, Mp;
     bool shared;
     __host__ __device__ size_t floats() const {
-        return (size_t)TT * Dk * (shared ? 1 : 2) + (size_t)TT * DT + (size_t)TT * M * (shared ? 1 : 2) +
-               (size_t)5 * M + (size_t)R * DT + TT + 8;
+        return (size_t)3 * Mp + (size_t)TT * Dk * (shared ? 1 : 2) + (size_t)TT * DT +
+               (size_t)TT * M * (shared ? 1 : 2) + (size_t)2 * M + (size_t)R * DT + TT + 8;
     }
 };
 
@@ -216,25 +220,27 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
         flag = only[(size_t)blockIdx.y * gridDim.x + blockIdx.x];
         if (flag == 0) return;
     }
-    extern __shared__ float smem[];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
     const int R = kNT / DT;
-    float* k_tile = smem;                                   // [TT][Dk]
+    const int Mp = R * ROWS;
+    float* gam = smem;                                      // [Mp]
+    float* eta = gam + Mp;                                  // [Mp]
+    float* wts = eta + Mp;                                  // [Mp]
+    float* k_tile = wts + Mp;                               // [TT][Dk]
     float* qd_tile = k_tile + TT * Dk;                      // [TT][Dk] (separate decoder only)
     float* v_tile = qd_tile + (shared ? 0 : TT * Dk);       // [TT][DT]
     float* s_tile = v_tile + TT * DT;                       // [TT][M]
     float* a_tile = s_tile + TT * M;                        // [TT][M] (separate decoder only)
     float* mstate = a_tile + (shared ? 0 : TT * M);         // [M]
     float* dstate = mstate + M;
-    float* gam = dstate + M;
-    float* eta = gam + M;
-    float* wts = eta + M;
-    float* ypart = wts + M;                                 // [R][DT]
+    float* ypart = dstate + M;                              // [R][DT]
     float* lse = ypart + R * DT;                            // [TT]
 
     const int c = blockIdx.x, bh = blockIdx.y, dt0 = blockIdx.z * DT;
     const int NC = gridDim.x;
     const int b = bh / H, h = bh % H;
     const int tid = threadIdx.x, col = tid % DT, rg = tid / DT;
+    const int mb = rg * ROWS;     // this thread's latents mb .. mb + ROWS - 1 (value column col)
     const T* q_h = Q + (size_t)h * M * Dk;
     const T* kd_h = shared ? q_h : Kdec + (size_t)h * M * Dk;
 
@@ -243,10 +249,15 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
         mstate[m] = pmax[pbase + m];
         dstate[m] = pden[pbase + m];
     }
+    for (int m = M + tid; m < Mp; m += kNT) {
+        gam[m] = 1.0f;
+        eta[m] = 0.0f;
+        wts[m] = 0.0f;
+    }
     float U[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        const int m = rg + R * r;
+        const int m = mb + r;
         U[r] = m < M ? pnum[(pbase + m) * Dv + dt0 + col] : 0.0f;
     }
 
@@ -270,38 +281,60 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
             v_tile[e] = i < nt ? to_f32(V[(((size_t)b * N + t0 + i) * H + h) * Dv + dt0 + d]) : 0.0f;
         }
         __syncthreads();
-        // Scores of the tile: thread m reads its latent's Q (and K_dec) row once per tile, four
-        // columns at a time, against the TT token rows in LDS (the same address in every lane:
-        // broadcast reads); the sums run over d in order, per token.
+        // Scores of the tile: thread m holds 32 columns of its latent's Q (and K_dec) row at a
+        // time and reads the TT token rows from LDS four columns at a time (the same address
+        // in every lane: broadcast reads); the sums run over d in order, per token.
         for (int m = tid; m < M; m += kNT) {
             const T* qrow = q_h + (size_t)m * Dk;
             const T* kdrow = kd_h + (size_t)m * Dk;
             float acc[16], acc2[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[i] = acc2[i] = 0.0f;
-            auto cols = [&](int d, int nd) {
-                float qv[4], kv[4];
+            if ((Dk & 3) == 0) {
+                for (int d0 = 0; d0 < Dk; d0 += 32) {
+                    float qv[32], kv[32];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    qv[e] = e < nd ? to_f32(qrow[d + e]) : 0.0f;
-                    kv[e] = (!shared && e < nd) ? to_f32(kdrow[d + e]) : 0.0f;
-                }
+                    for (int e = 0; e < 32; ++e) {
+                        qv[e] = d0 + e < Dk ? to_f32(qrow[d0 + e]) : 0.0f;
+                        kv[e] = (!shared && d0 + e < Dk) ? to_f32(kdrow[d0 + e]) : 0.0f;
+                    }
+                    const int nd = min(32, Dk - d0);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    if (i < nt) {
+                    for (int dd = 0; dd < 32; dd += 4) {
+                        if (dd < nd) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (e < nd) {
-                                acc[i] += k_tile[i * Dk + d + e] * qv[e];
-                                if (!shared) acc2[i] += qd_tile[i * Dk + d + e] * kv[e];
+                            for (int i = 0; i < 16; ++i) {
+                                if (i < nt) {
+                                    const float4 k4 = *reinterpret_cast<const float4*>(k_tile + i * Dk + d0 + dd);
+                                    acc[i] += k4.x * qv[dd];
+                                    acc[i] += k4.y * qv[dd + 1];
+                                    acc[i] += k4.z * qv[dd + 2];
+                                    acc[i] += k4.w * qv[dd + 3];
+                                    if (!shared) {
+                                        const float4 q4 = *reinterpret_cast<const float4*>(qd_tile + i * Dk + d0 + dd);
+                                        acc2[i] += q4.x * kv[dd];
+                                        acc2[i] += q4.y * kv[dd + 1];
+                                        acc2[i] += q4.z * kv[dd + 2];
+                                        acc2[i] += q4.w * kv[dd + 3];
+                                    }
+                                }
                             }
                         }
                     }
                 }
-            };
-            int d = 0;
-            for (; d + 4 <= Dk; d += 4) cols(d, 4);
-            if (d < Dk) cols(d, Dk - d);
+            } else {
+                for (int d = 0; d < Dk; ++d) {
+                    const float qd1 = to_f32(qrow[d]);
+                    const float kd1 = shared ? 0.0f : to_f32(kdrow[d]);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        if (i < nt) {
+                            acc[i] += k_tile[i * Dk + d] * qd1;
+                            if (!shared) acc2[i] += qd_tile[i * Dk + d] * kd1;
+                        }
+                    }
+                }
+            }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 if (i < nt) {
@@ -352,12 +385,17 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
             const float vc = v_tile[i * DT + col];
             float yp = 0.0f;
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) {
-                const int m = rg + R * r;
-                if (m < M) {
-                    U[r] = U[r] * gam[m] + eta[m] * vc;
-                    yp += wts[m] * U[r];
-                }
+            for (int r = 0; r < ROWS; r += 4) {
+                // (< Mp: past M the factors keep U = 0 and add 0; the same address in every
+                // lane of a wave: broadcast reads)
+                const float4 g4 = *reinterpret_cast<const float4*>(gam + mb + r);
+                const float4 e4 = *reinterpret_cast<const float4*>(eta + mb + r);
+                const float4 w4 = *reinterpret_cast<const float4*>(wts + mb + r);
+                U[r] = U[r] * g4.x + e4.x * vc;
+                U[r + 1] = U[r + 1] * g4.y + e4.y * vc;
+                U[r + 2] = U[r + 2] * g4.z + e4.z * vc;
+                U[r + 3] = U[r + 3] * g4.w + e4.w * vc;
+                yp += w4.x * U[r] + w4.y * U[r + 1] + w4.z * U[r + 2] + w4.w * U[r + 3];
             }
             ypart[rg * DT + col] = yp;
             __syncthreads();
@@ -447,7 +485,8 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
                       (long long)M, (long long)Dv);
         const int R = kNT / DT;
         const int64_t rows = (M + R - 1) / R;
-        OutSmem lay{16, (int)Dk, DT, (int)M, R, shared};
+        const int rows_t = rows <= 8 ? 8 : rows <= 16 ? 16 : rows <= 32 ? 32 : 64;   // the ROWS instance
+        OutSmem lay{16, (int)Dk, DT, (int)M, R, R * rows_t, shared};
         while (lay.floats() * sizeof(float) > 64 * 1024 && lay.TT > 1) lay.TT /= 2;
         FLARE_REQUIRE(lay.floats() * sizeof(float) <= 64 * 1024, "chunk_output: shape too large for LDS");
         const int TT = lay.TT;
