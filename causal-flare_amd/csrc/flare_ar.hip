@@ -201,6 +201,33 @@ struct OutSmem {
     }
 };
 
+// 32 consecutive elements (16-byte aligned) to fp32 through 16-byte loads.
+template <typename T>
+__device__ __forceinline__ void load_row32(const T* p, float* out) {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float4 x = reinterpret_cast<const float4*>(p)[j];
+            out[4 * j] = x.x;
+            out[4 * j + 1] = x.y;
+            out[4 * j + 2] = x.z;
+            out[4 * j + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 x = reinterpret_cast<const uint4*>(p)[j];
+            const unsigned w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const unsigned short lo = (unsigned short)(w[e] & 0xffffu), hi = (unsigned short)(w[e] >> 16);
+                out[8 * j + 2 * e] = to_f32(__builtin_bit_cast(T, lo));
+                out[8 * j + 2 * e + 1] = to_f32(__builtin_bit_cast(T, hi));
+            }
+        }
+    }
+}
+
 template <typename T, int ROWS>
 __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V,
@@ -293,10 +320,15 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
             if ((Dk & 3) == 0) {
                 for (int d0 = 0; d0 < Dk; d0 += 32) {
                     float qv[32], kv[32];
+                    if (d0 + 32 <= Dk && (Dk * (int)sizeof(T)) % 16 == 0) {   // 16-byte aligned pieces
+                        load_row32(qrow + d0, qv);
+                        if (!shared) load_row32(kdrow + d0, kv);
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 32; ++e) {
-                        qv[e] = d0 + e < Dk ? to_f32(qrow[d0 + e]) : 0.0f;
-                        kv[e] = (!shared && d0 + e < Dk) ? to_f32(kdrow[d0 + e]) : 0.0f;
+                        for (int e = 0; e < 32; ++e) {
+                            qv[e] = d0 + e < Dk ? to_f32(qrow[d0 + e]) : 0.0f;
+                            kv[e] = (!shared && d0 + e < Dk) ? to_f32(kdrow[d0 + e]) : 0.0f;
+                        }
                     }
                     const int nd = min(32, Dk - d0);
 #pragma unroll

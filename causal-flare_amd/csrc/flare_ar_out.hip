@@ -656,7 +656,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                                     const float dt = dn[mi][r] + dcum[ti][r];
                                     const float p = SEP ? (float)af[mi][ti][r]
                                                         : ref[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[ti][r], scale2, -ref[ti])) * f[ti];
-                                    q[r] = dt > 0.0f ? p / dt : 0.0f;
+                                    q[r] = dt > 0.0f ? p * __builtin_amdgcn_rcpf(dt) : 0.0f;
                                     w1[r] = (f16)(moved ? q[r] * dn[mi][r] : q[r]);
                                 }
                                 split_bf16x4(em[ti][0], em[ti][1], em[ti][2], em[ti][3], ehi[jb][ti], elo[jb][ti]);
