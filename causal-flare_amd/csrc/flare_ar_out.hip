@@ -572,6 +572,11 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                 __builtin_amdgcn_s_setprio(3);
                 f16* er = erl[buf];
                 f16* wq = wl[buf];
+                // (separate decoder weights: no softmax partials, so slow == moved)
+                auto light_path = [&](bool mv) {
+                    if constexpr (SEP) return false;
+                    else return !mv;
+                };
                 dnbig = false;
                 if (!slow) {
                     // ---- common path: E rows to LDS (fp16), the cumulative den
@@ -614,6 +619,43 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
 #pragma unroll
                     for (int mi = 0; mi < L::MTP; ++mi) dmx = fmaxf(dmx, fmaxf(fmaxf(dn[mi][0], dn[mi][1]), fmaxf(dn[mi][2], dn[mi][3])));
                     dnbig = dmx > kDenMax;
+                } else if (light_path(moved)) {
+                    // ---- a token's softmax partial would underflow against C_w, and no reference
+                    //      moved (e.g. latents whose reference jumped far above every later score:
+                    //      their E underflows while their alpha does not).  As the common path,
+                    //      with alpha = 2^(S - ref) f from the scores again instead of E A f.
+                    f32x4 dcum[L::MTP][2];
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi) {
+                        const f16* col = er + mp0 + 16 * mi + 4 * (c & 3);
+                        const f16x8 ea = cat8<f16x8>(lds_tr4(col + (4 * g + (c >> 2)) * L::RPE),
+                                                     lds_tr4(col + (16 + 4 * g + (c >> 2)) * L::RPE));
+                        const f32x4 d0 = f32x4{dn[mi][0], dn[mi][1], dn[mi][2], dn[mi][3]};
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) dcum[mi][ti] = mma(ea, tri[ti], d0);
+                    }
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi) {
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti) {
+                            const f32x4 sc = scores(mi, ti);
+                            f32x4 q;
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float p = ref[ti] == kNegInf ? 0.0f : exp2f_fast(fmaf(sc[r], scale2, -ref[ti])) * f[ti];
+                                q[r] = p * __builtin_amdgcn_rcpf(dcum[mi][ti][r]);
+                            }
+                            *reinterpret_cast<f16x4*>(wq + (16 * ti + c) * L::RPW + mp0 + 16 * mi + 4 * g) =
+                                __builtin_convertvector(q, f16x4);
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) dn[mi][r] = row_bcast15(dcum[mi][1][r]);   // den at t = 31
+                    }
+                    float dmx = 0.0f;
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi) dmx = fmaxf(dmx, fmaxf(fmaxf(dn[mi][0], dn[mi][1]), fmaxf(dn[mi][2], dn[mi][3])));
+                    dnbig = dmx > kDenMax;
+                    slow = false;     // the consumers form this wave's share of G as on the common path
                 } else {
                     // ---- general path: alpha = 2^(S - ref) f, guarded 1 / d_t, W1 = W d0 when a reference
                     //      moved (the consumers then read out z0 = U / d0), this wave's share of G^T in fp32
