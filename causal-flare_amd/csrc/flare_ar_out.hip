@@ -72,6 +72,14 @@ struct TrLayout {
     static constexpr int NP = M / 64;            // producer waves, 64 latents each
     static constexpr int NC = D / 32;            // consumer waves, 32 value columns each
     static constexpr int NT = 64 * (NP + NC);
+    // Roles by wave index.  A workgroup's waves go to distinct SIMDs, and a second workgroup
+    // on the same compute unit (the 128 x 64 bank fits two) places wave w on another SIMD
+    // than the first's wave w, one step further round the SIMDs (measured on MI355X): with
+    // producers and consumers interleaved (P, C, P, C) every SIMD then holds one producer
+    // and one consumer, where P, P, C, C would put two producers on one SIMD and two
+    // consumers on another.  One workgroup of 8 waves per CU gives waves w and w + 4 the
+    // same SIMD, so P, P, P, P, C, C, C, C pairs them there.
+    static constexpr bool IL = NP == 2 && NC == 2;
     static constexpr int MP = 64;
     static constexpr int MTP = 4;                // 16-latent tiles per producer
     static constexpr int MKP = 2;                // 32-latent k-steps per producer
@@ -194,6 +202,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     const int nchunks = gridDim.x;
     const int b = bh / H, h = bh % H;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const bool producer = L::IL ? (w & 1) == 0 : w < L::NP;
+    const int pw = L::IL ? w >> 1 : w;            // producer index (producer waves)
+    const int ptid = 64 * pw + lane;              // thread index among the producers
     const int g = lane >> 4, c = lane & 15;
     const int t_begin = c_idx * chunk;
     const int t_end = min(N, t_begin + chunk);
@@ -212,9 +223,9 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     bool rwhole = false;
     int rj1 = -1, rj2 = -1;
 
-    if (w < L::NP) {
+    if (producer) {
         // =========================== producer ===========================
-        const int mp0 = w * L::MP;
+        const int mp0 = pw * L::MP;
         bf16x8 qa[L::MTP][L::KS];      // Q rows of this wave's latents (A operands: rows m, k = d)
 #pragma unroll
         for (int mi = 0; mi < L::MTP; ++mi)
@@ -294,8 +305,8 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
             }
         };
         KDma<D, 64 * L::NP> kdma;
-        kdma.init(K, row0, stride, t_begin, tid);
-        kdma.issue(ksl0, 0, t_begin, N, stride, tid, lane);
+        kdma.init(K, row0, stride, t_begin, ptid);
+        kdma.issue(ksl0, 0, t_begin, N, stride, ptid, lane);
         FLARE_WAIT_VMCNT(0);
         __syncthreads();   // B0: K rows of subtile 0 visible
         auto subtile = [&](auto parity, int j) {
@@ -330,7 +341,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                             af[mi][ti] = ok ? load4<f16x4>(arow + 16 * mi) : f16x4{0, 0, 0, 0};
                     }
                 }
-                if (j + 1 < NS) kdma.issue(knext, j + 1, t0 + T, N, stride, 64 * w + lq, lq);
+                if (j + 1 < NS) kdma.issue(knext, j + 1, t0 + T, N, stride, 64 * pw + lq, lq);
                 // ---- raw scores A = Q K^T: acc[mi][ti][r] = A[t = 16 ti + c][m = 16 mi + 4 g + r]
                 const bool ragged = t0 + T > t_end;
                 f32x4 acc[L::MTP][2];
@@ -551,8 +562,8 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                         }
                     }
                     if (g == 0) {
-                        lsep[buf][w][c] = float2{ref[0], part[0]};
-                        lsep[buf][w][16 + c] = float2{ref[1], part[1]};
+                        lsep[buf][pw][c] = float2{ref[0], part[0]};
+                        lsep[buf][pw][16 + c] = float2{ref[1], part[1]};
                     }
                     meet(j + 1, gave_up);
                     // a jump in another producer's latents: this wave's (unmoved) state too
@@ -724,10 +735,10 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                         }
                     }
 #pragma unroll
-                    for (int q3 = 0; q3 < 3; ++q3) gpl[buf][w][q3][lq] = gacc[q3];
+                    for (int q3 = 0; q3 < 3; ++q3) gpl[buf][pw][q3][lq] = gacc[q3];
                 }
                 __builtin_amdgcn_s_setprio(0);
-                if (lq == 0) movedl[buf][w] = (moved ? 1 : 0) | (slow ? 2 : 0) | (jumped ? 4 : 0) | (gave_up ? 8 : 0);
+                if (lq == 0) movedl[buf][pw] = (moved ? 1 : 0) | (slow ? 2 : 0) | (jumped ? 4 : 0) | (gave_up ? 8 : 0);
                 FLARE_WAIT_VMCNT(0);     // this wave's K rows of the next subtile have landed
             }
             __syncthreads();   // hand-off: subtile j's operands visible, subtile j-1's consumed
@@ -738,7 +749,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         }
     } else {
         // =========================== consumer ===========================
-        const int cw = w - L::NP;
+        const int cw = L::IL ? w >> 1 : w - L::NP;
         const int dc0 = cw * L::DC;
         // U[mi][di][r] = U[m][d = dc0 + 16 di + c] for latent m = lat(mi, g) + r: lane row g holds
         // the 8 consecutive latents 32 k + 8 g .. + 7 of each 32-latent k-step k in tiles 2 k and
@@ -1044,7 +1055,7 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         __syncthreads();
         if constexpr (SEP) {
             if (tid == 0) redo[(size_t)bh * nchunks + c_idx] = redol;
-        } else if (tid == 64 * L::NP) {
+        } else if (!producer && w == (L::IL ? 1 : L::NP) && lane == 0) {   // the first consumer
             redo[(size_t)bh * nchunks + c_idx] = rwhole ? kRedoWhole : rj1 >= 0 ? redo_narrow(rj1, rj2) : 0;
         }
     }
