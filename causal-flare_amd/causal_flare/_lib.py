@@ -27,6 +27,8 @@ HEADER_FUNCTIONS = (
     "flare_ar_forward_masked",
     "flare_ar_default_chunk",
     "flare_stablemax_forward",
+    "flare_stablemax_backward_workspace_size",
+    "flare_stablemax_backward",
     "flare_forward_kernel_resources",
     "flare_ar_backward_workspace_size",
     "flare_ar_backward",
@@ -74,6 +76,10 @@ def _declare(lib):
     lib.flare_ar_default_chunk.argtypes = [_i64] * 5
     lib.flare_stablemax_forward.restype = _i
     lib.flare_stablemax_forward.argtypes = [_vp] * 5 + [_i] + [_i64] * 6 + [_f, _i64, _f, _vp, _i, _vp, _sz, _vp]
+    lib.flare_stablemax_backward_workspace_size.restype = _sz
+    lib.flare_stablemax_backward_workspace_size.argtypes = [_i64] * 6 + [_i]
+    lib.flare_stablemax_backward.restype = _i
+    lib.flare_stablemax_backward.argtypes = [_vp] * 5 + [_i] + [_i64] * 6 + [_f, _f] + [_vp] * 7 + [_vp, _sz, _vp]
     lib.flare_forward_kernel_resources.restype = _i
     lib.flare_forward_kernel_resources.argtypes = [_i] + [_i64] * 3 + [_i, _i64, _i, _vp]
     lib.flare_ar_forward_masked.restype = _i

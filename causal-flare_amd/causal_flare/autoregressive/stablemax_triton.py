@@ -16,7 +16,11 @@ output has V's dtype.  Kept as in the reference: the argument list, the
 ``NotImplementedError`` for the options its Triton path does not implement
 (``eps``, ``profile``, recurrent ``state``, ``attention_mask``,
 ``return_state``, write gates) and the chunk-size rule (a multiple of 16).
-The backward is not implemented here (``NotImplementedError``).
+The backward (``stablemax_triton.py:1981-2420``) runs on the library's fp32 kernels
+(C ``flare_stablemax_backward``): a chunked replay from the forward's chunk
+prefixes, exclusive suffix sums over chunks, the per-token score and value
+gradients, and the token-causal backward's contractions with Q, K, Q_dec, K_dec.
+It supports M <= 256 and head dims up to 256 (``NotImplementedError`` beyond).
 """
 from __future__ import annotations
 
@@ -44,7 +48,7 @@ def _resolve_stablemax_chunk_size(N, M, D_score, D_value, chunk_size):
     return 128
 
 
-def _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_precision):
+def _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_precision, ctx=None):
     B, N, H, M, D_score, D_value = validate_flare_qkv_layouts(Q, K, V, name="Stablemax Triton FLARE")
     scale_f = _resolve_attn_scale(scale, D_score)
     power_f = float(power)
@@ -78,7 +82,39 @@ def _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_pr
                                      D_value, float(scale_f), chunk, power_f, P(Y), _lib.dtype_code(out_dtype),
                                      P(ws), nbytes, _lib.stream_of(V.device))
     _lib.check(rc, "flare_stablemax_forward")
+    if ctx is not None:
+        ctx.save_for_backward(q, k, v, qd, kd, Y)
+        ctx.meta = (Q.dtype, K.dtype, V.dtype, Q_dec.dtype, K_dec.dtype, cdt, float(scale_f), power_f)
     return Y
+
+
+def _stablemax_backward(ctx, dY):
+    q, k, v, qd, kd, Y = ctx.saved_tensors
+    q_dt, k_dt, v_dt, qd_dt, kd_dt, cdt, scale_f, power_f = ctx.meta
+    H, M, D_score = q.shape
+    B, N, _, D_value = v.shape
+    if M > 256 or D_score > 256 or D_value > 256:
+        raise NotImplementedError(
+            "The MI355X stablemax FLARE backward supports M <= 256 and head dims <= 256; "
+            f"got M={M}, D_score={D_score}, D_value={D_value}."
+        )
+    dev = v.device
+    dyf = dY.to(torch.float32).contiguous()
+    yf = Y.to(torch.float32).contiguous()
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqd = torch.empty_like(qd) if qd is not None else None
+    dkd = torch.empty_like(kd) if kd is not None else None
+    lib = _lib.lib()
+    nbytes = lib.flare_stablemax_backward_workspace_size(B, N, H, M, D_score, D_value, int(qd is not None))
+    ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
+    P = _lib.ptr
+    rc = lib.flare_stablemax_backward(P(q), P(k), P(v), P(qd), P(kd), _lib.dtype_code(cdt), B, N, H, M, D_score,
+                                      D_value, scale_f, power_f, P(yf), P(dyf), P(dq), P(dk), P(dv), P(dqd), P(dkd),
+                                      P(ws), nbytes, _lib.stream_of(dev))
+    _lib.check(rc, "flare_stablemax_backward")
+    # a decoder tensor that is the encoder one has its share folded into dK / dQ
+    return (dq.to(q_dt), dk.to(k_dt), dv.to(v_dt), None if dqd is None else dqd.to(qd_dt),
+            None if dkd is None else dkd.to(kd_dt), None, None, None, None)
 
 
 class FLAREAutoregressiveStablemaxTriton(autograd.Function):
@@ -86,11 +122,18 @@ class FLAREAutoregressiveStablemaxTriton(autograd.Function):
 
     @staticmethod
     def forward(ctx, Q, K, V, Q_dec, K_dec, scale=None, chunk_size=None, power: float = 2.0, input_precision=None):
-        return _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_precision)
+        ctx.empty_shapes = None
+        if V.shape[1] == 0:
+            ctx.empty_shapes = (Q, K, V, Q_dec, K_dec)
+        return _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_precision, ctx)
 
     @staticmethod
     def backward(ctx, dY):
-        raise NotImplementedError("FLAREAutoregressiveStablemaxTriton backward is not implemented on MI355X.")
+        """Reference stablemax_triton.py:1981-2420 (zero gradients for an empty sequence,
+        as the reference's :1982-1999)."""
+        if ctx.empty_shapes is not None:
+            return tuple(torch.zeros_like(t) for t in ctx.empty_shapes) + (None, None, None, None)
+        return _stablemax_backward(ctx, dY)
 
 
 def flare_autoregressive_stablemax_triton(

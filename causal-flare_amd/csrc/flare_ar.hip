@@ -574,8 +574,8 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
 
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
-                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream) {
-    return launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, stream);
+                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream, float power) {
+    return launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, stream, nullptr, power);
 }
 
 int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M, int64_t Dv,

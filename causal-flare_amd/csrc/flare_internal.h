@@ -121,7 +121,8 @@ int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_
                    float* P1, float* P2, bool f16in, hipStream_t st);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
-                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);
+                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream,
+                          float power = 0.0f);
 int launch_prefix_public(float* cmax, float* cden, float* cnum, int64_t BH, int64_t NC, int64_t M, int64_t Dv,
                          const float* m0, const float* d0, const float* u0, float* m_fin, float* d_fin,
                          float* u_fin, hipStream_t stream);

@@ -14,10 +14,6 @@
 
 namespace flare {
 
-int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
-                          int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
-                          int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream);
-
 constexpr int kSemiNT = 256;
 constexpr int kSemiCols = 4;
 

@@ -22,6 +22,8 @@ Two layers:
       cached state (the semi-AR cached prefill / block decode, which the
       reference leaves as stubs).
     - ``chunk_summaries``: phase 1's per-chunk (max, den, num), fp64.
+    - ``stablemax_grads``: fp64 autograd of that definition (the stablemax backward's
+      ground truth), pinned by finite differences of ``brute_stablemax``;
     - ``brute_stablemax``: the stablemax variant's per-token definition
       (``autoregressive/stablemax_triton.py:1718-1731``), and
       ``stablemax_chunked``, its chunked form (``stablemax.py:578-635``).
@@ -490,6 +492,43 @@ def ar_grads(Q, K, V, dY, scale=None, Q_dec=None, K_dec=None):
 
     q, k, v, qd, kd = (leaf(x) for x in (Q, K, V, Q_dec, K_dec))
     y = ar_forward_torch64(q, k, v, scale, qd, kd)
+    (y * torch.as_tensor(_f64(dY))).sum().backward()
+    return tuple(None if x is None else x.grad.numpy() for x in (q, k, v, qd, kd))
+
+
+def stablemax_forward_torch64(Q, K, V, power=2.0, scale=None, Q_dec=None, K_dec=None):
+    """The stablemax definition of brute_stablemax (stablemax_triton.py:1718-1731) in fp64
+    torch ops, differentiable: E = s(a) with the piecewise transform, z_t = cumsum(E v) /
+    cumsum(E), y_t = softmax_m(scale qd_t . kd_m) . z_t.  Returns Y [B, N, H, Dv]."""
+    import torch
+    H, M, Dk = Q.shape
+    scale = resolve_scale(scale, Dk)
+    Qd = K if Q_dec is None else Q_dec
+    Kd = Q if K_dec is None else K_dec
+    S = scale * torch.einsum("bnhd,hmd->bhnm", K, Q)
+    A = scale * torch.einsum("bnhd,hmd->bhnm", Qd, Kd)
+    pos = torch.where(S >= 0, S + 1.0, torch.ones_like(S))
+    neg = torch.where(S < 0, 1.0 - S, torch.ones_like(S))
+    E = torch.where(S >= 0, pos ** power, neg ** (-power))
+    Vt = V.transpose(1, 2)
+    num = torch.cumsum(E.unsqueeze(-1) * Vt.unsqueeze(3), dim=2)
+    Z = num / torch.cumsum(E, dim=2).unsqueeze(-1)
+    Y = torch.einsum("bhnm,bhnmd->bhnd", torch.softmax(A, dim=-1), Z)
+    return Y.transpose(1, 2)
+
+
+def stablemax_grads(Q, K, V, dY, power=2.0, scale=None, Q_dec=None, K_dec=None):
+    """Gradients of sum(Y * dY) for the stablemax forward, fp64 autograd -- the ground
+    truth of the reference's stablemax backward test (testing/autoregressive/
+    test_stablemax.py, backward against the PyTorch path).  Returns numpy arrays
+    (None for an absent decoder tensor)."""
+    import torch
+
+    def leaf(x):
+        return None if x is None else torch.as_tensor(_f64(x)).requires_grad_(True)
+
+    q, k, v, qd, kd = (leaf(x) for x in (Q, K, V, Q_dec, K_dec))
+    y = stablemax_forward_torch64(q, k, v, power, scale, qd, kd)
     (y * torch.as_tensor(_f64(dY))).sum().backward()
     return tuple(None if x is None else x.grad.numpy() for x in (q, k, v, qd, kd))
 

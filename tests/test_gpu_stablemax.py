@@ -60,3 +60,81 @@ def test_stablemax_reference_sizes_bf16():
     ref = O.brute_stablemax(q, k, v, power=2.0)
     assert_parity(y, ref, torch.bfloat16, "stablemax 128x64")
     assert np.isfinite(y.float().cpu().numpy()).all()
+
+
+# --------------------------------------------------------------------------
+# Backward (C flare_stablemax_backward) against fp64 autograd of the definition
+# (O.stablemax_grads, pinned by finite differences in tests/test_oracle.py).
+# Bar: the reference's own (test_stablemax.py:428-482, fp32 inputs: rtol = atol
+# = 2e-3, 3e-3 for powers 3 and 4); 16-bit inputs: max |g - g_ref| <= 2e-2 of
+# max |g_ref| per tensor, as the token-causal backward tests.
+# --------------------------------------------------------------------------
+def _stablemax_grads_gpu(q, k, v, qd, kd, dy, power, scale, chunk):
+    from causal_flare.autoregressive import flare_autoregressive_stablemax_triton
+    leaves = [None if t is None else t.to(DEV).requires_grad_(True) for t in (q, k, v, qd, kd)]
+    y = flare_autoregressive_stablemax_triton(leaves[0], leaves[1], leaves[2], scale=scale, chunk_size=chunk,
+                                              Q_dec=leaves[3], K_dec=leaves[4], power=power)
+    (y.float() * dy.to(DEV)).sum().backward()
+    return [None if t is None else t.grad for t in leaves]
+
+
+def _grad_check(got, ref, names, dtype, tol, what):
+    for g, r, n in zip(got, ref, names):
+        if r is None:
+            continue
+        a = g.float().cpu().numpy()
+        assert np.isfinite(a).all(), f"{what} {n}: non-finite gradient"
+        if dtype == torch.float32:
+            np.testing.assert_allclose(a, r, rtol=tol, atol=tol, err_msg=f"{what} {n}")
+        else:
+            err = float(np.abs(a - r).max() / max(np.abs(r).max(), 1e-2))
+            assert err <= 2e-2, f"{what} {n}: max|g - ref| / max|ref| = {err:.3e}"
+
+
+@pytest.mark.parametrize("power", [2.0, 3.0, 4.0])
+def test_stablemax_backward_reference_case(power):
+    """The reference's backward test shape (test_stablemax.py:428-482): B=2, H=2, M=32,
+    N=128, D=32, chunk 64, separate decoder tensors, fp32."""
+    _case("stablemax backward", power)
+    g = torch.Generator().manual_seed(4)
+    B, H, M, N, D = 2, 2, 32, 128, 32
+    q, k, v = (torch.randn(s, generator=g) for s in ((H, M, D), (B, N, H, D), (B, N, H, D)))
+    qd, kd = torch.randn((B, N, H, D), generator=g), torch.randn((H, M, D), generator=g)
+    dy = torch.randn((B, N, H, D), generator=g)
+    got = _stablemax_grads_gpu(q, k, v, qd, kd, dy, power, D ** -0.5, 64)
+    ref = O.stablemax_grads(q, k, v, dy, power, D ** -0.5, qd, kd)
+    _grad_check(got, ref, ("dQ", "dK", "dV", "dQ_dec", "dK_dec"), torch.float32,
+                2e-3 if power == 2.0 else 3e-3, f"stablemax backward power={power}")
+
+
+@pytest.mark.parametrize("mode", ["shared", "sep_q", "sep_k"])
+@pytest.mark.parametrize("power", [1.0, 2.5])
+def test_stablemax_backward_decoder_modes(mode, power):
+    """Shared decoder weights (the decoder share folds into dQ / dK), one separate decoder
+    tensor, a non-integer power, ragged N (not a multiple of the 16-token chunk)."""
+    _case("stablemax backward modes", mode, power)
+    B, N, H, M, D, Dv = 2, 77, 2, 48, 16, 32
+    g = torch.Generator().manual_seed(81)
+    q = torch.randn((H, M, D), generator=g) * D ** -0.5 * 2
+    k, v = torch.randn((B, N, H, D), generator=g), torch.randn((B, N, H, Dv), generator=g)
+    qd = torch.randn((B, N, H, D), generator=g) if mode == "sep_q" else None
+    kd = torch.randn((H, M, D), generator=g) * 0.3 if mode == "sep_k" else None
+    dy = torch.randn((B, N, H, Dv), generator=g)
+    got = _stablemax_grads_gpu(q, k, v, qd, kd, dy, power, 0.5, None)
+    ref = O.stablemax_grads(q, k, v, dy, power, 0.5, qd, kd)
+    _grad_check(got, ref, ("dQ", "dK", "dV", "dQ_dec", "dK_dec"), torch.float32, 2e-3,
+                f"stablemax backward {mode} power={power}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stablemax_backward_16bit_large_bank(dtype):
+    """A 256 x 128 bank (the 8-token chunk, past the 60 KiB row budget of 16) and a
+    128 x 64 bank, 16-bit inputs."""
+    for (B, N, H, M, D) in ((1, 96, 2, 256, 128), (2, 200, 2, 128, 64)):
+        _case("stablemax backward 16-bit", dtype, M, D)
+        q, k, v = seeded(90 + M, B, N, H, M, D, D, dtype, q_std=D ** -0.5)
+        g = torch.Generator().manual_seed(91)
+        dy = torch.randn((B, N, H, D), generator=g)
+        got = _stablemax_grads_gpu(q, k, v, None, None, dy, 2.0, None, None)
+        ref = O.stablemax_grads(q, k, v, dy, 2.0, None, None, None)
+        _grad_check(got, ref, ("dQ", "dK", "dV"), dtype, None, f"stablemax backward {dtype} {M}x{D}")

@@ -397,3 +397,42 @@ def test_chunk_summaries_merge_to_the_whole_sequence_state():
         np.testing.assert_allclose(m.reshape(B, H, M), st["m"], rtol=1e-12)
         np.testing.assert_allclose(d.reshape(B, H, M), st["d"], rtol=1e-10)
         np.testing.assert_allclose(u.reshape(B, H, M, D), st["u"], rtol=1e-9, atol=1e-12)
+
+
+# --------------------------------------------------------------------------
+# Stablemax gradient oracle (stablemax_grads): pinned by the per-token
+# definition (forward values, powers 1-4 and 2.5) and central finite
+# differences of brute_stablemax.
+# --------------------------------------------------------------------------
+@pytest.mark.parametrize("power", [1.0, 2.0, 2.5, 4.0])
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, True)])
+def test_stablemax_grad_oracle_forward_is_the_definition(power, sep_q, sep_k):
+    Q, K, V, Qd, Kd, _ = _grad_inputs(13, 2, 17, 2, 8, 8, 5, sep_q, sep_k)
+    y = O.stablemax_forward_torch64(Q, K, V, power, 0.7, Qd, Kd)
+    _close(y.numpy(), O.brute_stablemax(Q, K, V, power, 0.7, Qd, Kd), 1e-12)
+
+
+@pytest.mark.parametrize("power", [2.0, 2.5])
+@pytest.mark.parametrize("sep_q,sep_k", [(False, False), (True, False), (False, True), (True, True)])
+def test_stablemax_grad_oracle_matches_finite_differences(power, sep_q, sep_k):
+    """Central differences of sum(brute_stablemax * dY) at every input entry (the
+    scores cross 0, where the transform's two branches meet with equal value and
+    slope p)."""
+    Q, K, V, Qd, Kd, G = _grad_inputs(17, 1, 6, 1, 4, 3, 2, sep_q, sep_k)
+    grads = O.stablemax_grads(Q, K, V, G, power, 0.8, Qd, Kd)
+    inputs = [Q, K, V, Qd, Kd]
+    Gn = G.numpy()
+    h = 1e-6
+    for idx, (x, gx) in enumerate(zip(inputs, grads)):
+        if x is None:
+            assert gx is None
+            continue
+        fd = np.zeros(x.shape)
+        for j in range(x.numel()):
+            vals = []
+            for sgn in (1.0, -1.0):
+                xs = [t.clone() if t is not None else None for t in inputs]
+                xs[idx].view(-1)[j] += sgn * h
+                vals.append(float((O.brute_stablemax(xs[0], xs[1], xs[2], power, 0.8, xs[3], xs[4]) * Gn).sum()))
+            fd.reshape(-1)[j] = (vals[0] - vals[1]) / (2 * h)
+        np.testing.assert_allclose(gx, fd, rtol=1e-6, atol=1e-8)
