@@ -9,9 +9,14 @@ exponential, the decoder weights stay a softmax over the latents:
           (sum_{tau<=t} s(a_tau,m) v_tau) / (sum_{tau<=t} s(a_tau,m)),
     a_tau,m = scale k_tau . q_m,   s(x) = (1+x)^p (x >= 0), (1-x)^-p (x < 0).
 
-It runs on the library's fp32 chunk kernels (C ``flare_stablemax_forward``):
-chunk sums of s(a) and s(a) v, their exclusive scan, and the tokenwise replay
-with the latent-softmax readout, all in fp32 whatever the input dtype.  The
+It runs in C ``flare_stablemax_forward``: chunk sums of s(a) and s(a) v, their
+exclusive scan, and the replay with the latent-softmax readout.  bf16 / fp16
+inputs with M in {128, 256} and D_score = D_value in {64, 128} take the MFMA
+kernels (the decoder softmax pass, then the producer / consumer output kernel
+with the stablemax transform of the scores, log2 s(a) against lazy per-latent
+references, fp32 accumulation); other dtypes and shapes, and explicit chunk
+sizes that are not a multiple of 32, the fp32 chunk kernels.  With no
+``chunk_size`` the library picks the chunk (one round of workgroups); the
 output has V's dtype.  Kept as in the reference: the argument list, the
 ``NotImplementedError`` for the options its Triton path does not implement
 (``eps``, ``profile``, recurrent ``state``, ``attention_mask``,
@@ -55,6 +60,9 @@ def _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_pr
     _normalize_input_precision(input_precision)
     _, _, sep_q, sep_k, shared = resolve_flare_causal_decode_inputs(Q, K, Q_dec, K_dec)
     chunk = _resolve_stablemax_chunk_size(N, M, D_score, D_value, chunk_size)
+    # (the reference's default chunk is a Triton tile size; without an explicit one the
+    # library chooses, which changes rounding only)
+    lib_chunk = chunk if (chunk_size is not None or os.environ.get("FLARE_PYTORCH_CHUNK_SIZE")) else 0
     if chunk % 16 != 0:
         raise ValueError(
             "FLAREAutoregressiveStablemaxTriton requires a chunk size divisible by 16. "
@@ -75,11 +83,11 @@ def _stablemax_forward(Q, K, V, Q_dec, K_dec, scale, chunk_size, power, input_pr
     kd = None if kd is None else kd.to(cdt).contiguous()
     Y = torch.empty((B, N, H, D_value), device=V.device, dtype=out_dtype)
     lib = _lib.lib()
-    nbytes = lib.flare_ar_forward_workspace_size(B, N, H, M, D_value, chunk)
+    nbytes = lib.flare_ar_forward_workspace_size_sep(B, N, H, M, D_value, lib_chunk)
     ws = torch.empty(max(nbytes, 1), device=V.device, dtype=torch.uint8)
     P = _lib.ptr
     rc = lib.flare_stablemax_forward(P(q), P(k), P(v), P(qd), P(kd), _lib.dtype_code(cdt), B, N, H, M, D_score,
-                                     D_value, float(scale_f), chunk, power_f, P(Y), _lib.dtype_code(out_dtype),
+                                     D_value, float(scale_f), lib_chunk, power_f, P(Y), _lib.dtype_code(out_dtype),
                                      P(ws), nbytes, _lib.stream_of(V.device))
     _lib.check(rc, "flare_stablemax_forward")
     if ctx is not None:

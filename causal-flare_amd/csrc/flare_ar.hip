@@ -272,9 +272,11 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
     const T* kd_h = shared ? q_h : Kdec + (size_t)h * M * Dk;
 
     const size_t pbase = ((size_t)bh * NC + c) * M;
+    // stablemax: the recurrence below keeps absolute sums (max 0); summaries written by the
+    // MFMA prepare carry a reference max, folded in here
     for (int m = tid; m < M; m += kNT) {
-        mstate[m] = pmax[pbase + m];
-        dstate[m] = pden[pbase + m];
+        mstate[m] = power > 0.0f ? 0.0f : pmax[pbase + m];
+        dstate[m] = power > 0.0f ? pden[pbase + m] * __expf(pmax[pbase + m]) : pden[pbase + m];
     }
     for (int m = M + tid; m < Mp; m += kNT) {
         gam[m] = 1.0f;
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(kNT) void chunk_output_kernel(
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         const int m = mb + r;
-        U[r] = m < M ? pnum[(pbase + m) * Dv + dt0 + col] : 0.0f;
+        U[r] = m < M ? pnum[(pbase + m) * Dv + dt0 + col] * (power > 0.0f ? __expf(pmax[pbase + m]) : 1.0f) : 0.0f;
     }
 
     int t_begin = c * chunk;
@@ -449,6 +451,10 @@ static int launch_prepare(const void* Q, const void* K, const void* V, int dtype
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum,
                           hipStream_t stream, const int32_t* tmask = nullptr, float power = 0.0f) {
+    if (power > 0.0f && (mfma_phase_mask() & 1) && chunk % 32 == 0 && tmask == nullptr &&
+        mfma_prepare_supported(dtype, M, Dk, Dv) && (M == 128 || M == 256) && (Dk == 64 || Dk == 128))
+        return launch_prepare_tr(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, nullptr, dtype == FLARE_F16,
+                                 stream, power);
     if (power <= 0.0f && (mfma_phase_mask() & 1) && chunk % 32 == 0 && mfma_prepare_supported(dtype, M, Dk, Dv)) {
         if (output_pc_enabled() && (M == 128 || M == 256))
             return launch_prepare_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, cmax, cden, cnum, tmask,
@@ -545,6 +551,20 @@ static int launch_output(const void* Q, const void* K, const void* V, const void
 #undef FLARE_OUT
         return check_launch("chunk_output_kernel");
     };
+    // the stablemax encoder on the MFMA output kernel: the decoder softmax first (as for
+    // separate decoder tensors; the encoder weights are not a softmax), then chunk_output_tr
+    // with the stablemax transform of the scores; flagged chunks replay in fp32
+    if (power > 0.0f && (mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr && redo != nullptr &&
+        alpha_ws != nullptr && tmask == nullptr && output_pc_enabled() && output_tr_enabled() &&
+        mfma_output_supported(dtype, out_dtype, true, M, Dk, Dv)) {
+        int rc = launch_decoder_alpha(Qdec ? Qdec : K, Kdec ? Kdec : Q, B, N, H, M, Dk, scale, nullptr, alpha_ws,
+                                      nullptr, dtype == FLARE_F16, stream);
+        if (rc) return rc;
+        rc = launch_output_pc(Q, K, V, B, N, H, M, Dk, scale, chunk, pmax, pden, pnum, Y, out_dtype, nullptr, alpha_ws,
+                              dtype == FLARE_F16, redo, stream, false, power);
+        if (rc) return rc;
+        return scalar(redo);
+    }
     // the MFMA kernels run with the redo flags (the chunks they hand back to the scalar kernel)
     if (power <= 0.0f && (mfma_phase_mask() & 2) && chunk % 32 == 0 && lse_dec == nullptr && redo != nullptr) {
         int rc = -1;
@@ -756,14 +776,20 @@ int flare_stablemax_forward(const void* Q, const void* K, const void* V, const v
     float* cmax = (float*)ws;
     float* cden = (float*)(ws + align256(per * sizeof(float)));
     float* cnum = (float*)(ws + 2 * align256(per * sizeof(float)));
+    int* redo = (int*)(ws + 2 * align256(per * sizeof(float)) + align256(per * Dv * sizeof(float)));
+    // with room for the decoder softmax (flare_ar_forward_workspace_size_sep), the MFMA
+    // kernels for bf16 / fp16 inputs of their shapes
+    void* alpha_ws = workspace_bytes >= flare_ar_forward_workspace_size_sep(B, N, H, M, Dv, chunk)
+                         ? (void*)(ws + summary_bytes(B, N, H, M, Dv, chunk)) : nullptr;
     hipStream_t s = (hipStream_t)stream;
     int rc = launch_prepare(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, s, nullptr, power);
     if (rc) return rc;
-    // the summaries' maxima are 0: the online-softmax merges of the scan are plain sums
+    // the scan's online-softmax merges: plain sums for the scalar prepare's summaries (max 0),
+    // reference-scaled ones for the MFMA prepare's
     rc = launch_prefix(cmax, cden, cnum, B * H, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, s);
     if (rc) return rc;
     return launch_output(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, chunk, cmax, cden, cnum, Y,
-                         out_dtype, nullptr, s, nullptr, nullptr, nullptr, power);
+                         out_dtype, nullptr, s, nullptr, alpha_ws, alpha_ws ? redo : nullptr, power);
 }
 
 int flare_ar_forward_masked(const void* Q, const void* K, const void* V, const void* Qdec,

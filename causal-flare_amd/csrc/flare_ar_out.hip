@@ -166,13 +166,14 @@ struct KDma {
     }
 };
 
-template <int M, int D, bool SEP, bool F16>
+template <int M, int D, bool SEP, bool F16, bool SMX = false>
 __global__ __launch_bounds__(64 * (M / 64 + D / 32), (512 / (64 * (M / 64 + D / 32))) > 0 ? 512 / (64 * (M / 64 + D / 32)) : 1)
 void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N,
                      int H, float scale2, int chunk, const float* pmax, const float* pden,
                      const float* pnum, void* __restrict__ Y, int out_dtype,
                      const int32_t* __restrict__ tmask, const f16* __restrict__ alpha, int* __restrict__ redo,
-                     int spin_limit, int record) {
+                     int spin_limit, int record, float power) {
+    // SMX (separate decoder weights only): the stablemax encoder, smx_log2 on the scores
     // record (shared decoder weights only): the prefix slot of this chunk (pmax, pden,
     // pnum, read once at the start) may be overwritten with the state at the start of
     // the first subtile whose reference jumped, so that the tokenwise fp32 replay only
@@ -371,6 +372,14 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
 #pragma unroll
                             for (int mi = 0; mi < L::MTP; ++mi) acc[mi][ti] = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
                 }
+                if constexpr (SMX) {
+#pragma unroll
+                    for (int mi = 0; mi < L::MTP; ++mi)
+#pragma unroll
+                        for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) acc[mi][ti][r] = smx_log2(acc[mi][ti][r], scale2, power);
+                }
                 // one tile of the same scores again (general path only)
                 auto scores = [&](int mi, int ti) {
                     f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -379,6 +388,10 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
                     for (int kq = 0; kq < L::KS; ++kq)
                         a = mma_in<F16>(qa[mi][kq], load8<bf16x8>(kj + row * D + 8 * swz<D>(row, 4 * kq + g)), a);
                     if (!valid[ti]) a = f32x4{kNegInf, kNegInf, kNegInf, kNegInf};
+                    if constexpr (SMX) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) a[r] = smx_log2(a[r], scale2, power);
+                    }
                     return a;
                 };
                 // ---- E = 2^(S - R) against the current references
@@ -1068,8 +1081,9 @@ using namespace mfma;
 int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record) {
+                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record, float power) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_tr: chunk must be a multiple of %d", T);
+    FLARE_REQUIRE(power <= 0.0f || alpha != nullptr, "chunk_output_tr: the stablemax encoder needs decoder weights");
     // a narrow redo flag holds subtile indices below kRedoMaxSubtiles
     const int rec = record && alpha == nullptr && chunk / T < kRedoMaxSubtiles ? 1 : 0;
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
@@ -1078,19 +1092,21 @@ int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
-#define FLARE_OUT_TR_T(MM, DD, SP, F)                                                                          \
-    hipLaunchKernelGGL((chunk_output_tr<MM, DD, SP, F>), grid, dim3(64 * (MM / 64 + DD / 32)), 0, stream,      \
+#define FLARE_OUT_TR_T(MM, DD, SP, F, SX)                                                                      \
+    hipLaunchKernelGGL((chunk_output_tr<MM, DD, SP, F, SX>), grid, dim3(64 * (MM / 64 + DD / 32)), 0, stream,  \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, \
-                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit, rec)
-#define FLARE_OUT_TR(MM, DD)                                     \
-    do {                                                         \
-        if (f16in) {                                             \
-            if (alpha) FLARE_OUT_TR_T(MM, DD, true, true);       \
-            else FLARE_OUT_TR_T(MM, DD, false, true);            \
-        } else {                                                 \
-            if (alpha) FLARE_OUT_TR_T(MM, DD, true, false);      \
-            else FLARE_OUT_TR_T(MM, DD, false, false);           \
-        }                                                        \
+                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit, rec, power)
+#define FLARE_OUT_TR(MM, DD)                                            \
+    do {                                                                \
+        if (f16in) {                                                    \
+            if (alpha && power > 0.0f) FLARE_OUT_TR_T(MM, DD, true, true, true); \
+            else if (alpha) FLARE_OUT_TR_T(MM, DD, true, true, false);  \
+            else FLARE_OUT_TR_T(MM, DD, false, true, false);            \
+        } else {                                                        \
+            if (alpha && power > 0.0f) FLARE_OUT_TR_T(MM, DD, true, false, true); \
+            else if (alpha) FLARE_OUT_TR_T(MM, DD, true, false, false); \
+            else FLARE_OUT_TR_T(MM, DD, false, false, false);           \
+        }                                                               \
     } while (0)
     if (M == 128 && D == 64) FLARE_OUT_TR(128, 64);
     else if (M == 128 && D == 128) FLARE_OUT_TR(128, 128);

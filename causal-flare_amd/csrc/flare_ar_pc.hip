@@ -1102,13 +1102,14 @@ int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, i
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, hipStream_t stream, bool record) {
+                     bool f16in, int* redo, hipStream_t stream, bool record, float power) {
     FLARE_REQUIRE(chunk % T == 0, "chunk_output_pc: chunk must be a multiple of %d", T);
+    FLARE_REQUIRE(power <= 0.0f || output_tr_enabled(), "chunk_output_pc: the stablemax encoder runs on chunk_output_tr");
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_output_pc: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     if (output_tr_enabled())
         return launch_output_tr(Q, K, V, B, N, H, M, D, scale, chunk, pmax, pden, pnum, Y, out_dtype, tmask, alpha,
-                                f16in, redo, g_spin_limit, stream, record);
+                                f16in, redo, g_spin_limit, stream, record, power);
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;

@@ -95,12 +95,13 @@ struct TileDma {
 
 }  // namespace
 
-template <int M, int D, bool F16, bool MASK>
+template <int M, int D, bool F16, bool MASK, bool SMX = false>
 __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                           const bf16* __restrict__ V, int N, int H, float scale2,
                                                           int chunk, float* __restrict__ cmax,
                                                           float* __restrict__ cden, float* __restrict__ cnum,
-                                                          const int32_t* __restrict__ tmask) {
+                                                          const int32_t* __restrict__ tmask, float power) {
+    // SMX: the stablemax encoder (smx_log2 on the scores; power > 0), else the softmax one
     constexpr int NT = 2 * M;           // M / 32 waves
     constexpr int KS = D / 32;          // k-steps of the scores
     constexpr int DT = D / 16;          // value-column tiles
@@ -261,6 +262,14 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                             acc[ti][0][r] = acc[ti][1][r] = kNegInf;
                     }
             }
+            if constexpr (SMX) {
+#pragma unroll
+                for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[ti][mt][r] = smx_log2(acc[ti][mt][r], scale2, power);
+            }
         };
         // the lazy references, then E = 2^(S - R) of the tile in acc into eh and its den
         auto exps = [&](f32x4 (&acc)[TI][2]) __attribute__((always_inline)) {
@@ -412,8 +421,9 @@ using namespace mfma;
 
 int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      const int32_t* tmask, bool f16in, hipStream_t stream) {
+                      const int32_t* tmask, bool f16in, hipStream_t stream, float power) {
     FLARE_REQUIRE(chunk > 0, "chunk_prepare_tr: chunk must be positive");
+    FLARE_REQUIRE(power <= 0.0f || tmask == nullptr, "chunk_prepare_tr: the stablemax encoder takes no token mask");
     FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
                   "chunk_prepare_tr: unsupported M=%lld D=%lld", (long long)M, (long long)D);
     const int64_t NC = (N + chunk - 1) / chunk;
@@ -421,14 +431,18 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
     const float s2 = scale * kLog2e;
 #define FLARE_PREP_TR_T(MM, DD, F)                                                                           \
     do {                                                                                                     \
-        if (tmask != nullptr)                                                                                \
+        if (power > 0.0f)                                                                                    \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true>), grid, dim3(2 * MM), 0, stream,    \
+                               (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
+                               cmax, cden, cnum, tmask, power);                                              \
+        else if (tmask != nullptr)                                                                           \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, true>), grid, dim3(2 * MM), 0, stream,           \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask);                                                     \
+                               cmax, cden, cnum, tmask, 0.0f);                                               \
         else                                                                                                 \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false>), grid, dim3(2 * MM), 0, stream,          \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask);                                                     \
+                               cmax, cden, cnum, tmask, 0.0f);                                               \
     } while (0)
 #define FLARE_PREP_TR(MM, DD)                        \
     do {                                             \

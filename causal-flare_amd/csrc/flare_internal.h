@@ -56,7 +56,8 @@ inline bool output_tr_enabled() {
 int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record = false);
+                     bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record = false,
+                     float power = 0.0f);
 // Meetings of chunk_output_tr that gave up waiting (optionally reset to 0).
 int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset);
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
@@ -64,9 +65,10 @@ int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, in
                       const int32_t* tmask, bool f16in, hipStream_t stream);
 // Phase 1 with wave-private latents (chunk_prepare_tr); FLARE_PREPARE_KERNEL=pc keeps
 // the producer / consumer kernel chunk_prepare_pc instead (A/B checks).
+// power > 0: the stablemax encoder (no token mask).
 int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
-                      const int32_t* tmask, bool f16in, hipStream_t stream);
+                      const int32_t* tmask, bool f16in, hipStream_t stream, float power = 0.0f);
 // Register, scratch and LDS use of the kernels the forward launches (profile=True).
 int prepare_tr_attributes(int64_t M, int64_t D, bool f16in, hipFuncAttributes* attr, int* threads);
 int output_tr_attributes(int64_t M, int64_t D, bool sep, bool f16in, hipFuncAttributes* attr, int* threads);
@@ -88,7 +90,7 @@ inline bool prepare_tr_enabled() {
 int launch_output_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
                      int64_t D, float scale, int64_t chunk, const float* pmax, const float* pden,
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
-                     bool f16in, int* redo, hipStream_t stream, bool record = false);
+                     bool f16in, int* redo, hipStream_t stream, bool record = false, float power = 0.0f);
 int launch_decoder_alpha(const void* Qd, const void* Kd, int64_t B, int64_t N, int64_t H, int64_t M, int64_t D,
                          float scale, const int32_t* tmask, void* alpha, float* lse, bool f16in, hipStream_t stream);
 }  // namespace flare

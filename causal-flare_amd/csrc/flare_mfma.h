@@ -25,6 +25,16 @@ constexpr float kDenMax = 16.0f;         // den (relative to the reference) that
 // MFMA output kernels resolve; beyond it the earlier tokens' den would approach the fp32
 // underflow against the new reference, and the chunk is replayed tokenwise in fp32.
 constexpr float kJumpMax = 96.0f;
+
+// The stablemax encoder on the MFMA kernels: a raw score x (k . q, before the scale)
+// becomes log2 s(a) / scale2 with a = x scale and s(a) = (1 + a)^p (a >= 0), (1 - a)^-p
+// (a < 0), so that every later `x * scale2` is log2 of the encoder weight and the lazy
+// references, dens and numerators work unchanged.  -inf (a masked token) stays -inf.
+__device__ __forceinline__ float smx_log2(float x, float scale2, float power) {
+    const float a = x * scale2 * kLn2;
+    const float l = a >= 0.0f ? power * __log2f(1.0f + a) : -power * __log2f(1.0f - a);
+    return l * __builtin_amdgcn_rcpf(scale2);
+}
 constexpr float kF16Max = 65504.0f;
 constexpr int kMaxPrepM = 256;           // largest latent bank of the prepare kernel (8 waves)
 

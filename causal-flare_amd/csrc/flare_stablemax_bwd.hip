@@ -86,7 +86,8 @@ template <typename T>
 __global__ __launch_bounds__(kSBT) void stablemax_bwd_forward(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const T* __restrict__ Qd,
     const T* __restrict__ Kd, const float* __restrict__ dY, int N, int H, int M, int Dk, int Dv, float scale,
-    float power, int CT, const float* __restrict__ pden, const float* __restrict__ pnum, float* __restrict__ AL,
+    float power, int CT, const float* __restrict__ pmax, const float* __restrict__ pden,
+    const float* __restrict__ pnum, float* __restrict__ AL,
     float* __restrict__ Cc, float* __restrict__ Wt, float* __restrict__ GZ, float* __restrict__ Sx,
     float* __restrict__ Sy) {
     extern __shared__ __attribute__((aligned(16))) float sm[];
@@ -156,8 +157,10 @@ __global__ __launch_bounds__(kSBT) void stablemax_bwd_forward(
     if (!on) return;     // (no barrier below)
     const size_t pb = ((size_t)bh * NC + c) * M + m;
     // E, the cumulative den from the chunk's prefix, and g_t . U0_m from its numerator row
+    // (summaries written by the MFMA prepare carry a reference max: absolute sums here)
+    const float ps = __expf(pmax[pb]);
     float E[kSBC], Dt[kSBC], gu[kSBC];
-    float dcur = pden[pb];
+    float dcur = pden[pb] * ps;
 #pragma unroll
     for (int i = 0; i < kSBC; ++i) {
         E[i] = i < nt ? stablemax_transform(a[i], power) : 0.0f;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(kSBT) void stablemax_bwd_forward(
     }
     const float* u0 = pnum + pb * Dv;
     for (int d = 0; d < Dv; ++d) {
-        const float u = u0[d];
+        const float u = u0[d] * ps;
 #pragma unroll
         for (int i = 0; i < kSBC; ++i)
             if (i < CT) gu[i] += u * gs[i * Dv + d];
@@ -403,7 +406,7 @@ static int run_stablemax_backward(const void* Q, const void* K, const void* V, c
     dim3 grid((unsigned)NC, (unsigned)BH);
     hipLaunchKernelGGL(stablemax_bwd_forward<T>, grid, dim3(kSBT), s.floats1() * sizeof(float), st, (const T*)Q,
                        (const T*)K, (const T*)V, (const T*)Qd, (const T*)Kd, dY, (int)N, (int)H, (int)M,
-                       (int)Dk, (int)Dv, scale, power, CT, F(lay.off_pd), F(lay.off_pn), F(lay.off_al),
+                       (int)Dk, (int)Dv, scale, power, CT, F(lay.off_pm), F(lay.off_pd), F(lay.off_pn), F(lay.off_al),
                        F(lay.off_c), F(lay.off_w), F(lay.off_gz), F(lay.off_sx), F(lay.off_sy));
     if ((rc = check_launch("stablemax_bwd_forward"))) return rc;
     const int64_t threads = BH * M * Dv + BH * M;

@@ -62,6 +62,32 @@ def test_stablemax_reference_sizes_bf16():
     assert np.isfinite(y.float().cpu().numpy()).all()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("power", [1.0, 2.0, 4.0, 2.5])
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_stablemax_mfma_forward(dtype, power, M, D):
+    """The MFMA path (bf16 / fp16, M in {128, 256}, D in {64, 128}): decoder softmax pass,
+    then chunk_output_tr with the stablemax transform; ragged N, the library's chunk and an
+    explicit one, shared and separate decoder tensors."""
+    from causal_flare.autoregressive import flare_autoregressive_stablemax_triton
+    _case("stablemax mfma", dtype, power, M, D)
+    B, N, H = 2, 1000, 2
+    q, k, v = seeded(74 + M, B, N, H, M, D, D, dtype, q_std=D ** -0.5)
+    # (the chunked fp64 form, pinned to brute_stablemax in tests/test_oracle.py: the
+    # per-token definition is quadratic in N)
+    ref = O.stablemax_chunked(q, k, v, power=power)
+    for chunk in (None, 256):
+        y = flare_autoregressive_stablemax_triton(q.to(DEV), k.to(DEV), v.to(DEV), power=power, chunk_size=chunk)
+        assert_parity(y, ref, dtype, f"stablemax mfma power={power} {M}x{D} chunk={chunk}")
+    g = torch.Generator().manual_seed(75)
+    qd = torch.randn(k.shape, generator=g).to(dtype)
+    kd = (torch.randn(q.shape, generator=g) * D ** -0.5).to(dtype)
+    y = flare_autoregressive_stablemax_triton(q.to(DEV), k.to(DEV), v.to(DEV), power=power, Q_dec=qd.to(DEV),
+                                              K_dec=kd.to(DEV))
+    ref = O.stablemax_chunked(q, k, v, power=power, Q_dec=qd, K_dec=kd)
+    assert_parity(y, ref, dtype, f"stablemax mfma separate decoder power={power} {M}x{D}")
+
+
 # --------------------------------------------------------------------------
 # Backward (C flare_stablemax_backward) against fp64 autograd of the definition
 # (O.stablemax_grads, pinned by finite differences in tests/test_oracle.py).
