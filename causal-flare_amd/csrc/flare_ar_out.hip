@@ -44,6 +44,7 @@
 #include "flare_common.h"
 #include "flare_internal.h"
 #include "flare_mfma.h"
+#include "flare_replay.h"
 
 namespace flare {
 namespace mfma {
@@ -166,18 +167,37 @@ struct KDma {
     }
 };
 
+// The tokenwise replay of an M x D chunk: value-column slices of DT columns, ROWS latents
+// per thread, and the largest token tile (16 or less) whose LDS scratch fits `bytes`.
+template <int M, int D>
+struct ReplayShape {
+    static constexpr int DT = replay_dt(M, D);
+    static constexpr int ROWS = replay_rows(M, DT);
+    static constexpr int NSL = DT > 0 ? D / DT : 0;
+    template <size_t bytes>
+    static constexpr int tt() {
+        int t = 16;
+        while (t > 1 && OutSmem{t, D, DT, M, kNT / DT, (kNT / DT) * ROWS, true}.floats() * sizeof(float) > bytes) t /= 2;
+        return t;
+    }
+};
+
 template <int M, int D, bool SEP, bool F16, bool SMX = false>
 __global__ __launch_bounds__(64 * (M / 64 + D / 32), (512 / (64 * (M / 64 + D / 32))) > 0 ? 512 / (64 * (M / 64 + D / 32)) : 1)
 void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, const bf16* __restrict__ V, int N,
                      int H, float scale2, int chunk, const float* pmax, const float* pden,
                      const float* pnum, void* __restrict__ Y, int out_dtype,
                      const int32_t* __restrict__ tmask, const f16* __restrict__ alpha, int* __restrict__ redo,
-                     int spin_limit, int record, float power) {
+                     int spin_limit, int record, float power, float scale, int replay) {
     // SMX (separate decoder weights only): the stablemax encoder, smx_log2 on the scores
     // record (shared decoder weights only): the prefix slot of this chunk (pmax, pden,
     // pnum, read once at the start) may be overwritten with the state at the start of
     // the first subtile whose reference jumped, so that the tokenwise fp32 replay only
     // covers the flagged subtiles (a narrow redo flag) instead of the whole chunk.
+    // replay (shared decoder weights, with redo): the workgroup runs that replay itself
+    // once its subtiles are done (the shapes whose threads make whole replay slices; the
+    // host then launches no replay kernel).  scale: the natural-log score scale (scale2 =
+    // scale log2(e)), for the replay.
     using L = TrLayout<M, D>;
     // K rows of the even / odd subtiles (swizzled, filled by DMA)
     __shared__ __attribute__((aligned(16))) bf16 ksl0[T * D];
@@ -191,7 +211,8 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
     __shared__ __attribute__((aligned(16))) float d0l[2][M];                  // den at the subtile start
     __shared__ int movedl[2][L::NP];    // bit 0: a reference moved; bit 1: general path
     __shared__ int psync;               // producer arrivals (monotonic)
-    __shared__ int redol;               // separate decoder: a reference jumped past kJumpMax
+    __shared__ int redol;               // separate decoder: a reference jumped past kJumpMax;
+                                        // shared weights: the chunk's redo flag (in-place replay)
     // shared weights: subtile j + 1 in jumpl[j & 1] when a reference jumped past kJumpMax
     // in subtile j (read by the other producers after their meeting); the references and
     // dens at the start of such a subtile (rare: written only then)
@@ -1068,8 +1089,30 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
         __syncthreads();
         if constexpr (SEP) {
             if (tid == 0) redo[(size_t)bh * nchunks + c_idx] = redol;
-        } else if (!producer && w == (L::IL ? 1 : L::NP) && lane == 0) {   // the first consumer
-            redo[(size_t)bh * nchunks + c_idx] = rwhole ? kRedoWhole : rj1 >= 0 ? redo_narrow(rj1, rj2) : 0;
+        } else {
+            if (!producer && w == (L::IL ? 1 : L::NP) && lane == 0) {   // the first consumer
+                const int fl = rwhole ? kRedoWhole : rj1 >= 0 ? redo_narrow(rj1, rj2) : 0;
+                redo[(size_t)bh * nchunks + c_idx] = fl;
+                redol = fl;
+            }
+            // In-place replay of a flagged chunk: slice s of the value columns by threads
+            // 256 s .. 256 s + 255, over the E / W rows (free once the subtiles are done).
+            using RS = ReplayShape<M, D>;
+            if constexpr (RS::NSL * kNT == L::NT) {
+                if (replay) {
+                    __syncthreads();
+                    const int fl = redol;
+                    if (fl != 0) {
+                        using TI = std::conditional_t<F16, __half, __hip_bfloat16>;
+                        const int sl = tid / kNT;
+                        float* sm = reinterpret_cast<float*>(sl == 0 ? erl[0] : wl[0]);
+                        output_chunk_replay<TI, RS::ROWS>(
+                            (const TI*)Q, (const TI*)K, (const TI*)V, (const TI*)K, (const TI*)Q, N, H, M, D, D, RS::DT,
+                            RS::template tt<sizeof(erl)>(), scale, chunk, true, pmax, pden, pnum, Y, out_dtype, nullptr,
+                            tmask, 0.0f, sm, c_idx, bh, sl * RS::DT, nchunks, tid % kNT, fl);
+                    }
+                }
+            }
         }
     }
 }
@@ -1092,10 +1135,12 @@ int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
+    const int inl = redo != nullptr && alpha == nullptr && output_tr_replays_inline(M, D, false) ? 1 : 0;
 #define FLARE_OUT_TR_T(MM, DD, SP, F, SX)                                                                      \
     hipLaunchKernelGGL((chunk_output_tr<MM, DD, SP, F, SX>), grid, dim3(64 * (MM / 64 + DD / 32)), 0, stream,  \
                        (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, pmax, pden, \
-                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit, rec, power)
+                       pnum, Y, out_dtype, tmask, (const f16*)alpha, redo, spin_limit, rec, power, scale,      \
+                       inl)
 #define FLARE_OUT_TR(MM, DD)                                            \
     do {                                                                \
         if (f16in) {                                                    \
@@ -1115,6 +1160,17 @@ int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int
 #undef FLARE_OUT_TR
 #undef FLARE_OUT_TR_T
     return check_launch("chunk_output_tr");
+}
+
+bool output_tr_replays_inline(int64_t M, int64_t D, bool sep) {
+    if (sep || !output_pc_enabled() || !output_tr_enabled()) return false;
+#define FLARE_INL(MM, DD) (ReplayShape<MM, DD>::NSL * kNT == TrLayout<MM, DD>::NT)
+    if (M == 128 && D == 64) return FLARE_INL(128, 64);
+    if (M == 128 && D == 128) return FLARE_INL(128, 128);
+    if (M == 256 && D == 64) return FLARE_INL(256, 64);
+    if (M == 256 && D == 128) return FLARE_INL(256, 128);
+#undef FLARE_INL
+    return false;
 }
 
 int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset) {

@@ -58,6 +58,9 @@ int launch_output_tr(const void* Q, const void* K, const void* V, int64_t B, int
                      const float* pnum, void* Y, int out_dtype, const int32_t* tmask, const void* alpha,
                      bool f16in, int* redo, int spin_limit, hipStream_t stream, bool record = false,
                      float power = 0.0f);
+// chunk_output_tr replays its own flagged chunks (shared decoder weights; the shapes whose
+// threads make whole replay slices): the caller then launches no replay kernel.
+bool output_tr_replays_inline(int64_t M, int64_t D, bool sep);
 // Meetings of chunk_output_tr that gave up waiting (optionally reset to 0).
 int meet_timeouts_tr(hipStream_t stream, unsigned int* count, bool reset);
 int launch_prepare_pc(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
