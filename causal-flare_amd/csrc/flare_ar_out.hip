@@ -89,12 +89,14 @@ struct TrLayout {
     static constexpr int DC = 32;
     static constexpr int DTC = 2;
     static constexpr int KS = D / 32;            // k-steps of the scores
-    // Row pitch (halves) of E[tau][m] and W[t][m]: M + 48 keeps every read pattern used
-    // below at the LDS's full rate on gfx950 (measured: 16-byte reads down 16 rows, and the
-    // transposed 8-byte reads of 4 consecutive rows with either column pattern); pitches
-    // such as M + 24 or M + 36 cost 1.5x to 12x on one of them.
-    static constexpr int RPW = M + 48;
-    static constexpr int RPE = M + 48;
+    // Row pitch (halves) of E[tau][m] and W[t][m]: M + 40 keeps every access pattern used
+    // below at the best rate measured on gfx950 -- the producers' 8-byte row stores, the
+    // 16-byte reads down 16 rows and the transposed 8-byte reads of 4 consecutive rows with
+    // either column pattern.  M + 48 (the same reads) costs 2x on the stores and 1.6x on
+    // the den's transposed reads; pitches such as M + 24, M + 36 or M + 64 cost 1.5x to 10x
+    // on one of them.
+    static constexpr int RPW = M + 40;
+    static constexpr int RPE = M + 40;
     static constexpr int VP = DC + 8;            // row pitch (halves) of a consumer's V[tau][d]
     static constexpr float kVCap = 2048.0f;      // bound on |V'| and |z'| (fp16 operands)
     static constexpr float kLazyE = 256.0f;      // 2^kLazy: an E above it moves the reference
