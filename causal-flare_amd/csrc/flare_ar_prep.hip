@@ -107,8 +107,13 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
     constexpr int DT = D / 16;          // value-column tiles
     constexpr int TI = TT / 16;         // token tiles of a tile
     constexpr int KK = TT / 32;         // k-steps of U^T += V^T E
-    constexpr int NCV = TT * D / 8 / NT;
-    using Dma = TileDma<D, NT>;
+    // M = 256: the waves of the first half (threads 0 .. NT/2 - 1) issue every DMA and
+    // convert every V tile, so that the second half, whose tile chain is the longer one
+    // (it places its barrier after the scores), does neither
+    constexpr bool SPLIT = M >= 256;
+    constexpr int NTD = SPLIT ? NT / 2 : NT;   // threads that issue the DMA and convert V
+    constexpr int NCV = TT * D / 8 / NTD;
+    using Dma = TileDma<D, NTD>;
     // K tiles j mod 3 and V tiles j mod 4 (DMA two tiles ahead; V of tile j is read
     // until iteration j + 1); bf16 inputs: V tiles j mod 2 converted to fp16
     __shared__ __attribute__((aligned(16))) bf16 ktl[3][TT * D];
@@ -143,6 +148,7 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
 #pragma unroll
         for (int kq = 0; kq < KS; ++kq) asm volatile("" : "+v"(qb[mt][kq]));
     const int wofs = 8 * __builtin_amdgcn_readfirstlane(tid - lane);
+    const bool dmaw = !SPLIT || tid < NTD;     // (wave-uniform)
     // per-lane LDS offsets (elements) of the swizzled operand reads: K rows 16 ti + c at
     // chunk 4 kq + g (row & (KC - 1) = c & (KC - 1)), and the transposed V reads of rows
     // 32 kk + 4 g + c / 4 (+ 16) at columns 16 di + 4 (c & 3) (row & (KC - 1) does not
@@ -170,10 +176,12 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
         Dma kdma, vdma;
         kdma.init(Kb, t_begin, stride, tid);
         vdma.init(Vb, t_begin, stride, tid);
-        kdma.issue(ktl[0], wofs, t_begin, t_end, stride, tid);
-        vdma.issue(vtl[0], wofs, t_begin, t_end, stride, tid);
-        kdma.issue(ktl[1], wofs, t_begin + TT, t_end, stride, tid);
-        vdma.issue(vtl[1], wofs, t_begin + TT, t_end, stride, tid);
+        if (dmaw) {
+            kdma.issue(ktl[0], wofs, t_begin, t_end, stride, tid);
+            vdma.issue(vtl[0], wofs, t_begin, t_end, stride, tid);
+            kdma.issue(ktl[1], wofs, t_begin + TT, t_end, stride, tid);
+            vdma.issue(vtl[1], wofs, t_begin + TT, t_end, stride, tid);
+        }
 #pragma unroll
         for (int di = 0; di < DT; ++di) U[di][0] = U[di][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -327,24 +335,31 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
         // product).  The waves of the second half of a 256-latent workgroup place the
         // barrier one step later, after S(j) instead of after E(j): a SIMD then holds one
         // wave in its MFMA-heavy part (P, S) while the other is in its VALU-heavy part (E),
-        // instead of both in the same part at once.
+        // instead of both in the same part at once.  The first half, which does the DMA and
+        // the V conversion for both, runs P(j - 1) before them, while the second half is in
+        // E(j - 1).
         auto loop = [&](auto late_tag) __attribute__((always_inline)) {
             constexpr bool LATE = decltype(late_tag)::value;
             f32x4 acc[TI][2];
             for (int j = 0; j < NS; ++j) {
                 const int t0 = t_begin + TT * j;
+                if constexpr (!LATE) {
+                    if (j > 0) value_product(j - 1);
+                }
                 // tile j + 2 (past the chunk's last tile: copies of its last row, never read), so
                 // that every iteration issues the same number of DMA requests
-                kdma.issue(ktl[(j + 2) % 3], wofs, t0 + 2 * TT, t_end, stride, tid);
-                vdma.issue(vtl[(j + 2) & 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+                if (dmaw) {
+                    kdma.issue(ktl[(j + 2) % 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+                    vdma.issue(vtl[(j + 2) & 3], wofs, t0 + 2 * TT, t_end, stride, tid);
+                }
                 // bf16 inputs, first pass: V of tile j (landed at the last barrier) to fp16 for
                 // iteration j + 1 (a value outside the fp16 range becomes inf and shows in U)
-                if constexpr (!F16 && !BF) {
+                if (!F16 && !BF && dmaw) {
                     const bf16* src = vtl[j & 3];
                     f16* dst = vhl[j & 1];
 #pragma unroll
                     for (int k = 0; k < NCV; ++k) {
-                        const int idx = tid + k * NT;
+                        const int idx = tid + k * NTD;
                         const bf16x8 x = load8<bf16x8>(src + 8 * idx);
                         f16x8 y;
 #pragma unroll
@@ -359,7 +374,6 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                     }
                     scores(j, acc);
                 } else {
-                    if (j > 0) value_product(j - 1);
                     scores(j, acc);
                     exps(acc);
                 }
