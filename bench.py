@@ -198,6 +198,9 @@ def bench_decode(torch, flare, steps=256):
             "traffic": measured_traffic("traffic_cfg4_decode.txt", "decode_step_fast"),
             "alg_bytes_per_step": bytes_step,
             "note": "graph replay of 256 back-to-back steps; per-step time includes launch gaps",
+            "basis": ("algorithmic bytes per step over the step time: the 34.6 MB fp32 state fits in the 256 MB "
+                      "last-level cache between steps, and FETCH_SIZE / WRITE_SIZE cannot tell its hits from HBM, "
+                      "so this is not a measured HBM rate"),
         },
         # the prefill state (before any decode step): the CPU baseline's decode starts from it
         "prefill_state": {kk: vv.cpu() for kk, vv in base.items()},
