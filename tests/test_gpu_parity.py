@@ -160,13 +160,15 @@ def test_score_jump_within_subtile(M, D, dtype):
     assert_noise_model(y, ref, f"repeated outlier M={M} D={D}")
 
 
-@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128), (128, 128), (256, 64)])
 def test_score_jumps_replay_flagged_subtiles(M, D):
     """Two jumps in one chunk (subtiles 2 and 5 of a 512-token chunk) and one in the
     first subtile of another chunk: the output kernel records the state at the first
-    flagged subtile's start over the chunk's prefix slot, and the tokenwise fp32 kernel
-    replays subtiles 2 .. 5 (and 0 .. 0) only, from that state.  Tokens after the
-    replayed range come from the MFMA kernel with the jumped references."""
+    flagged subtile's start over the chunk's prefix slot, and the tokenwise fp32 replay
+    covers subtiles 2 .. 5 (and 0 .. 0) only, from that state -- inside chunk_output_tr
+    for the 128 x 64 and 256 x 128 banks, by the replay launch after it for 128 x 128 and
+    256 x 64.  Tokens after the replayed range come from the MFMA kernel with the jumped
+    references."""
     from causal_flare import flare_autoregressive_triton
     _print_case("score_jump_narrow", M, D)
     B, N, H = 1, 2048, 2
