@@ -17,7 +17,8 @@ __device__ __forceinline__ void store_out(void* Y, size_t idx, float v, int out_
 }
 
 // ---------------------------------------------------------------------------
-// Phase 3.  grid = (NC, B*H, Dv/DT), 256 threads.  Thread (col, rg) owns the
+// Phase 3 (chunk_output_kernel: grid = (NC, B*H, Dv/DT), 256 threads; inside
+// chunk_output_tr: one 256-thread slice per DT value columns).  Thread (col, rg) owns the
 // numerator entries u[m][dt0+col] for m = rg, rg+R, ... (R = 256/DT) in
 // registers; per-latent max/den live in LDS.  Tokens are processed in tiles
 // of TT: scores and decoder log-sum-exps for the tile first, then the
@@ -62,7 +63,6 @@ __device__ __forceinline__ void load_row32(const T* p, float* out) {
         }
     }
 }
-
 
 template <typename T, int ROWS>
 __device__ __forceinline__ void output_chunk_replay(
