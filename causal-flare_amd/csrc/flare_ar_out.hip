@@ -1101,6 +1101,10 @@ void chunk_output_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K, con
             // 256 s .. 256 s + 255, over the E / W rows (free once the subtiles are done).
             using RS = ReplayShape<M, D>;
             if constexpr (RS::NSL * kNT == L::NT) {
+                static_assert(RS::NSL <= 2 && sizeof(erl) == sizeof(wl), "one LDS region per replay slice");
+                static_assert(OutSmem{RS::template tt<sizeof(erl)>(), D, RS::DT, M, kNT / RS::DT, (kNT / RS::DT) * RS::ROWS,
+                                      true}.floats() * sizeof(float) <= sizeof(erl),
+                              "the replay's LDS scratch fits one region");
                 if (replay) {
                     __syncthreads();
                     const int fl = redol;
