@@ -160,6 +160,24 @@ def test_score_jump_within_subtile(M, D, dtype):
     assert_noise_model(y, ref, f"repeated outlier M={M} D={D}")
 
 
+@pytest.mark.parametrize("M,D", [(128, 64), (256, 128)])
+def test_score_jump_in_ragged_tail(M, D):
+    """A jump in the last, partial subtile of the sequence (N = 1100: the default chunk
+    leaves a 12-token last chunk, chunk 256 a 76-token one whose third subtile holds 12
+    tokens): the replay of the flagged subtile stops at the sequence end."""
+    from causal_flare import flare_autoregressive_triton
+    _print_case("score_jump_tail", M, D)
+    B, N, H = 1, 1100, 2
+    q, k, v = seeded(505 + M, B, N, H, M, D, D, torch.bfloat16, q_std=D ** -0.5)
+    scale = D ** -0.5
+    lat = list(range(0, M, M // 8))
+    kj = _jump_keys(q, k, [1090, 1097], lat=lat, nats=[200.0, 350.0], scale=scale)
+    ref = O.ar_chunked(q, kj, v, scale=scale, nthreads=16)
+    for chunk in (None, 256):
+        y = flare_autoregressive_triton(q.to(DEV), kj.to(DEV), v.to(DEV), chunk_size=chunk)
+        assert_parity(y, ref, torch.bfloat16, f"tail jump M={M} D={D} chunk={chunk}")
+
+
 @pytest.mark.parametrize("M,D", [(128, 64), (256, 128), (128, 128), (256, 64)])
 def test_score_jumps_replay_flagged_subtiles(M, D):
     """Two jumps in one chunk (subtiles 2 and 5 of a 512-token chunk) and one in the
