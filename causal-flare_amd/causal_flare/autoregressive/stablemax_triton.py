@@ -21,11 +21,11 @@ output has V's dtype.  Kept as in the reference: the argument list, the
 ``NotImplementedError`` for the options its Triton path does not implement
 (``eps``, ``profile``, recurrent ``state``, ``attention_mask``,
 ``return_state``, write gates) and the chunk-size rule (a multiple of 16).
-The backward (``stablemax_triton.py:1981-2420``) runs on the library's fp32 kernels
-(C ``flare_stablemax_backward``): a chunked replay from the forward's chunk
-prefixes, exclusive suffix sums over chunks, the per-token score and value
-gradients, and the token-causal backward's contractions with Q, K, Q_dec, K_dec.
-It supports M <= 256 and head dims up to 256 (``NotImplementedError`` beyond).
+The backward (``stablemax_triton.py:1981-2420``, C ``flare_stablemax_backward``)
+is the softmax backward's pipeline with the encoder weight s(a) in place of e^a
+(scores as log2 s(a), score gradients times p / (1 + |a|)) when M, D_score and
+D_value are multiples of 16, and a chunked fp32 replay otherwise.  It supports
+M <= 256 and head dims up to 256 (``NotImplementedError`` beyond).
 """
 from __future__ import annotations
 
@@ -107,8 +107,8 @@ def _stablemax_backward(ctx, dY):
             f"got M={M}, D_score={D_score}, D_value={D_value}."
         )
     dev = v.device
-    dyf = dY.to(torch.float32).contiguous()
-    yf = Y.to(torch.float32).contiguous()
+    dyc = dY.to(cdt).contiguous()
+    yc = Y.to(cdt).contiguous()
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dqd = torch.empty_like(qd) if qd is not None else None
     dkd = torch.empty_like(kd) if kd is not None else None
@@ -117,7 +117,7 @@ def _stablemax_backward(ctx, dY):
     ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
     P = _lib.ptr
     rc = lib.flare_stablemax_backward(P(q), P(k), P(v), P(qd), P(kd), _lib.dtype_code(cdt), B, N, H, M, D_score,
-                                      D_value, scale_f, power_f, P(yf), P(dyf), P(dq), P(dk), P(dv), P(dqd), P(dkd),
+                                      D_value, scale_f, power_f, P(yc), P(dyc), P(dq), P(dk), P(dv), P(dqd), P(dkd),
                                       P(ws), nbytes, _lib.stream_of(dev))
     _lib.check(rc, "flare_stablemax_backward")
     # a decoder tensor that is the encoder one has its share folded into dK / dQ

@@ -70,13 +70,19 @@ __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast
 // running den from the chunk's starting state, the decoder weights alpha and
 // LA = L2 - log2(alpha), so that e^{s_tau - L_t} alpha_t = exp2(s2_tau - LA_t).
 // S, L and LA hold log2-domain values: every later factor is one exp2.
+// power > 0 (stablemax encoder): s2 = log2 s(a) with s(a) = (1 + |a|)^(+-p), the
+// encoder weight in place of e^a; the decoder keeps the raw scores.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float stablemax_log2(float a, float p) {
+    return a >= 0.0f ? p * __log2f(1.0f + a) : -p * __log2f(1.0f - a);
+}
+
 template <typename T, bool MF>
 __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ Qd, const T* __restrict__ Kd,
     int N, int H, int M, int Dk, float scale, bool shared, const float* __restrict__ pmax,
     const float* __restrict__ pden, float* __restrict__ S, float* __restrict__ L, float* __restrict__ AL,
-    float* __restrict__ LA) {
+    float* __restrict__ LA, float power) {
     __shared__ float kt[kBTok * 256];
     __shared__ float qdt[kBTok * 256];
     __shared__ float at[kBTok * 256];
@@ -168,7 +174,7 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
             for (int i = 0; i < kBTok; ++i) {
                 if (i < ni) {
                     const float s = as[i] * scale;
-                    const float s2 = s * kBLog2e;
+                    const float s2 = power > 0.0f ? stablemax_log2(s, power) : s * kBLog2e;
                     const float mn = fmaxf(mx, s2);
                     dn = dn * ex2(mx - mn) + ex2(s2 - mn);     // mx = -inf before the first token: ex2 -> 0
                     mx = mn;
@@ -844,13 +850,15 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 // written over s.  Thread m.  The first and last terms are formed in one
 // reverse pass over the chunk and parked in the chunk's L slots (L is not
 // needed after this kernel); the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
-// runs per tau over 16-token blocks of t as in bwd_gz.
+// runs per tau over 16-token blocks of t as in bwd_gz.  power > 0 (stablemax,
+// s2 = log2 s(a)): the gradient with respect to a is the one with respect to
+// log s(a) times d log s / da = p / (1 + |a|) = p 2^(-|s2| / p).
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv, float* __restrict__ S,
     float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ C,
-    const float* __restrict__ X, const float* __restrict__ Ysum) {
+    const float* __restrict__ X, const float* __restrict__ Ysum, float power) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     // dY and V slabs; afterwards (bf16) v_t . X_m of one 16-token half as [m][17]
     __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
@@ -974,7 +982,8 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
             }
         }
         const size_t o = (size_t)tau * M;
-        scol[o] = lcol[o] + sum;
+        const float dlog = lcol[o] + sum;
+        scol[o] = power > 0.0f ? dlog * (power * ex2(-fabsf(s) / power)) : dlog;
     }
 }
 
@@ -1235,7 +1244,7 @@ template <typename T>
 static int run_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
                         int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                         const void* Yp, const void* dYp, void* dQ, void* dK, void* dV, void* dQd, void* dKd,
-                        char* ws, const BwdLayout& lay, hipStream_t st) {
+                        char* ws, const BwdLayout& lay, hipStream_t st, float power) {
     const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
     const bool shared = !sep_q && !sep_k;
     float* pm = reinterpret_cast<float*>(ws + lay.off_pm);
@@ -1259,7 +1268,8 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     const T* dy = static_cast<const T*>(dYp);
     int rc;
     // chunk starting states at the backward's chunk length
-    if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, kBT, pm, pd, pn, st))) return rc;
+    if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, kBT, pm, pd, pn, st, power)))
+        return rc;
     if ((rc = launch_prefix_public(pm, pd, pn, BH, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr,
                                    nullptr, st)))
         return rc;
@@ -1269,11 +1279,11 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
         stats_mfma = M % 16 == 0 && Dk % 32 == 0;
         if (stats_mfma)
             hipLaunchKernelGGL((bwd_stats_kernel<T, true>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H,
-                               (int)M, (int)Dk, scale, shared, pm, pd, S, L, AL, LA);
+                               (int)M, (int)Dk, scale, shared, pm, pd, S, L, AL, LA, power);
     }
     if (!stats_mfma)
         hipLaunchKernelGGL((bwd_stats_kernel<T, false>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M,
-                           (int)Dk, scale, shared, pm, pd, S, L, AL, LA);
+                           (int)Dk, scale, shared, pm, pd, S, L, AL, LA, power);
     if ((rc = check_launch("bwd_stats_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
                        L, AL, C);
@@ -1297,10 +1307,38 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
                        (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
-                       C, pn, pd);
+                       C, pn, pd, power);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
     return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, dQ, dK, dQd, dKd, P1,
                            P2, st);
+}
+
+bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv) {
+    return M % 16 == 0 && M >= 16 && M <= 256 && Dk % 16 == 0 && Dk >= 16 && Dk <= 256 && Dv % 16 == 0 &&
+           Dv >= 16 && Dv <= 512;
+}
+
+size_t ar_backward_workspace(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
+    return BwdLayout(B, N, H, M, Dk, Dv).total;
+}
+
+int ar_backward_run(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
+                    int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale, const void* Y,
+                    const void* dY, void* dQ, void* dK, void* dV, void* dQdec, void* dKdec, void* workspace,
+                    size_t workspace_bytes, hipStream_t st, float power) {
+    const BwdLayout lay(B, N, H, M, Dk, Dv);
+    FLARE_REQUIRE(workspace && workspace_bytes >= lay.total,
+                  "flare_ar_backward: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                  lay.total);
+    FLARE_REQUIRE((((uintptr_t)workspace) & 255) == 0, "flare_ar_backward: workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+#define FLARE_BWD(TY)                                                                                          \
+    return run_backward<TY>(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, Y, dY, dQ, dK, dV, dQdec, \
+                            dKdec, ws, lay, st, power)
+    if (dtype == FLARE_BF16) FLARE_BWD(__hip_bfloat16);
+    if (dtype == FLARE_F16) FLARE_BWD(__half);
+    FLARE_BWD(float);
+#undef FLARE_BWD
 }
 
 }  // namespace flare
@@ -1310,7 +1348,7 @@ using namespace flare;
 extern "C" {
 
 size_t flare_ar_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
-    return BwdLayout(B, N, H, M, Dk, Dv).total;
+    return ar_backward_workspace(B, N, H, M, Dk, Dv);
 }
 
 int flare_ar_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
@@ -1330,20 +1368,8 @@ int flare_ar_backward(const void* Q, const void* K, const void* V, const void* Q
                   "flare_ar_backward: D_value=%lld must be a multiple of 16 in [16, 512]", (long long)Dv);
     FLARE_REQUIRE(!Qdec || dQdec, "flare_ar_backward: Qdec given without dQdec");
     FLARE_REQUIRE(!Kdec || dKdec, "flare_ar_backward: Kdec given without dKdec");
-    const BwdLayout lay(B, N, H, M, Dk, Dv);
-    FLARE_REQUIRE(workspace && workspace_bytes >= lay.total,
-                  "flare_ar_backward: workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
-                  lay.total);
-    FLARE_REQUIRE((((uintptr_t)workspace) & 255) == 0, "flare_ar_backward: workspace must be 256-byte aligned");
-    char* ws = static_cast<char*>(workspace);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-#define FLARE_BWD(TY)                                                                                          \
-    return run_backward<TY>(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, Y, dY, dQ, dK, dV, dQdec, \
-                            dKdec, ws, lay, st)
-    if (dtype == FLARE_BF16) FLARE_BWD(__hip_bfloat16);
-    if (dtype == FLARE_F16) FLARE_BWD(__half);
-    FLARE_BWD(float);
-#undef FLARE_BWD
+    return ar_backward_run(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, Y, dY, dQ, dK, dV, dQdec, dKdec,
+                           workspace, workspace_bytes, static_cast<hipStream_t>(stream), 0.0f);
 }
 
 }  // extern "C"

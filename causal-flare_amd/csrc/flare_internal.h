@@ -142,4 +142,12 @@ int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const vo
                         int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
                         const float* C, const float* gy, void* dQ, void* dK, void* dQdec, void* dKdec, float* P1,
                         float* P2, hipStream_t stream);
+// The token-causal backward (shapes as ar_backward_supported).  power > 0: the
+// stablemax encoder weight s(a) in place of e^a (the decoder stays a softmax).
+bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv);
+size_t ar_backward_workspace(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv);
+int ar_backward_run(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec, int dtype,
+                    int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale, const void* Y,
+                    const void* dY, void* dQ, void* dK, void* dV, void* dQdec, void* dKdec, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream, float power);
 }  // namespace flare

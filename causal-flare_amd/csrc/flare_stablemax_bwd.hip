@@ -19,6 +19,11 @@
 // da (as the score gradient DS) and dv.  The contractions with Q, K, Q_dec and K_dec are
 // the token-causal backward's (launch_bwd_contract, with AL = alpha and C = alpha gz).
 // Everything is fp32 on VALU lanes; thread m of a 256-thread workgroup owns latent m.
+//
+// Shapes with M, Dk and Dv multiples of 16 (ar_backward_supported) take the softmax
+// backward instead (flare_ar_bwd.hip, with its MFMA contractions): its formulas hold
+// with e^a replaced by s(a) -- the scores become log2 s(a), and the score gradient
+// picks up d log s / da = p / (1 + |a|).  The kernels here serve the other shapes.
 #include "flare_common.h"
 #include "flare_internal.h"
 
@@ -85,7 +90,7 @@ __device__ __forceinline__ void latent_scores(const T* qrow, const T* kdrow, con
 template <typename T>
 __global__ __launch_bounds__(kSBT) void stablemax_bwd_forward(
     const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const T* __restrict__ Qd,
-    const T* __restrict__ Kd, const float* __restrict__ dY, int N, int H, int M, int Dk, int Dv, float scale,
+    const T* __restrict__ Kd, const T* __restrict__ dY, int N, int H, int M, int Dk, int Dv, float scale,
     float power, int CT, const float* __restrict__ pmax, const float* __restrict__ pden,
     const float* __restrict__ pnum, float* __restrict__ AL,
     float* __restrict__ Cc, float* __restrict__ Wt, float* __restrict__ GZ, float* __restrict__ Sx,
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(256) void stablemax_bwd_suffix(float* __restrict__ 
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kSBT) void stablemax_bwd_tokens(
-    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const float* __restrict__ dY, int N,
+    const T* __restrict__ Q, const T* __restrict__ K, const T* __restrict__ V, const T* __restrict__ dY, int N,
     int H, int M, int Dk, int Dv, float scale, float power, int CT, const float* __restrict__ Wt,
     const float* __restrict__ GZ, const float* __restrict__ Sx, const float* __restrict__ Sy,
     float* __restrict__ DS, T* __restrict__ dV) {
@@ -390,7 +395,7 @@ static int stablemax_bwd_chunk(int64_t M, int64_t Dk, int64_t Dv, bool sep) {
 template <typename T>
 static int run_stablemax_backward(const void* Q, const void* K, const void* V, const void* Qd, const void* Kd,
                                   int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
-                                  float scale, float power, const float* Y, const float* dY, void* dQ, void* dK,
+                                  float scale, float power, const void* Y, const void* dY, void* dQ, void* dK,
                                   void* dV, void* dQd, void* dKd, char* ws, const SbLayout& lay, int CT,
                                   hipStream_t st) {
     auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
@@ -405,7 +410,7 @@ static int run_stablemax_backward(const void* Q, const void* K, const void* V, c
     SbSmem s{CT, (int)Dk, (int)Dv, (int)M, Qd != nullptr};
     dim3 grid((unsigned)NC, (unsigned)BH);
     hipLaunchKernelGGL(stablemax_bwd_forward<T>, grid, dim3(kSBT), s.floats1() * sizeof(float), st, (const T*)Q,
-                       (const T*)K, (const T*)V, (const T*)Qd, (const T*)Kd, dY, (int)N, (int)H, (int)M,
+                       (const T*)K, (const T*)V, (const T*)Qd, (const T*)Kd, (const T*)dY, (int)N, (int)H, (int)M,
                        (int)Dk, (int)Dv, scale, power, CT, F(lay.off_pm), F(lay.off_pd), F(lay.off_pn), F(lay.off_al),
                        F(lay.off_c), F(lay.off_w), F(lay.off_gz), F(lay.off_sx), F(lay.off_sy));
     if ((rc = check_launch("stablemax_bwd_forward"))) return rc;
@@ -414,10 +419,10 @@ static int run_stablemax_backward(const void* Q, const void* K, const void* V, c
                        F(lay.off_sx), F(lay.off_sy), (int)BH, (int)NC, (int)M, (int)Dv);
     if ((rc = check_launch("stablemax_bwd_suffix"))) return rc;
     hipLaunchKernelGGL(stablemax_bwd_tokens<T>, grid, dim3(kSBT), s.floats3() * sizeof(float), st, (const T*)Q,
-                       (const T*)K, (const T*)V, dY, (int)N, (int)H, (int)M, (int)Dk, (int)Dv, scale, power, CT,
+                       (const T*)K, (const T*)V, (const T*)dY, (int)N, (int)H, (int)M, (int)Dk, (int)Dv, scale, power, CT,
                        F(lay.off_w), F(lay.off_gz), F(lay.off_sx), F(lay.off_sy), F(lay.off_ds), (T*)dV);
     if ((rc = check_launch("stablemax_bwd_tokens"))) return rc;
-    if ((rc = launch_bwd_gy(dY, Y, FLARE_F32, B, N, H, Dv, F(lay.off_gy), st))) return rc;
+    if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, F(lay.off_gy), st))) return rc;
     return launch_bwd_contract(Q, K, Qd, Kd, dtype, B, N, H, M, Dk, scale, F(lay.off_ds), F(lay.off_al),
                                F(lay.off_c), F(lay.off_gy), dQ, dK, dQd, dKd, F(lay.off_p1), F(lay.off_p2), st);
 }
@@ -430,13 +435,14 @@ extern "C" {
 
 size_t flare_stablemax_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk,
                                                int64_t Dv, int separate_decoder) {
+    if (ar_backward_supported(M, Dk, Dv)) return ar_backward_workspace(B, N, H, M, Dk, Dv);
     const int CT = stablemax_bwd_chunk(M, Dk, Dv, separate_decoder != 0);
     return SbLayout(B, N, H, M, Dk, Dv, CT).total;
 }
 
 int flare_stablemax_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec,
                              int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
-                             float scale, float power, const float* Y, const float* dY, void* dQ, void* dK,
+                             float scale, float power, const void* Y, const void* dY, void* dQ, void* dK,
                              void* dV, void* dQdec, void* dKdec, void* workspace, size_t workspace_bytes,
                              void* stream) {
     FLARE_REQUIRE(Q && K && V && Y && dY && dQ && dK && dV, "stablemax_backward: null pointer");
@@ -447,6 +453,18 @@ int flare_stablemax_backward(const void* Q, const void* K, const void* V, const 
     FLARE_REQUIRE(power > 0.0f && power < 1e30f, "stablemax_backward: power must be positive and finite");
     FLARE_REQUIRE((Qdec == nullptr) == (dQdec == nullptr) && (Kdec == nullptr) == (dKdec == nullptr),
                   "stablemax_backward: a separate decoder tensor needs its gradient buffer");
+    hipStream_t st = (hipStream_t)stream;
+    FLARE_REQUIRE(dtype == FLARE_F32 || dtype == FLARE_BF16 || dtype == FLARE_F16,
+                  "stablemax_backward: unknown dtype code %d", dtype);
+    if (ar_backward_supported(M, Dk, Dv)) {
+        const size_t need = ar_backward_workspace(B, N, H, M, Dk, Dv);
+        if (!workspace || workspace_bytes < need) {
+            set_error("stablemax_backward: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+            return FLARE_ERR_WORKSPACE;
+        }
+        return ar_backward_run(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, Y, dY, dQ, dK, dV, dQdec,
+                               dKdec, workspace, workspace_bytes, st, power);
+    }
     const int CT = stablemax_bwd_chunk(M, Dk, Dv, Qdec != nullptr);
     const SbLayout lay(B, N, H, M, Dk, Dv, CT);
     if (!workspace || workspace_bytes < lay.total) {
@@ -454,7 +472,6 @@ int flare_stablemax_backward(const void* Q, const void* K, const void* V, const 
         return FLARE_ERR_WORKSPACE;
     }
     char* ws = (char*)workspace;
-    hipStream_t st = (hipStream_t)stream;
 #define FLARE_SB(TY)                                                                                              \
     return run_stablemax_backward<TY>(Q, K, V, Qdec, Kdec, dtype, B, N, H, M, Dk, Dv, scale, power, Y, dY, dQ, dK, \
                                       dV, dQdec, dKdec, ws, lay, CT, st)

@@ -147,16 +147,18 @@ int flare_stablemax_forward(const void* Q, const void* K, const void* V, const v
  * (autoregressive/stablemax_triton.py:1981-2420): gradients of sum(Y * dY) with
  * respect to Q, K, V and the separate decoder tensors.  Inputs as the forward's
  * (compute dtype `dtype`; Qdec / Kdec NULL when they are K / Q, whose gradients
- * then carry the decoder share), Y and dY fp32 [B, N, H, Dv]; dQ, dK, dV, dQdec,
- * dKdec in `dtype` (dQdec / dKdec NULL exactly when Qdec / Kdec are).  M <= 256,
- * Dk, Dv <= 256.  Workspace of flare_stablemax_backward_workspace_size bytes
- * (separate_decoder: Qdec != NULL).  fp32 arithmetic.
+ * then carry the decoder share), Y and dY [B, N, H, Dv] in `dtype`; dQ, dK, dV,
+ * dQdec, dKdec in `dtype` (dQdec / dKdec NULL exactly when Qdec / Kdec are).
+ * M <= 256, Dk, Dv <= 256.  Workspace of flare_stablemax_backward_workspace_size
+ * bytes (separate_decoder: Qdec != NULL), 256-byte aligned.  fp32 accumulation;
+ * M, Dk, Dv multiples of 16 run flare_ar_backward's kernels (bf16 / fp16
+ * contractions on MFMA).
  */
 size_t flare_stablemax_backward_workspace_size(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk,
                                                int64_t Dv, int separate_decoder);
 int flare_stablemax_backward(const void* Q, const void* K, const void* V, const void* Qdec, const void* Kdec,
                              int dtype, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv,
-                             float scale, float power, const float* Y, const float* dY, void* dQ, void* dK,
+                             float scale, float power, const void* Y, const void* dY, void* dQ, void* dK,
                              void* dV, void* dQdec, void* dKdec, void* workspace, size_t workspace_bytes,
                              void* stream);
 

@@ -164,3 +164,32 @@ def test_stablemax_backward_16bit_large_bank(dtype):
         got = _stablemax_grads_gpu(q, k, v, None, None, dy, 2.0, None, None)
         ref = O.stablemax_grads(q, k, v, dy, 2.0, None, None, None)
         _grad_check(got, ref, ("dQ", "dK", "dV"), dtype, None, f"stablemax backward {dtype} {M}x{D}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_stablemax_backward_other_shapes(dtype):
+    """M and D_score not multiples of 16: the chunked fp32 replay kernels (every
+    other shape runs the softmax backward's pipeline with log2 s(a) as scores)."""
+    B, N, H, M, D, Dv = 2, 70, 2, 40, 24, 32
+    _case("stablemax backward other shapes", dtype, M, D, Dv)
+    g = torch.Generator().manual_seed(93)
+    q = (torch.randn((H, M, D), generator=g) * D ** -0.5).to(dtype)
+    k, v = torch.randn((B, N, H, D), generator=g).to(dtype), torch.randn((B, N, H, Dv), generator=g).to(dtype)
+    dy = torch.randn((B, N, H, Dv), generator=g)
+    got = _stablemax_grads_gpu(q, k, v, None, None, dy, 3.0, None, None)
+    ref = O.stablemax_grads(q, k, v, dy, 3.0, None, None, None)
+    _grad_check(got, ref, ("dQ", "dK", "dV"), dtype, 3e-3, f"stablemax backward {dtype} {M}x{D}x{Dv}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_stablemax_backward_long_wide_scores(dtype):
+    """Many 32-token backward chunks and wide scores (|a| up to about 10, power 4:
+    weights spanning about 2^28), shared decoder."""
+    B, N, H, M, D = 1, 700, 2, 128, 64
+    _case("stablemax backward long", dtype)
+    q, k, v = seeded(95, B, N, H, M, D, D, dtype, q_std=2.5)   # a = scale k.q ~ N(0, 2.5^2)
+    g = torch.Generator().manual_seed(96)
+    dy = torch.randn((B, N, H, D), generator=g)
+    got = _stablemax_grads_gpu(q, k, v, None, None, dy, 4.0, None, None)
+    ref = O.stablemax_grads(q, k, v, dy, 4.0, None, None, None)
+    _grad_check(got, ref, ("dQ", "dK", "dV"), dtype, 3e-3, f"stablemax backward long {dtype}")
