@@ -34,10 +34,12 @@ HIP_FLAGS = [
 # Per-file additions.  chunk_prepare_tr: MFMA accumulators in VGPRs rather than AGPRs, so
 # that the exponentials read the scores (and the rare rescale reads U) without a
 # v_accvgpr_read per value each tile (measured: config 2 prepare 25.9 -> 23.8 us); the
-# backward's per-chunk kernels likewise (config 3 backward 21.5 -> 20.9 ms).
+# backward's per-chunk kernels (config 3 backward 21.5 -> 20.9 ms) and the decoder softmax
+# pass of separate decoder tensors (config-2 shape forward 0.127 -> 0.121 ms) likewise.
 FILE_FLAGS = {
     "flare_ar_prep.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "flare_ar_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "flare_ar_pc.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 
