@@ -346,15 +346,19 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
         lt[t] = t < nt ? L[rbase + (size_t)t * M + m] : __builtin_huge_valf();
         acc[t] = pm == kNegInf ? 0.0f : ex2(pm2 - lt[t]) * acc[t];
     }
+    // the chunk's scores of latent m, all loaded before the pair sums (one wait, not one
+    // per token)
     const float* scol = S + rbase + m;
+    float sv[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) sv[t] = t < nt ? scol[(size_t)t * M] : 0.0f;
 #pragma unroll
     for (int tb = 0; tb < kBT / 16; ++tb) {
         if (16 * tb >= nt) break;
         // tau < 16 tb: every t of the block is >= tau
-        float sn = scol[0];
+#pragma unroll
         for (int tau = 0; tau < 16 * tb; ++tau) {
-            const float s = sn;
-            sn = scol[(size_t)(tau + 1) * M];
+            const float s = sv[tau];
             const float* gr = gvt + tau * kGT + 16 * tb;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -367,15 +371,16 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
             }
         }
         // the diagonal block: tau in [16 tb, min(nt, 16 tb + 16))
-        const int tend = min(nt, 16 * tb + 16);
-        for (int tau = 16 * tb; tau < tend; ++tau) {
-            const float s = scol[(size_t)tau * M];
+#pragma unroll
+        for (int du = 0; du < 16; ++du) {
+            const int tau = 16 * tb + du;
+            if (tau >= nt) break;
+            const float s = sv[tau];
             const float* gr = gvt + tau * kGT + 16 * tb;
 #pragma unroll
-            for (int u = 0; u < 16; ++u) {
+            for (int u = du; u < 16; ++u) {
                 const int t = 16 * tb + u;
-                const float e = ex2(s - lt[t]) * gr[u];
-                acc[t] += t >= tau ? e : 0.0f;
+                acc[t] += ex2(s - lt[t]) * gr[u];
             }
         }
     }
@@ -848,8 +853,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 //                  - e^{s_tau m - L_tau m} R_tau m,
 // R_tau = sum_{t >= tau} e^{L_tau - L_t} c_t = c_tau + e^{L_tau - L_tau+1} R_tau+1,
 // written over s.  Thread m.  The first and last terms are formed in one
-// reverse pass over the chunk and parked in the chunk's L slots (L is not
-// needed after this kernel); the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
+// reverse pass over the chunk and kept in registers, with the chunk's scores; the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
 // runs per tau over 16-token blocks of t as in bwd_gz.  power > 0 (stablemax,
 // s2 = log2 s(a)): the gradient with respect to a is the one with respect to
 // log s(a) times d log s / da = p / (1 + |a|) = p 2^(-|s2| / p).
@@ -940,25 +944,30 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const float lend = lcol[(size_t)(nt - 1) * M];
     const float ysum = carry ? Ysum[((size_t)bh * NC + c) * M + m] : 0.0f;
     float R = 0.0f, lnext = 0.0f;
+    // the scores of latent m, and the first and last terms of its ds (in acc, whose
+    // v . X it replaces), kept in registers for the pair sums below
+    float sv[kBT];
+#pragma unroll
+    for (int t = 0; t < kBT; ++t) sv[t] = t < nt ? scol[(size_t)t * M] : 0.0f;
 #pragma unroll
     for (int t = kBT - 1; t >= 0; --t) {
         if (t < nt) {
             const size_t o = (size_t)t * M;
-            const float l = lcol[o], s = scol[o];
+            const float l = lcol[o], s = sv[t];
             R = ccol[o] + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
             lnext = l;
             float park = -ex2(s - l) * R;
             if (carry) park += ex2(s - lend) * (acc[t] - ysum);
-            lcol[o] = park;
+            acc[t] = park;
         }
     }
     float la[kBT];
 #pragma unroll
     for (int t = 0; t < kBT; ++t) la[t] = t < nt ? LA[rbase + (size_t)t * M + m] : __builtin_huge_valf();
-    float sn = scol[0];
-    for (int tau = 0; tau < nt; ++tau) {
-        const float s = sn;
-        if (tau + 1 < nt) sn = scol[(size_t)(tau + 1) * M];
+#pragma unroll
+    for (int tau = 0; tau < kBT; ++tau) {
+        if (tau >= nt) break;
+        const float s = sv[tau];
         const float* gr = gvt + tau * kGT;
         const int tb0 = tau >> 4;
         float sum = 0.0f;
@@ -982,7 +991,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
             }
         }
         const size_t o = (size_t)tau * M;
-        const float dlog = lcol[o] + sum;
+        const float dlog = acc[tau] + sum;
         scol[o] = power > 0.0f ? dlog * (power * ex2(-fabsf(s) / power)) : dlog;
     }
 }
