@@ -63,7 +63,7 @@ __device__ __forceinline__ void dma16(const bf16* src, bf16* wave_dst) {
 // swz(row, slot).  Each thread keeps the global addresses of its pieces and
 // advances them by TT rows per tile.  Rows at or past `rows_end` repeat row
 // rows_end - 1 (their scores are masked).
-template <int D, int NTHR>
+template <int D, int NTHR, int TT>
 struct TileDma {
     static constexpr int KC = D / 8;
     static constexpr int NK = TT * KC / NTHR;
@@ -95,13 +95,15 @@ struct TileDma {
 
 }  // namespace
 
-template <int M, int D, bool F16, bool MASK, bool SMX = false>
+template <int M, int D, bool F16, bool MASK, bool SMX = false, int TTK = TT>
 __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                           const bf16* __restrict__ V, int N, int H, float scale2,
                                                           int chunk, float* __restrict__ cmax,
                                                           float* __restrict__ cden, float* __restrict__ cnum,
                                                           const int32_t* __restrict__ tmask, float power) {
-    // SMX: the stablemax encoder (smx_log2 on the scores; power > 0), else the softmax one
+    // SMX: the stablemax encoder (smx_log2 on the scores; power > 0), else the softmax one.
+    // TTK: tokens per tile (32 for 32-token chunks, whose 64-token tiles would be half masked)
+    constexpr int TT = TTK;
     constexpr int NT = 2 * M;           // M / 32 waves
     constexpr int KS = D / 32;          // k-steps of the scores
     constexpr int DT = D / 16;          // value-column tiles
@@ -113,7 +115,7 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
     constexpr bool SPLIT = M >= 256;
     constexpr int NTD = SPLIT ? NT / 2 : NT;   // threads that issue the DMA and convert V
     constexpr int NCV = TT * D / 8 / NTD;
-    using Dma = TileDma<D, NTD>;
+    using Dma = TileDma<D, NTD, TT>;
     // K tiles j mod 3 and V tiles j mod 4 (DMA two tiles ahead; V of tile j is read
     // until iteration j + 1); bf16 inputs: V tiles j mod 2 converted to fp16
     __shared__ __attribute__((aligned(16))) bf16 ktl[3][TT * D];
@@ -443,9 +445,19 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
     const int64_t NC = (N + chunk - 1) / chunk;
     dim3 grid((unsigned)NC, (unsigned)(B * H));
     const float s2 = scale * kLog2e;
+    // 32-token chunks (the backward's): 32-token tiles, none of them half masked
+    const bool t32 = chunk == 32 && tmask == nullptr;
 #define FLARE_PREP_TR_T(MM, DD, F)                                                                           \
     do {                                                                                                     \
-        if (power > 0.0f)                                                                                    \
+        if (t32 && power > 0.0f)                                                                             \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true, 32>), grid, dim3(2 * MM), 0, stream, \
+                               (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
+                               cmax, cden, cnum, tmask, power);                                              \
+        else if (t32)                                                                                        \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, false, 32>), grid, dim3(2 * MM), 0, stream, \
+                               (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
+                               cmax, cden, cnum, tmask, 0.0f);                                               \
+        else if (power > 0.0f)                                                                               \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true>), grid, dim3(2 * MM), 0, stream,    \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
                                cmax, cden, cnum, tmask, power);                                              \
