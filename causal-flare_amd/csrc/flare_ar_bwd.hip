@@ -1221,12 +1221,22 @@ int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const vo
 #undef FLARE_CONTRACT
 }
 
+// The chunk starting states come from one walk over long chunks (chunk_prepare_tr's EMIT
+// instance) where the shapes allow it: the summaries and scan of those long chunks first.
+static bool bwd_states_walk(int dtype, int64_t M, int64_t Dk, int64_t Dv) {
+    return (dtype == FLARE_BF16 || dtype == FLARE_F16) && (mfma_phase_mask() & 1) && output_pc_enabled() &&
+           output_tr_enabled() && mfma_prepare_supported(dtype, M, Dk, Dv) && (M == 128 || M == 256);
+}
+
 struct BwdLayout {
-    int64_t NC, NG;
-    size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_la, off_c, off_gy, off_p1, off_p2, total;
+    int64_t NC, NG, seg, NCS;
+    size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_la, off_c, off_gy, off_p1, off_p2, off_gm, off_gd,
+        off_gn, total;
     BwdLayout(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
         NC = (N + kBT - 1) / kBT;
         NG = (N + kBGroup - 1) / kBGroup;
+        seg = default_chunk(B, N, H, M, Dv);   // the walk's chunk (a multiple of 64)
+        NCS = (N + seg - 1) / seg;
         const size_t BH = (size_t)B * H;
         size_t o = 0;
         auto take = [&](size_t floats) {
@@ -1245,6 +1255,9 @@ struct BwdLayout {
         off_gy = take(BH * N);
         off_p1 = take(BH * NG * M * Dk);
         off_p2 = take(BH * NG * M * Dk);
+        off_gm = take(BH * NCS * M);
+        off_gd = take(BH * NCS * M);
+        off_gn = take(BH * NCS * M * Dv);
         total = o + 256;
     }
 };
@@ -1276,12 +1289,27 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     const T* y = static_cast<const T*>(Yp);
     const T* dy = static_cast<const T*>(dYp);
     int rc;
-    // chunk starting states at the backward's chunk length
-    if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, kBT, pm, pd, pn, st, power)))
-        return rc;
-    if ((rc = launch_prefix_public(pm, pd, pn, BH, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr,
-                                   nullptr, st)))
-        return rc;
+    // chunk starting states at the backward's chunk length: from a walk over long chunks
+    // (their summaries and scan first), else the prepare and scan at 32 tokens
+    if (bwd_states_walk(dtype, M, Dk, Dv)) {
+        float* gm = reinterpret_cast<float*>(ws + lay.off_gm);
+        float* gd = reinterpret_cast<float*>(ws + lay.off_gd);
+        float* gn = reinterpret_cast<float*>(ws + lay.off_gn);
+        if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, lay.seg, gm, gd, gn, st, power)))
+            return rc;
+        if ((rc = launch_prefix_public(gm, gd, gn, BH, lay.NCS, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, st)))
+            return rc;
+        if ((rc = launch_states_tr(Q, K, V, B, N, H, M, Dk, scale, lay.seg, gm, gd, gn, pm, pd, pn,
+                                   dtype == FLARE_F16, st, power)))
+            return rc;
+    } else {
+        if ((rc = launch_prepare_public(Q, K, V, dtype, B, N, H, M, Dk, Dv, scale, kBT, pm, pd, pn, st, power)))
+            return rc;
+        if ((rc = launch_prefix_public(pm, pd, pn, BH, NC, M, Dv, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                       nullptr, st)))
+            return rc;
+    }
     const dim3 gc((unsigned)NC, (unsigned)BH);
     bool stats_mfma = false;
     if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {

@@ -95,15 +95,24 @@ struct TileDma {
 
 }  // namespace
 
-template <int M, int D, bool F16, bool MASK, bool SMX = false, int TTK = TT>
+template <int M, int D, bool F16, bool MASK, bool SMX = false, int TTK = TT, bool EMIT = false>
 __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict__ Q, const bf16* __restrict__ K,
                                                           const bf16* __restrict__ V, int N, int H, float scale2,
                                                           int chunk, float* __restrict__ cmax,
                                                           float* __restrict__ cden, float* __restrict__ cnum,
-                                                          const int32_t* __restrict__ tmask, float power) {
+                                                          const int32_t* __restrict__ tmask, float power,
+                                                          const float* __restrict__ s0max,
+                                                          const float* __restrict__ s0den,
+                                                          const float* __restrict__ s0num, int NC32) {
     // SMX: the stablemax encoder (smx_log2 on the scores; power > 0), else the softmax one.
     // TTK: tokens per tile (32 for 32-token chunks, whose 64-token tiles would be half masked)
+    // EMIT: the running state instead of a summary.  The workgroup starts from its chunk's
+    // exclusive prefix (s0max / s0den / s0num, [B*H, NC, M(, D)], from the scan) and writes
+    // the state at the start of every 32-token chunk k that starts inside it to slot k of
+    // cmax / cden / cnum ([B*H, NC32, M(, D)]): (R ln 2, den and U relative to 2^R) with R
+    // the lazy reference.  These are the backward's chunk starting states.
     constexpr int TT = TTK;
+    static_assert(!EMIT || TTK == 64, "the state is written at the two 32-token halves of a 64-token tile");
     constexpr int NT = 2 * M;           // M / 32 waves
     constexpr int KS = D / 32;          // k-steps of the scores
     constexpr int DT = D / 16;          // value-column tiles
@@ -168,6 +177,9 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
     f32x4 U[DT][2];
     // per latent m0 + 16 mt + c (replicated over g): reference R, this lane's max rt and den dl
     float R[2], rt[2], dl[2];
+    // EMIT: the reference and this lane's den in the middle of the last tile, and the
+    // rescale of U between its two halves
+    float Rmid[2] = {kNegInf, kNegInf}, dmid[2] = {0.0f, 0.0f}, g1[2] = {1.0f, 1.0f};
 
     // One pass over the chunk.  BF = false: fp16 E (<= 2^kLazy) against fp16 V (the fp16
     // inputs, or bf16 V converted in LDS); BF = true (bf16 inputs only, a rerun when the
@@ -192,10 +204,60 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
             rt[mt] = kNegInf;
             dl[mt] = 0.0f;
         }
+        // EMIT: the state at the start of 32-token chunk k: reference Rv, this lane's den dv
+        auto emit = [&](int k, const float (&Rv)[2], const float (&dv)[2]) __attribute__((always_inline)) {
+            if (k >= NC32 || 32 * k >= t_end) return;
+            const size_t sb = ((size_t)bh * NC32 + k) * M;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const float den = rows_sum4(dv[mt]);
+                const int m = m0 + 16 * mt + c;
+                if (g == 0) {
+                    cmax[sb + m] = Rv[mt] == kNegInf ? kNegInf : Rv[mt] * kLn2;
+                    cden[sb + m] = den;
+                }
+#pragma unroll
+                for (int di = 0; di < DT; ++di)
+                    *reinterpret_cast<f32x4*>(cnum + (sb + m) * D + 16 * di + 4 * g) = U[di][mt];
+            }
+        };
+        if constexpr (EMIT) {
+            // start from the chunk's exclusive prefix: reference R = its max (log2), den in
+            // the g = 0 lanes (the den is summed over the four lane rows), U relative to 2^R
+            const size_t pb = ((size_t)bh * NC + c_idx) * M;
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt) {
+                const int m = m0 + 16 * mt + c;
+                const float pd = s0den[pb + m];
+                R[mt] = pd > 0.0f ? s0max[pb + m] * kLog2e : kNegInf;
+                dl[mt] = (g == 0 && pd > 0.0f) ? pd : 0.0f;
+#pragma unroll
+                for (int di = 0; di < DT; ++di)
+                    U[di][mt] = pd > 0.0f ? *reinterpret_cast<const f32x4*>(s0num + (pb + m) * D + 16 * di + 4 * g)
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            emit(t_begin / 32, R, dl);
+        }
         // E of the previous tile in fp16, k-slot order tau(g, e): the B operand of U^T += V^T E
         f16x8 eh[KK][2];
         FLARE_WAIT_VMCNT((2 * Dma::NK));   // tile 0 has landed
         lds_barrier();
+        // EMIT, after the k-step kk of tile jp's product: the state at the start of the next
+        // 32-token chunk (the middle of tile jp, or its end), then U rescaled for the second
+        // half's reference
+        auto emit_half = [&](int jp, int kk) __attribute__((always_inline)) {
+            if (kk == 0) {
+                emit((t_begin + TT * jp) / 32 + 1, Rmid, dmid);
+                if (__any(g1[0] != 1.0f || g1[1] != 1.0f)) {
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+                        for (int di = 0; di < DT; ++di) U[di][mt] *= g1[mt];
+                }
+            } else {
+                emit((t_begin + TT * jp) / 32 + 2, R, dl);
+            }
+        };
         auto value_product = [&](int jp) __attribute__((always_inline)) {
             auto vread = [&](const bf16* base, int kk, int di) __attribute__((always_inline)) {
                 const bf16* p = base + vofs[di] + 32 * kk * D;
@@ -204,13 +266,15 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
             if constexpr (!BF) {
                 const bf16* vf = F16 ? vtl[jp & 3] : reinterpret_cast<const bf16*>(vhl[jp & 1]);
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk)
+                for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
                     for (int di = 0; di < DT; ++di) {
                         const f16x8 va = __builtin_bit_cast(f16x8, vread(vf, kk, di));
 #pragma unroll
                         for (int mt = 0; mt < 2; ++mt) U[di][mt] = mma(va, eh[kk][mt], U[di][mt]);
                     }
+                    if constexpr (EMIT) emit_half(jp, kk);
+                }
             } else {
                 bf16x8 hi[KK][2], lo[KK][2];
 #pragma unroll
@@ -220,7 +284,7 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
 #pragma unroll
                         for (int i = 0; i < 8; ++i) SPLIT2(bf16, (float)eh[kk][mt][i], hi[kk][mt][i], lo[kk][mt][i]);
 #pragma unroll
-                for (int kk = 0; kk < KK; ++kk)
+                for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
                     for (int di = 0; di < DT; ++di) {
                         const bf16x8 va = vread(vtl[jp & 3], kk, di);
@@ -230,6 +294,8 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                             U[di][mt] = mma(va, lo[kk][mt], U[di][mt]);
                         }
                     }
+                    if constexpr (EMIT) emit_half(jp, kk);
+                }
             }
         };
 
@@ -332,6 +398,63 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                 dl[mt] += es;
             }
         };
+        // EMIT: the same per 32-token half, so that the state in the middle of the tile has
+        // a reference of its own: a move in the first half rescales U and den at once; a
+        // move in the second half rescales den, and U only after the first half's product
+        // (by g1, in emit_half), as E of that half is relative to the new reference.
+        auto exps_emit = [&](f32x4 (&acc)[TI][2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                float mx[2];
+                bool need = false;
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    float x = max3_raw(acc[2 * hf][mt][0], acc[2 * hf][mt][1], acc[2 * hf][mt][2]);
+                    x = max3_raw(x, acc[2 * hf][mt][3], acc[2 * hf + 1][mt][0]);
+                    x = max3_raw(x, acc[2 * hf + 1][mt][1], acc[2 * hf + 1][mt][2]);
+                    x = fmaxf(x, acc[2 * hf + 1][mt][3]);
+                    mx[mt] = x * scale2;
+                    need |= mx[mt] > R[mt] + kLazy;
+                    if (hf == 1) g1[mt] = 1.0f;
+                }
+                if (__any(need)) {
+                    asm volatile("");
+#pragma unroll
+                    for (int mt = 0; mt < 2; ++mt) {
+                        const float m4 = rows_max4(mx[mt]);
+                        const bool mv = m4 > R[mt] + kLazy;
+                        const float Rn = mv ? m4 : R[mt];
+                        const float gam = mv ? exp2f_fast(R[mt] - Rn) : 1.0f;   // 0 when R = -inf
+                        R[mt] = Rn;
+                        dl[mt] *= gam;
+                        if (hf == 0) {
+#pragma unroll
+                            for (int di = 0; di < DT; ++di) U[di][mt] *= gam;
+                        } else {
+                            g1[mt] = gam;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < 2; ++mt) {
+                    const float nR = R[mt] == kNegInf ? kNegInf : -R[mt];
+                    float es = 0.0f;
+#pragma unroll
+                    for (int ti = 2 * hf; ti < 2 * hf + 2; ++ti)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const float e = exp2f_fast(fmaf(acc[ti][mt][r], scale2, nR));
+                            es += e;
+                            eh[hf][mt][4 * (ti & 1) + r] = (f16)e;
+                        }
+                    dl[mt] += es;
+                    if (hf == 0) {
+                        dmid[mt] = dl[mt];
+                        Rmid[mt] = R[mt];
+                    }
+                }
+            }
+        };
         // Iteration j issues the DMA of tile j + 2, converts V of tile j and runs, per wave,
         // ... S(j) E(j) | P(j) S(j+1) E(j+1) | ... (S scores, E exponentials, P the value
         // product).  The waves of the second half of a 256-latent workgroup place the
@@ -371,13 +494,13 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                 }
                 if constexpr (LATE) {
                     if (j > 0) {
-                        exps(acc);
+                        if constexpr (EMIT) exps_emit(acc); else exps(acc);
                         value_product(j - 1);
                     }
                     scores(j, acc);
                 } else {
                     scores(j, acc);
-                    exps(acc);
+                    if constexpr (EMIT) exps_emit(acc); else exps(acc);
                 }
                 // tile j + 1 has landed (tile j + 2 may still be in flight); every wave is done
                 // with the buffers that iteration j + 1 refills
@@ -385,7 +508,10 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
                 lds_barrier();   // no memory fence: it would wait for the DMA of tile j + 2
             }
             if constexpr (LATE) {
-                if (NS > 0) exps(acc);
+                if (NS > 0) {
+                    if constexpr (EMIT) exps_emit(acc);
+                    else exps(acc);
+                }
             }
         };
         if (M >= 256 && w >= M / 64) loop(std::true_type{});
@@ -396,6 +522,12 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
 
     if (tid == 0) redo_bf16 = 0;
     __syncthreads();
+    if constexpr (EMIT && !F16) {
+        // the running states of bf16 inputs: E as a bf16 hi + lo pair against bf16 V in one
+        // pass (no fp16 copy of V whose range could overflow, so no second pass)
+        pass(std::true_type{});
+        return;
+    }
     pass(std::false_type{});
     if constexpr (!F16) {
         // a bf16 value outside the fp16 range (or a non-finite input) left U non-finite:
@@ -411,6 +543,7 @@ __global__ __launch_bounds__(2 * M) void chunk_prepare_tr(const bf16* __restrict
         __syncthreads();
         if (redo_bf16) pass(std::true_type{});
     }
+    if constexpr (EMIT) return;
     // ---- the summary relative to the true chunk max
     const size_t sbase = ((size_t)bh * NC + c_idx) * M;
 #pragma unroll
@@ -452,23 +585,23 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
         if (t32 && power > 0.0f)                                                                             \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true, 32>), grid, dim3(2 * MM), 0, stream, \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask, power);                                              \
+                               cmax, cden, cnum, tmask, power, nullptr, nullptr, nullptr, 0);                                              \
         else if (t32)                                                                                        \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, false, 32>), grid, dim3(2 * MM), 0, stream, \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask, 0.0f);                                               \
+                               cmax, cden, cnum, tmask, 0.0f, nullptr, nullptr, nullptr, 0);                                               \
         else if (power > 0.0f)                                                                               \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true>), grid, dim3(2 * MM), 0, stream,    \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask, power);                                              \
+                               cmax, cden, cnum, tmask, power, nullptr, nullptr, nullptr, 0);                                              \
         else if (tmask != nullptr)                                                                           \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, true>), grid, dim3(2 * MM), 0, stream,           \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask, 0.0f);                                               \
+                               cmax, cden, cnum, tmask, 0.0f, nullptr, nullptr, nullptr, 0);                                               \
         else                                                                                                 \
             hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false>), grid, dim3(2 * MM), 0, stream,          \
                                (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2, (int)chunk, \
-                               cmax, cden, cnum, tmask, 0.0f);                                               \
+                               cmax, cden, cnum, tmask, 0.0f, nullptr, nullptr, nullptr, 0);                                               \
     } while (0)
 #define FLARE_PREP_TR(MM, DD)                        \
     do {                                             \
@@ -482,6 +615,42 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
 #undef FLARE_PREP_TR
 #undef FLARE_PREP_TR_T
     return check_launch("chunk_prepare_tr");
+}
+
+int launch_states_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t D, float scale, int64_t chunk, const float* s0max, const float* s0den,
+                     const float* s0num, float* smax, float* sden, float* snum, bool f16in, hipStream_t stream,
+                     float power) {
+    FLARE_REQUIRE(chunk > 0 && chunk % 64 == 0, "chunk_states: chunk must be a positive multiple of 64");
+    FLARE_REQUIRE((M == 128 || M == 256) && (D == 64 || D == 128),
+                  "chunk_states: unsupported M=%lld D=%lld", (long long)M, (long long)D);
+    const int64_t NC = (N + chunk - 1) / chunk;
+    const int NC32 = (int)((N + 31) / 32);
+    dim3 grid((unsigned)NC, (unsigned)(B * H));
+    const float s2 = scale * kLog2e;
+#define FLARE_STATES_T(MM, DD, F)                                                                            \
+    do {                                                                                                     \
+        if (power > 0.0f)                                                                                    \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, true, TT, true>), grid, dim3(2 * MM), 0,  \
+                               stream, (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2,    \
+                               (int)chunk, smax, sden, snum, nullptr, power, s0max, s0den, s0num, NC32);      \
+        else                                                                                                 \
+            hipLaunchKernelGGL((chunk_prepare_tr<MM, DD, F, false, false, TT, true>), grid, dim3(2 * MM), 0, \
+                               stream, (const bf16*)Q, (const bf16*)K, (const bf16*)V, (int)N, (int)H, s2,    \
+                               (int)chunk, smax, sden, snum, nullptr, 0.0f, s0max, s0den, s0num, NC32);       \
+    } while (0)
+#define FLARE_STATES(MM, DD)                         \
+    do {                                             \
+        if (f16in) FLARE_STATES_T(MM, DD, true);     \
+        else FLARE_STATES_T(MM, DD, false);          \
+    } while (0)
+    if (M == 128 && D == 64) FLARE_STATES(128, 64);
+    else if (M == 128 && D == 128) FLARE_STATES(128, 128);
+    else if (M == 256 && D == 64) FLARE_STATES(256, 64);
+    else FLARE_STATES(256, 128);
+#undef FLARE_STATES
+#undef FLARE_STATES_T
+    return check_launch("chunk_prepare_tr (states)");
 }
 
 int prepare_tr_attributes(int64_t M, int64_t D, bool f16in, hipFuncAttributes* attr, int* threads) {

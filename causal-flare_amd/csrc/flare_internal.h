@@ -73,6 +73,14 @@ int launch_prepare_tr(const void* Q, const void* K, const void* V, int64_t B, in
                       int64_t D, float scale, int64_t chunk, float* cmax, float* cden, float* cnum,
                       const int32_t* tmask, bool f16in, hipStream_t stream, float power = 0.0f);
 // Register, scratch and LDS use of the kernels the forward launches (profile=True).
+// The running state at the start of every 32-token chunk, [B*H, ceil(N/32), M(, D)]
+// (max in natural-log units, den and num relative to it), from one pass over chunks of
+// `chunk` tokens (a multiple of 64) that start from their exclusive prefixes s0*.  The
+// shapes of launch_prepare_tr.
+int launch_states_tr(const void* Q, const void* K, const void* V, int64_t B, int64_t N, int64_t H, int64_t M,
+                     int64_t D, float scale, int64_t chunk, const float* s0max, const float* s0den,
+                     const float* s0num, float* smax, float* sden, float* snum, bool f16in, hipStream_t stream,
+                     float power);
 int prepare_tr_attributes(int64_t M, int64_t D, bool f16in, hipFuncAttributes* attr, int* threads);
 int output_tr_attributes(int64_t M, int64_t D, bool sep, bool f16in, hipFuncAttributes* attr, int* threads);
 inline bool prepare_tr_enabled() {
