@@ -1228,6 +1228,14 @@ static bool bwd_states_walk(int dtype, int64_t M, int64_t Dk, int64_t Dv) {
            output_tr_enabled() && mfma_prepare_supported(dtype, M, Dk, Dv) && (M == 128 || M == 256);
 }
 
+// The walk's chunk: the forward's own, or FLARE_BWD_WALK_CHUNK tokens (rounded up to a
+// multiple of 64; read at every call, for tests of walks over many tiles and A/B runs).
+static int64_t bwd_walk_chunk(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv) {
+    const char* e = getenv("FLARE_BWD_WALK_CHUNK");
+    if (e && atoll(e) > 0) return ((atoll(e) + 63) / 64) * 64;
+    return default_chunk(B, N, H, M, Dv);
+}
+
 struct BwdLayout {
     int64_t NC, NG, seg, NCS;
     size_t off_pm, off_pd, off_pn, off_s, off_l, off_al, off_la, off_c, off_gy, off_p1, off_p2, off_gm, off_gd,
@@ -1235,7 +1243,7 @@ struct BwdLayout {
     BwdLayout(int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv) {
         NC = (N + kBT - 1) / kBT;
         NG = (N + kBGroup - 1) / kBGroup;
-        seg = default_chunk(B, N, H, M, Dv);   // the walk's chunk (a multiple of 64)
+        seg = bwd_walk_chunk(B, N, H, M, Dv);   // the walk's chunk (a multiple of 64)
         NCS = (N + seg - 1) / seg;
         const size_t BH = (size_t)B * H;
         size_t o = 0;

@@ -165,6 +165,31 @@ def test_backward_bf16_score_jump(M, D):
     _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 jump M={M} D={D}")
 
 
+@pytest.mark.parametrize("M,D,N,jumps", [(128, 64, 2500, ()), (256, 128, 1500, ()), (128, 64, 1500, (650, 700)),
+                                         (256, 128, 1100, (1000,))])
+def test_backward_bf16_long_walk(M, D, N, jumps, monkeypatch):
+    """The chunk starting states walked over long chunks (1024 tokens: 16 tiles each, as
+    config 3's 4096-token chunks hold 64): the running state written at every 32-token
+    chunk across tiles, with K rows scaled by 12 (scores up to about 8, past the lazy
+    references of many latents) that move a reference in the first (token 650 of its
+    tile's 640 .. 703) and the second half (700, 1000) of a tile.  (Rows scaled by 40 put
+    some gradients past the bf16 bar on every path, the fp32 kernels included: da = alpha
+    (gz - g . y) cancels where alpha peaks, against the saved bf16 y.)"""
+    _case("bwd_bf16_long_walk", M, D, N, jumps)
+    monkeypatch.setenv("FLARE_BWD_WALK_CHUNK", "1024")
+    Q, K, V, Qd, Kd, G = _inputs(23, 1, N, 2, M, D, D, torch.bfloat16, False, False)
+    Q = (Q.float() / math.sqrt(D)).to(torch.bfloat16)
+    if jumps:
+        K = K.float()
+        for t in jumps:
+            K[:, t] *= 12.0
+        K = K.to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    y, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    tol = 3e-2 if D >= 128 else 2e-2
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"bf16 long walk M={M} D={D} N={N} jumps={jumps}")
+
+
 @pytest.mark.parametrize("M,D,N", [(128, 64, 300), (256, 128, 200)])
 @pytest.mark.parametrize("sep", [(False, False), (True, True)])
 def test_backward_fp16(M, D, N, sep):

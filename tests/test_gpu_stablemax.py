@@ -182,11 +182,13 @@ def test_stablemax_backward_other_shapes(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_stablemax_backward_long_wide_scores(dtype):
+def test_stablemax_backward_long_wide_scores(dtype, monkeypatch):
     """Many 32-token backward chunks and wide scores (|a| up to about 10, power 4:
-    weights spanning about 2^28), shared decoder."""
+    weights spanning about 2^28), shared decoder; the chunk starting states walked over
+    256-token chunks (four tiles each)."""
     B, N, H, M, D = 1, 700, 2, 128, 64
     _case("stablemax backward long", dtype)
+    monkeypatch.setenv("FLARE_BWD_WALK_CHUNK", "256")
     q, k, v = seeded(95, B, N, H, M, D, D, dtype, q_std=2.5)   # a = scale k.q ~ N(0, 2.5^2)
     g = torch.Generator().manual_seed(96)
     dy = torch.randn((B, N, H, D), generator=g)
