@@ -250,6 +250,45 @@ __device__ __forceinline__ void gv_store(const float (&gv)[kGVJ], float* gvt) {
     for (int j = 0; j < kGVJ; ++j) gvt[(tq + j) * kGT + t] = gv[j];
 }
 
+// D[m][t] += sum_d P[m][d] r[t][d] over one 16 x 16 tile for an fp32 row of P (the
+// chunk's state rows, split into bf16 hi + lo) and a 16-bit token row r: each group of
+// four 32-column steps issues all its loads before its MFMAs, so that a wave waits for
+// the state once per 128 columns rather than once per 32.
+template <bool F16>
+__device__ __forceinline__ mfma::f32x4 state_row_mma(const float* __restrict__ prow, const mfma::bf16* __restrict__ rrow,
+                                                    bool tok_ok, int Dv, mfma::f32x4 d2) {
+    using namespace mfma;
+    int k0 = 0;
+    for (; k0 + 128 <= Dv; k0 += 128) {
+        float4 p[8];
+        bf16x8 rb[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            p[2 * kk] = ld4(prow + k0 + 32 * kk);
+            p[2 * kk + 1] = ld4(prow + k0 + 32 * kk + 4);
+            rb[kk] = tok_ok ? load8<bf16x8>(rrow + k0 + 32 * kk) : zero8();
+        }
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const float pv[8] = {p[2 * kk].x, p[2 * kk].y, p[2 * kk].z, p[2 * kk].w,
+                                 p[2 * kk + 1].x, p[2 * kk + 1].y, p[2 * kk + 1].z, p[2 * kk + 1].w};
+            bf16x8 ph, pl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+            d2 = mma_split<F16>(ph, pl, rb[kk], d2);
+        }
+    }
+    for (; k0 < Dv; k0 += 32) {
+        const float4 p0 = ld4(prow + k0), p1 = ld4(prow + k0 + 4);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        bf16x8 ph, pl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
+        d2 = mma_split<F16>(ph, pl, tok_ok ? load8<bf16x8>(rrow + k0) : zero8(), d2);
+    }
+    return d2;
+}
+
 // ---------------------------------------------------------------------------
 // bwd_gz: c_tm = alpha_tm gz_tm with
 //   gz_tm = e^{pm_m - L_tm} (g_t . pu_m) + sum_{tau <= t} e^{s_tau m - L_tm} (g_t . v_tau)
@@ -315,15 +354,7 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
                 for (int mt = w; mt < M / 16; mt += kBNT / 64) {
                     f32x4 d2 = f32x4{0.f, 0.f, 0.f, 0.f};
                     const float* prow = pnum + (((size_t)bh * NC + c) * M + 16 * mt + cl) * Dv + 8 * g4;
-                    for (int k0 = 0; k0 < Dv; k0 += 32) {
-                        const float4 p0 = ld4(prow + k0), p1 = ld4(prow + k0 + 4);
-                        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                        bf16x8 ph, pl;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
-                        const bf16x8 gb = t < nt ? load8<bf16x8>(grow + k0) : zero8();
-                        d2 = mma_split<std::is_same<T, __half>::value>(ph, pl, gb, d2);
-                    }
+                    d2 = state_row_mma<std::is_same<T, __half>::value>(prow, grow, t < nt, Dv, d2);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
                 }
@@ -915,15 +946,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
                 for (int mt = w; mt < M / 16; mt += kBNT / 64) {
                     f32x4 d2 = f32x4{0.f, 0.f, 0.f, 0.f};
                     const float* xrow = X + (((size_t)bh * NC + c) * M + 16 * mt + cl) * Dv + 8 * g4;
-                    for (int k0 = 0; k0 < Dv; k0 += 32) {
-                        const float4 p0 = ld4(xrow + k0), p1 = ld4(xrow + k0 + 4);
-                        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                        bf16x8 ph, pl;
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) SPLIT2(bf16, pv[e], ph[e], pl[e]);
-                        const bf16x8 vb = t < nt ? load8<bf16x8>(vrow + k0) : zero8();
-                        d2 = mma_split<std::is_same<T, __half>::value>(ph, pl, vb, d2);
-                    }
+                    d2 = state_row_mma<std::is_same<T, __half>::value>(xrow, vrow, t < nt, Dv, d2);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) gsv[(16 * mt + 4 * g4 + r) * 17 + cl] = d2[r];
                 }
