@@ -595,8 +595,9 @@ __global__ __launch_bounds__(256) void bwd_carry_kernel(float* __restrict__ a, f
 // G covers the causal 16 x 16 blocks (ib <= jb) of the chunk: thread
 // (u = tid % 16, v = tid / 16) owns pair (16 ib + u, 16 jb + v) of each, over
 // latent slabs of 64 staged in LDS.  The output, for value slabs of 64
-// (Dv <= 512), is accumulated by thread (col, rg) owning
+// (Dv <= 64 NSL), is accumulated by thread (col, rg) owning
 // dv[tau = rg + 4 r][64 sl + col]; the X term runs over latent slabs of 64.
+// NSL = 2 serves Dv <= 128 with a quarter of the accumulator registers of NSL = 8.
 // ---------------------------------------------------------------------------
 constexpr int kMaxVSlab = 8;
 constexpr int kTB = kBT / 16;                         // 16-token blocks per chunk
@@ -617,7 +618,7 @@ constexpr BlockPairs block_pairs() {
     return p;
 }
 
-template <typename T>
+template <typename T, int NSL>
 __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ S,
     const float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ X, T* __restrict__ dV) {
@@ -744,13 +745,13 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         }
     }
     const int col = tid & 63, rg = tid >> 6;
-    float acc[kMaxVSlab][kRT];
+    float acc[NSL][kRT];
 #pragma unroll
-    for (int sl = 0; sl < kMaxVSlab; ++sl)
+    for (int sl = 0; sl < NSL; ++sl)
 #pragma unroll
         for (int r = 0; r < kRT; ++r) acc[sl][r] = 0.0f;
 #pragma unroll
-    for (int sl = 0; sl < kMaxVSlab; ++sl) {
+    for (int sl = 0; sl < NSL; ++sl) {
         if (sl * kBSlab >= Dv) break;
         __syncthreads();
         stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, sl * kBSlab, min(kBSlab, Dv - sl * kBSlab), kBP);
@@ -832,7 +833,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
                 }
                 __syncthreads();
 #pragma unroll
-                for (int sl = 0; sl < kMaxVSlab; ++sl) {
+                for (int sl = 0; sl < NSL; ++sl) {
                     if (sl * kBSlab >= Dv) break;
 #pragma unroll
                     for (int r = 0; r < kRT; ++r) acc[sl][r] += uni[(rg + 4 * r) * Dv + sl * kBSlab + col];
@@ -849,7 +850,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
             }
             __syncthreads();
 #pragma unroll
-            for (int sl = 0; sl < kMaxVSlab; ++sl) {
+            for (int sl = 0; sl < NSL; ++sl) {
                 if (sl * kBSlab >= Dv) break;
                 if (sl * kBSlab + col >= Dv) continue;
                 const float* xr = xb + (size_t)m0 * Dv + sl * kBSlab + col;
@@ -866,7 +867,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
         }
     }
 #pragma unroll
-    for (int sl = 0; sl < kMaxVSlab; ++sl) {
+    for (int sl = 0; sl < NSL; ++sl) {
         if (sl * kBSlab >= Dv) break;
         const int d = sl * kBSlab + col;
         if (d >= Dv) continue;
@@ -1371,8 +1372,8 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_carry_kernel, dim3((unsigned)((cthreads + 255) / 256)), dim3(256), 0, st, pn, pd, L,
                        (int)N, (int)NC, (int)M, (int)Dv, BH * M);
     if ((rc = check_launch("bwd_carry_kernel"))) return rc;
-    hipLaunchKernelGGL(bwd_dv_kernel<T>, gc, dim3(kBNT), 0, st, dy, (int)N,
-                       (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
+    auto* dv_kernel = Dv <= 2 * kBSlab ? bwd_dv_kernel<T, 2> : bwd_dv_kernel<T, kMaxVSlab>;
+    hipLaunchKernelGGL(dv_kernel, gc, dim3(kBNT), 0, st, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd, power);
