@@ -269,15 +269,15 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
 // bwd_summary in flare_ar_bwd.hip), for chunks c >= 1 of 32 tokens:
 //     a_c[m][:] = sum_t w_tm g_t,   b_c[m] = sum_t w_tm c_tm,
 //     w_tm = 2^(Lpre_m - L_tm) alpha_tm   (Lpre = L at the last token of chunk c-1)
-// a is a contraction over tokens: w^T (bf16 hi and lo, computed by the thread of
-// latent m) and g^T (dY, exact) are staged transposed in LDS.
+// a is a contraction over tokens: each lane forms its own A operand (latent
+// row m, tokens 8 g .. 8 g + 7) from L, alpha and c as bf16 hi and lo; g^T (dY,
+// exact) is staged transposed in LDS.  b sums the lanes' 8-token parts.
 template <int MW, int DV, bool F16>
 __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__ dY, int N, int H,
                                                         const float* __restrict__ L, const float* __restrict__ AL,
                                                         const float* __restrict__ C, float* __restrict__ a_out,
                                                         float* __restrict__ b_out) {
     constexpr int M = 64 * MW, NJ = DV / 16;
-    __shared__ __attribute__((aligned(16))) bf16 wh[M * kDqTP], wlo[M * kDqTP];   // w^T hi, lo
     __shared__ __attribute__((aligned(16))) bf16 gt[DV * kDqTP];                  // g^T
     const int c = blockIdx.x, bh = blockIdx.y, NC = gridDim.x;
     if (c == 0) return;
@@ -286,30 +286,6 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
     const int t0 = c * 32, nt = min(32, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
     const size_t sbase = ((size_t)bh * NC + c) * M;
-    if (tid < M) {
-        const int m = tid;
-        const float lp = L[rbase - M + m];
-        float bsum = 0.0f;
-#pragma unroll
-        for (int t8 = 0; t8 < 4; ++t8) {
-            bf16x8 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int t = 8 * t8 + e;
-                float wv = 0.0f;
-                if (t < nt) {
-                    const size_t o = rbase + (size_t)t * M + m;
-                    const float f = __builtin_amdgcn_exp2f(lp - L[o]);
-                    wv = f * AL[o];
-                    bsum += f * C[o];
-                }
-                SPLIT2(bf16, wv, hi[e], lo[e]);
-            }
-            *reinterpret_cast<bf16x8*>(wh + m * kDqTP + 8 * t8) = hi;
-            *reinterpret_cast<bf16x8*>(wlo + m * kDqTP + 8 * t8) = lo;
-        }
-        b_out[sbase + m] = bsum;
-    }
     const size_t stride = (size_t)H * DV;
     for (int e = tid; e < DV * 8; e += 256) {
         const int d = e % DV, tq = e / DV;
@@ -321,19 +297,60 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
         }
         *reinterpret_cast<bf16x4*>(gt + d * kDqTP + 4 * tq) = gv;
     }
+    const int mw0 = w * 16 * MW;
+    bf16x8 ah[MW], alo[MW];
+#pragma unroll
+    for (int mi = 0; mi < MW; ++mi) {
+        const int m = mw0 + 16 * mi + cl;
+        const float lp = L[rbase - M + m];
+        float bsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int t = 8 * g + e;
+            float wv = 0.0f;
+            if (t < nt) {
+                const size_t o = rbase + (size_t)t * M + m;
+                const float f = __builtin_amdgcn_exp2f(lp - L[o]);
+                wv = f * AL[o];
+                bsum += f * C[o];
+            }
+            SPLIT2(bf16, wv, ah[mi][e], alo[mi][e]);
+        }
+        bsum += __shfl_xor(bsum, 16);
+        bsum += __shfl_xor(bsum, 32);
+        if (g == 0) b_out[sbase + m] = bsum;
+    }
     __syncthreads();
+    if constexpr (F16) {
+        // fp16 dY: each B tile split into its exact bf16 pair once, for all MW row tiles
+        // (the products of mma_split<true>, in its order)
+#pragma unroll
+        for (int nj = 0; nj < NJ; ++nj) {
+            const f16x8 bf = __builtin_bit_cast(f16x8, load8<bf16x8>(gt + (16 * nj + cl) * kDqTP + 8 * g));
+            bf16x8 bh, bl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) SPLIT2(bf16, (float)bf[e], bh[e], bl[e]);
+#pragma unroll
+            for (int mi = 0; mi < MW; ++mi) {
+                f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                acc = mma(ah[mi], bh, acc);
+                acc = mma(alo[mi], bh, acc);
+                acc = mma(ah[mi], bl, acc);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) a_out[(sbase + mw0 + 16 * mi + 4 * g + r) * DV + 16 * nj + cl] = acc[r];
+            }
+        }
+        return;
+    }
     bf16x8 bg[NJ];
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) bg[nj] = load8<bf16x8>(gt + (16 * nj + cl) * kDqTP + 8 * g);
-    const int mw0 = w * 16 * MW;
 #pragma unroll
     for (int mi = 0; mi < MW; ++mi) {
-        const int row = (mw0 + 16 * mi + cl) * kDqTP + 8 * g;
-        const bf16x8 a0 = load8<bf16x8>(wh + row), a1 = load8<bf16x8>(wlo + row);
 #pragma unroll
         for (int nj = 0; nj < NJ; ++nj) {
             f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-            acc = mma_split<F16>(a0, a1, bg[nj], acc);
+            acc = mma_split<false>(ah[mi], alo[mi], bg[nj], acc);
             // rows m = mw0 + 16 mi + 4 g + r, column 16 nj + cl
 #pragma unroll
             for (int r = 0; r < 4; ++r) a_out[(sbase + mw0 + 16 * mi + 4 * g + r) * DV + 16 * nj + cl] = acc[r];
