@@ -250,6 +250,28 @@ __device__ __forceinline__ void gv_store(const float (&gv)[kGVJ], float* gvt) {
     for (int j = 0; j < kGVJ; ++j) gvt[(tq + j) * kGT + t] = gv[j];
 }
 
+// 16-bit inputs, Dv a multiple of 32: GV on the MFMA straight from the token rows
+// (exact products, fp32 sums), one 16 x 16 tile of (t, tau) per wave, stored
+// transposed into gvt; the tile t < 16 <= tau, which no t >= tau reads, is zeroed.
+template <bool F16>
+__device__ __forceinline__ void gv_mfma(const mfma::bf16* __restrict__ dY, const mfma::bf16* __restrict__ V, int b,
+                                        int t0, int nt, int h, int N, int H, int Dv, float* gvt) {
+    using namespace mfma;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g4 = lane >> 4, cl = lane & 15;
+    const int ti = w >> 1, tj = w & 1;
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (ti >= tj) {
+        const int t = 16 * ti + cl, tau = 16 * tj + cl;
+        const bf16* grow = dY + tok_index(b, t0 + min(t, nt - 1), h, N, H, Dv) + 8 * g4;
+        const bf16* vrow = V + tok_index(b, t0 + min(tau, nt - 1), h, N, H, Dv) + 8 * g4;
+#pragma unroll 4
+        for (int k0 = 0; k0 < Dv; k0 += 32)
+            d = mma_in<F16>(t < nt ? load8<bf16x8>(grow + k0) : zero8(), tau < nt ? load8<bf16x8>(vrow + k0) : zero8(), d);
+    }
+    // D[t = 16 ti + 4 g4 + r][tau = 16 tj + cl]
+    *reinterpret_cast<float4*>(gvt + (16 * tj + cl) * kGT + 16 * ti + 4 * g4) = make_float4(d[0], d[1], d[2], d[3]);
+}
+
 // D[m][t] += sum_d P[m][d] r[t][d] over one 16 x 16 tile for an fp32 row of P (the
 // chunk's state rows, split into bf16 hi + lo) and a 16-bit token row r: each group of
 // four 32-column steps issues all its loads before its MFMAs, so that a wave waits for
@@ -323,14 +345,19 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
 #pragma unroll
     for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
     const float* pu = pnum + (((size_t)bh * NC + c) * M + (act ? m : 0)) * Dv;
-    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+    if constexpr (kBf16) {
+        if (mf)
+            gv_mfma<std::is_same<T, __half>::value>(reinterpret_cast<const mfma::bf16*>(dY),
+                                                    reinterpret_cast<const mfma::bf16*>(V), b, t0, nt, h, N, H, Dv, gvt);
+    }
+    for (int d0 = 0; d0 < (mf ? 0 : Dv); d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
         stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
-        if (act && !mf) {
+        if (act) {
             for (int d = 0; d < ds; d += 4) {
                 const float4 p = ld4(pu + d0 + d);
 #pragma unroll
@@ -366,7 +393,7 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
             }
         }
     }
-    gv_store(gv, gvt);
+    if (!mf) gv_store(gv, gvt);
     __syncthreads();
     if (!act) return;
     const float pm = pmax[((size_t)bh * NC + c) * M + m];
@@ -916,14 +943,19 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 #pragma unroll
     for (int t = 0; t < kBT; ++t) acc[t] = 0.0f;
     const float* xr = X + (((size_t)bh * NC + c) * M + (act ? m : 0)) * Dv;
-    for (int d0 = 0; d0 < Dv; d0 += kBSlab) {
+    if constexpr (kBf16) {
+        if (mf)
+            gv_mfma<std::is_same<T, __half>::value>(reinterpret_cast<const mfma::bf16*>(dY),
+                                                    reinterpret_cast<const mfma::bf16*>(V), b, t0, nt, h, N, H, Dv, gvt);
+    }
+    for (int d0 = 0; d0 < (mf ? 0 : Dv); d0 += kBSlab) {
         const int ds = min(kBSlab, Dv - d0);
         __syncthreads();
         stage_slab(gs, dY, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         stage_slab(vs, V, b, t0, nt, h, N, H, Dv, d0, ds, kGT);
         __syncthreads();
         gv_accumulate(gv, gs, vs, ds);
-        if (act && carry && !mf) {
+        if (act && carry) {
             for (int d = 0; d < ds; d += 4) {
                 const float4 p = ld4(xr + d0 + d);
 #pragma unroll
@@ -959,7 +991,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
             }
         }
     }
-    gv_store(gv, gvt);
+    if (!mf) gv_store(gv, gvt);
     __syncthreads();
     if (!act) return;
     float* scol = S + rbase + m;
