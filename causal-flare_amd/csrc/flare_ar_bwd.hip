@@ -28,7 +28,7 @@
 //
 // Kernels, in launch order:
 //   bwd_stats    s, L, alpha per (t, m)                   grid (NC, BH)
-//   bwd_gz       c = alpha gz per (t, m)                  grid (NC, BH)
+//   bwd_gz       gz per (t, m), into C                    grid (NC, BH)
 //   bwd_gy       gy = dY . Y per token                    grid (tokens)
 //   bwd_summary  per-chunk terms of X, Y                  grid (NC, BH)
 //   bwd_carry    reverse scan over chunks -> X_c, Y_c     grid (BH M Dv/4)
@@ -312,7 +312,7 @@ __device__ __forceinline__ mfma::f32x4 state_row_mma(const float* __restrict__ p
 }
 
 // ---------------------------------------------------------------------------
-// bwd_gz: c_tm = alpha_tm gz_tm with
+// bwd_gz: gz_tm (stored in C; alpha_tm gz_tm is formed where needed) with
 //   gz_tm = e^{pm_m - L_tm} (g_t . pu_m) + sum_{tau <= t} e^{s_tau m - L_tm} (g_t . v_tau)
 // (pm, pu: the chunk's starting max and numerator, pu relative to pm).
 // Thread m; the pair sum runs over 16-token blocks of t: blocks wholly after
@@ -323,7 +323,7 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv,
     const float* __restrict__ pmax, const float* __restrict__ pnum, const float* __restrict__ S,
-    const float* __restrict__ L, const float* __restrict__ AL, float* __restrict__ C) {
+    const float* __restrict__ L, float* __restrict__ C) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     // dY and V slabs; afterwards (bf16) g_t . pu_m of one 16-token half as [m][17]
     __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kBNT) void bwd_gz_kernel(
     }
 #pragma unroll
     for (int t = 0; t < kBT; ++t)
-        if (t < nt) C[rbase + (size_t)t * M + m] = AL[rbase + (size_t)t * M + m] * acc[t];
+        if (t < nt) C[rbase + (size_t)t * M + m] = acc[t];
 }
 
 // ---------------------------------------------------------------------------
@@ -513,14 +513,14 @@ __device__ __forceinline__ void outer8(float (&acc)[8][8], const float* a, const
 // bwd_summary: chunk c's own terms of the reverse scan, relative to
 // Lpre = L at the last token of chunk c-1 (chunk 0 has none):
 //   a_c,m = sum_{t in c} w_tm g_t,  b_c,m = sum_{t in c} w_tm gz_tm,
-//   w_tm = e^{Lpre_m - L_tm} alpha_tm  (c_tm = alpha_tm gz_tm is stored).
+//   w_tm = e^{Lpre_m - L_tm} alpha_tm = 2^(Lpre_m - LA_tm)  (gz is stored in C).
 // a overwrites the chunk's starting numerator, b its starting den.
 // Thread (mi = tid % 32, di = tid / 32) owns a[8 mi .. +8][d0 + 8 di .. +8].
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_summary_kernel(
     const T* __restrict__ dY, int N, int H, int M, int Dv, const float* __restrict__ L,
-    const float* __restrict__ AL, const float* __restrict__ C, float* __restrict__ a_out,
+    const float* __restrict__ LA, const float* __restrict__ C, float* __restrict__ a_out,
     float* __restrict__ b_out) {
     __shared__ __attribute__((aligned(16))) float wl[kBT * 256];
     __shared__ __attribute__((aligned(16))) float gs[kBT * kGT];
@@ -530,13 +530,13 @@ __global__ __launch_bounds__(kBNT) void bwd_summary_kernel(
     const int t0 = c * kBT, nt = min(kBT, N - t0);
     const size_t rbase = ((size_t)bh * N + t0) * M;
     const float* lpre = L + rbase - M;
-    for (int e = tid; e < nt * M; e += kBNT) wl[e] = ex2(lpre[e % M] - L[rbase + e]) * AL[rbase + e];
+    for (int e = tid; e < nt * M; e += kBNT) wl[e] = ex2(lpre[e % M] - LA[rbase + e]);
     const size_t sbase = ((size_t)bh * NC + c) * M;
     if (tid < M) {
         float sum = 0.0f;
         for (int t = 0; t < nt; ++t) {
             const size_t o = rbase + (size_t)t * M + tid;
-            sum += ex2(lpre[tid] - L[o]) * C[o];
+            sum += ex2(lpre[tid] - LA[o]) * C[o];
         }
         b_out[sbase + tid] = sum;
     }
@@ -911,7 +911,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 //                  + sum_{t >= tau} e^{s_tau m - L_tm} alpha_tm GV[t][tau]
 //                  - e^{s_tau m - L_tau m} R_tau m,
 // R_tau = sum_{t >= tau} e^{L_tau - L_t} c_t = c_tau + e^{L_tau - L_tau+1} R_tau+1,
-// written over s.  Thread m.  The first and last terms are formed in one
+// c_t = alpha_t gz_t = 2^(L_t - LA_t) gz_t (C holds gz), written over s.  Thread m.  The first and last terms are formed in one
 // reverse pass over the chunk and kept in registers, with the chunk's scores; the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
 // runs per tau over 16-token blocks of t as in bwd_gz.  power > 0 (stablemax,
 // s2 = log2 s(a)): the gradient with respect to a is the one with respect to
@@ -1002,24 +1002,24 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     float R = 0.0f, lnext = 0.0f;
     // the scores of latent m, and the first and last terms of its ds (in acc, whose
     // v . X it replaces), kept in registers for the pair sums below
-    float sv[kBT];
+    float sv[kBT], la[kBT];
 #pragma unroll
-    for (int t = 0; t < kBT; ++t) sv[t] = t < nt ? scol[(size_t)t * M] : 0.0f;
+    for (int t = 0; t < kBT; ++t) {
+        sv[t] = t < nt ? scol[(size_t)t * M] : 0.0f;
+        la[t] = t < nt ? LA[rbase + (size_t)t * M + m] : __builtin_huge_valf();
+    }
 #pragma unroll
     for (int t = kBT - 1; t >= 0; --t) {
         if (t < nt) {
             const size_t o = (size_t)t * M;
             const float l = lcol[o], s = sv[t];
-            R = ccol[o] + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
+            R = ex2(l - la[t]) * ccol[o] + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
             lnext = l;
             float park = -ex2(s - l) * R;
             if (carry) park += ex2(s - lend) * (acc[t] - ysum);
             acc[t] = park;
         }
     }
-    float la[kBT];
-#pragma unroll
-    for (int t = 0; t < kBT; ++t) la[t] = t < nt ? LA[rbase + (size_t)t * M + m] : __builtin_huge_valf();
 #pragma unroll
     for (int tau = 0; tau < kBT; ++tau) {
         if (tau >= nt) break;
@@ -1054,7 +1054,8 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 
 // ---------------------------------------------------------------------------
 // bwd_dk: per token, dK_t = scale sum_m (ds_tm Q_m [+ da_tm Kd_m when Qd = K])
-// and dQd_t = scale sum_m da_tm Kd_m (separate Qd); da_tm = c_tm - alpha_tm gy_t.
+// and dQd_t = scale sum_m da_tm Kd_m (separate Qd); da_tm = alpha_tm (gz_tm - gy_t)
+// (score_grad_da).
 // Thread (col, tg) owns tokens tg + 4 r (r < kDkTok / 4) and columns col + 64 k.
 // ---------------------------------------------------------------------------
 constexpr int kDkTok = 32;     // tokens per bwd_dk workgroup
@@ -1063,7 +1064,7 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
     const T* __restrict__ Q, const T* __restrict__ Kd, int N, int H, int M, int Dk, float scale, bool sep_q,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
-    const float* __restrict__ gy, T* __restrict__ dK, T* __restrict__ dQd) {
+    const float* __restrict__ gy, bool cgz, T* __restrict__ dK, T* __restrict__ dQd) {
     __shared__ __attribute__((aligned(16))) float dsl[kDkTok * 256];
     __shared__ __attribute__((aligned(16))) float dal[kDkTok * 256];
     const int bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
@@ -1073,7 +1074,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
         const int i = e / M;
         const bool ok = i < nt;
         dsl[e] = ok ? DS[rbase + e] : 0.0f;
-        dal[e] = ok ? C[rbase + e] - AL[rbase + e] * gy[(size_t)bh * N + t0 + i] : 0.0f;
+        dal[e] = ok ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
     }
     __syncthreads();
     const int col = tid & 63, tg = tid >> 6;
@@ -1124,7 +1125,7 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
     const T* __restrict__ K, const T* __restrict__ Qd, int N, int H, int M, int Dk, bool sep_k,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
-    const float* __restrict__ gy, float* __restrict__ P1, float* __restrict__ P2) {
+    const float* __restrict__ gy, bool cgz, float* __restrict__ P1, float* __restrict__ P2) {
     __shared__ __attribute__((aligned(16))) float dsl[kBTok * 256];
     __shared__ __attribute__((aligned(16))) float dal[kBTok * 256];
     __shared__ __attribute__((aligned(16))) float kt[kBTok * kGT];
@@ -1147,7 +1148,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
             const int i = e / M;
             const bool ok = i < nt;
             dsl[e] = ok ? DS[rbase + e] : 0.0f;
-            dal[e] = ok ? C[rbase + e] - AL[rbase + e] * gy[(size_t)bh * N + t0 + i] : 0.0f;
+            dal[e] = ok ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
         }
         for (int e = tid; e < kBTok * 64; e += kBNT) {
             const int i = e >> 6, dd = e & 63, d = d0 + dd;
@@ -1201,26 +1202,26 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict
 template <typename T>
 static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, bool sep_q, bool sep_k, int64_t B,
                            int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                           const float* C, const float* gy, void* dQ, void* dK, void* dQd, void* dKd, float* P1,
-                           float* P2, hipStream_t st) {
+                           const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQd, void* dKd,
+                           float* P1, float* P2, hipStream_t st) {
     const int64_t BH = B * H, NG = (N + kBGroup - 1) / kBGroup;
     int rc;
     constexpr bool kHalf = std::is_same<T, __half>::value;
     constexpr bool k16 = std::is_same<T, __hip_bfloat16>::value || kHalf;
     if (k16 && bwd_dk_mfma_supported(M, Dk)) {
-        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dK, dQd, kHalf, st)))
+        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dK, dQd, kHalf, st)))
             return rc;
     } else {
         hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT),
                            0, st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
-                           static_cast<T*>(dK), static_cast<T*>(dQd));
+                           cgz, static_cast<T*>(dK), static_cast<T*>(dQd));
         if ((rc = check_launch("bwd_dk_kernel"))) return rc;
     }
     if (k16 && bwd_dq_mfma_supported(M, Dk)) {
-        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, P1, P2, kHalf, st))) return rc;
+        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, cgz, P1, P2, kHalf, st))) return rc;
     } else {
         hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
-                           dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, P1, P2);
+                           dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, cgz, P1, P2);
         if ((rc = check_launch("bwd_dq_kernel"))) return rc;
     }
     const int64_t red = H * M * Dk;
@@ -1265,12 +1266,12 @@ int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N
 
 int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
                         int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                        const float* C, const float* gy, void* dQ, void* dK, void* dQdec, void* dKdec, float* P1,
-                        float* P2, hipStream_t st) {
+                        const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQdec, void* dKdec,
+                        float* P1, float* P2, hipStream_t st) {
     const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
 #define FLARE_CONTRACT(TY)                                                                                       \
     return launch_contract((const TY*)Q, (const TY*)K, (const TY*)(sep_q ? Qdec : K), (const TY*)(sep_k ? Kdec : Q), \
-                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, dQ, dK, dQdec, dKdec, P1, P2, st)
+                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dQ, dK, dQdec, dKdec, P1, P2, st)
     if (dtype == FLARE_BF16) FLARE_CONTRACT(__hip_bfloat16);
     if (dtype == FLARE_F16) FLARE_CONTRACT(__half);
     FLARE_CONTRACT(float);
@@ -1387,17 +1388,17 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
                            (int)Dk, scale, shared, pm, pd, S, L, AL, LA, power);
     if ((rc = check_launch("bwd_stats_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
-                       L, AL, C);
+                       L, C);
     if ((rc = check_launch("bwd_gz_kernel"))) return rc;
     if ((rc = launch_gy(dy, y, B, N, H, Dv, gy, st))) return rc;
     static_assert(kBT == 32, "the MFMA chunk summary assumes 32-token chunks");
     if ((std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) &&
         bwd_summary_mfma_supported(M, Dv)) {
-        if ((rc = launch_summary_mfma(dy, B, N, H, M, Dv, L, AL, C, pn, pd, std::is_same<T, __half>::value, st)))
+        if ((rc = launch_summary_mfma(dy, B, N, H, M, Dv, L, LA, C, pn, pd, std::is_same<T, __half>::value, st)))
             return rc;
     } else {
         hipLaunchKernelGGL(bwd_summary_kernel<T>, gc, dim3(kBNT), 0, st, dy,
-                           (int)N, (int)H, (int)M, (int)Dv, L, AL, C, pn, pd);
+                           (int)N, (int)H, (int)M, (int)Dv, L, LA, C, pn, pd);
         if ((rc = check_launch("bwd_summary_kernel"))) return rc;
     }
     const int64_t cthreads = BH * M * (Dv / 4);
@@ -1410,8 +1411,8 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd, power);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
-    return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, dQ, dK, dQd, dKd, P1,
-                           P2, st);
+    return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, true, dQ, dK, dQd, dKd,
+                           P1, P2, st);
 }
 
 bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv) {

@@ -1,7 +1,7 @@
 // flare_bwd_mfma.hip -- bf16 MFMA contractions of the FLARE backward on gfx950.
 //
 // dK (and dQ_dec) are contractions over the latent bank of the score gradients
-// ds and da = c - alpha gy (fp32, [B*H, N, M]) with the bf16 latent tensors:
+// ds and da = alpha (gz - gy) (fp32, [B*H, N, M]; C holds alpha gz or gz, see score_grad_da) with the bf16 latent tensors:
 //     dK_t   = scale sum_m (ds_tm Q_m  [+ da_tm Kd_m when Qd = K])
 //     dQd_t  = scale sum_m  da_tm Kd_m                  (separate Qd)
 // (the per-token loop of bwd_dk in flare_ar_bwd.hip, which stays the fp32 /
@@ -31,7 +31,7 @@ template <int DK, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, const bf16* __restrict__ Kd, int N,
                                                    int H, int M, float scale, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
-                                                   const float* __restrict__ gy, __hip_bfloat16* __restrict__ dK,
+                                                   const float* __restrict__ gy, bool cgz, __hip_bfloat16* __restrict__ dK,
                                                    __hip_bfloat16* __restrict__ dQd) {
     constexpr int NJ = DK / 16;
     __shared__ __attribute__((aligned(16))) bf16 qt[DK * kDkLP];                 // Q^T[d][m]
@@ -87,8 +87,8 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
                 for (int e = 0; e < 4; ++e) {
                     ds[e] = s0[e];
                     ds[4 + e] = s1[e];
-                    da[e] = c0[e] - a0[e] * gyt[ti];
-                    da[4 + e] = c1[e] - a1[e] * gyt[ti];
+                    da[e] = score_grad_da(c0[e], a0[e], gyt[ti], cgz);
+                    da[4 + e] = score_grad_da(c1[e], a1[e], gyt[ti], cgz);
                 }
             } else {
 #pragma unroll
@@ -156,7 +156,7 @@ template <int MW, int DKS, bool TWO_A, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, const bf16* __restrict__ Qd, int N,
                                                    int H, int Dk, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
-                                                   const float* __restrict__ gy, float* __restrict__ P1,
+                                                   const float* __restrict__ gy, bool cgz, float* __restrict__ P1,
                                                    float* __restrict__ P2) {
     constexpr int M = 64 * MW, NJ = DKS / 16;
     __shared__ __attribute__((aligned(16))) bf16 sh[M * kDqTP], sl[M * kDqTP];                    // ds^T hi, lo
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
                 if (t < tg1) {
                     const size_t o = ((size_t)bh * N + t) * M + m;
                     x[i] = DS[o];
-                    y[i] = C[o] - AL[o] * gy[(size_t)bh * N + t];
+                    y[i] = score_grad_da(C[o], AL[o], gy[(size_t)bh * N + t], cgz);
                 } else {
                     x[i] = y[i] = 0.0f;
                 }
@@ -268,13 +268,14 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
 // Per-chunk terms of the backward's reverse scan (the bf16 MFMA form of
 // bwd_summary in flare_ar_bwd.hip), for chunks c >= 1 of 32 tokens:
 //     a_c[m][:] = sum_t w_tm g_t,   b_c[m] = sum_t w_tm c_tm,
-//     w_tm = 2^(Lpre_m - L_tm) alpha_tm   (Lpre = L at the last token of chunk c-1)
+//     w_tm = 2^(Lpre_m - L_tm) alpha_tm = 2^(Lpre_m - LA_tm)
+// (Lpre = L at the last token of chunk c-1; C holds gz).
 // a is a contraction over tokens: each lane forms its own A operand (latent
-// row m, tokens 8 g .. 8 g + 7) from L, alpha and c as bf16 hi and lo; g^T (dY,
-// exact) is staged transposed in LDS.  b sums the lanes' 8-token parts.
+// row m, tokens 8 g .. 8 g + 7) from LA as bf16 hi and lo; g^T (dY, exact) is
+// staged transposed in LDS.  b sums the lanes' 8-token parts.
 template <int MW, int DV, bool F16>
 __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__ dY, int N, int H,
-                                                        const float* __restrict__ L, const float* __restrict__ AL,
+                                                        const float* __restrict__ L, const float* __restrict__ LA,
                                                         const float* __restrict__ C, float* __restrict__ a_out,
                                                         float* __restrict__ b_out) {
     constexpr int M = 64 * MW, NJ = DV / 16;
@@ -310,9 +311,8 @@ __global__ __launch_bounds__(256) void bwd_summary_mfma(const bf16* __restrict__
             float wv = 0.0f;
             if (t < nt) {
                 const size_t o = rbase + (size_t)t * M + m;
-                const float f = __builtin_amdgcn_exp2f(lp - L[o]);
-                wv = f * AL[o];
-                bsum += f * C[o];
+                wv = __builtin_amdgcn_exp2f(lp - LA[o]);
+                bsum += wv * C[o];
             }
             SPLIT2(bf16, wv, ah[mi][e], alo[mi][e]);
         }
@@ -471,14 +471,14 @@ bool bwd_summary_mfma_supported(int64_t M, int64_t Dv) {
 }
 
 int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
-                        const float* AL, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st) {
+                        const float* LA, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_summary_mfma_supported(M, Dv), "bwd_summary_mfma: unsupported M=%lld Dv=%lld",
                   (long long)M, (long long)Dv);
     dim3 grid((unsigned)((N + 31) / 32), (unsigned)(B * H));
 #define FLARE_SUM_T(MW, DD, F)                                                                              \
     hipLaunchKernelGGL((bwd_summary_mfma<MW, DD, F>), grid, dim3(256), 0, st, (const bf16*)dY, (int)N, (int)H, \
-                       L, AL, C, a_out, b_out)
+                       L, LA, C, a_out, b_out)
 #define FLARE_SUM(MW, DD)                        \
     do {                                         \
         if (f16in) FLARE_SUM_T(MW, DD, true);    \
@@ -503,7 +503,7 @@ bool bwd_dq_mfma_supported(int64_t M, int64_t Dk) {
 // partial sums per group of 512 tokens into P1 (and P2 when sep_k), as bwd_dq_kernel
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
-                   float* P1, float* P2, bool f16in, hipStream_t st) {
+                   bool cgz, float* P1, float* P2, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dq_mfma_supported(M, Dk), "bwd_dq_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
@@ -513,7 +513,7 @@ int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_
     dim3 grid((unsigned)NG, (unsigned)(B * H), (unsigned)(Dk / dks));
 #define FLARE_DQ_T(MW, DKS, TA, TB, TO, F)                                                                     \
     hipLaunchKernelGGL((bwd_dq_mfma<MW, DKS, TA, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)K,         \
-                       (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, P1, P2)
+                       (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, cgz, P1, P2)
 #define FLARE_DQ(MW, DKS, TA, TB, TO)                          \
     do {                                                       \
         if (f16in) FLARE_DQ_T(MW, DKS, TA, TB, TO, true);      \
@@ -547,14 +547,14 @@ bool bwd_dk_mfma_supported(int64_t M, int64_t Dk) {
 // sep_q: dQd is its own output; sep_k: Kd is not Q (Q / Kd as in bwd_dk_kernel)
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
-                   const float* gy, void* dK, void* dQd, bool f16in, hipStream_t st) {
+                   const float* gy, bool cgz, void* dK, void* dQd, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dk_mfma_supported(M, Dk), "bwd_dk_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
     dim3 grid((unsigned)((N + kDkMfmaTok - 1) / kDkMfmaTok), (unsigned)(B * H));
 #define FLARE_DK_T(DD, TB, TO, F)                                                                              \
     hipLaunchKernelGGL((bwd_dk_mfma<DD, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)Q, (const bf16*)Kd,  \
-                       (int)N, (int)H, (int)M, scale, DS, AL, C, gy, (__hip_bfloat16*)dK, (__hip_bfloat16*)dQd)
+                       (int)N, (int)H, (int)M, scale, DS, AL, C, gy, cgz, (__hip_bfloat16*)dK, (__hip_bfloat16*)dQd)
 #define FLARE_DK(DD, TB, TO)                          \
     do {                                              \
         if (f16in) FLARE_DK_T(DD, TB, TO, true);      \

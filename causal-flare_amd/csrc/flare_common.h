@@ -26,6 +26,12 @@ template <> __device__ __forceinline__ __half from_f32<__half>(float x) { return
 
 __device__ __forceinline__ bool is_neg_inf(float x) { return x == kNegInf; }
 
+// da_tm = alpha_tm (gz_tm - gy_t), from the stored C = alpha gz (cgz false) or C = gz
+// (cgz true, the token-causal backward, whose later kernels need no alpha).
+__device__ __forceinline__ float score_grad_da(float c, float al, float gy, bool cgz) {
+    return cgz ? al * (c - gy) : c - al * gy;
+}
+
 // ---------------------------------------------------------------------------
 // Per-chunk replay flags of the MFMA output kernels ([B*H, NC] ints), read by the
 // tokenwise fp32 kernel: 0 leaves the chunk alone, kRedoWhole replays the whole

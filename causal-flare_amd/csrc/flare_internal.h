@@ -121,17 +121,17 @@ constexpr int kBwdGroup = 512;
 bool bwd_dk_mfma_supported(int64_t M, int64_t Dk);
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
-                   const float* gy, void* dK, void* dQd, bool f16in, hipStream_t st);
+                   const float* gy, bool cgz, void* dK, void* dQd, bool f16in, hipStream_t st);
 bool bwd_summary_mfma_supported(int64_t M, int64_t Dv);
 int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
-                        const float* AL, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st);
+                        const float* LA, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st);
 // block sums dz_g, Yb_g of the block-causal backward (M and Dv as bwd_summary_mfma_supported)
 int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, int64_t blk,
                         const float* AL, const float* C, float* X, float* Yb, bool f16in, hipStream_t st);
 bool bwd_dq_mfma_supported(int64_t M, int64_t Dk);
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
-                   float* P1, float* P2, bool f16in, hipStream_t st);
+                   bool cgz, float* P1, float* P2, bool f16in, hipStream_t st);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream,
@@ -148,8 +148,8 @@ int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N
                   hipStream_t stream);
 int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
                         int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                        const float* C, const float* gy, void* dQ, void* dK, void* dQdec, void* dKdec, float* P1,
-                        float* P2, hipStream_t stream);
+                        const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQdec, void* dKdec,
+                        float* P1, float* P2, hipStream_t stream);
 // The token-causal backward (shapes as ar_backward_supported).  power > 0: the
 // stablemax encoder weight s(a) in place of e^a (the decoder stays a softmax).
 bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv);

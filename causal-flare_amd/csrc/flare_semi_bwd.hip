@@ -599,8 +599,8 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
                            (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
     if ((rc = check_launch("semi_bwd_ds_kernel"))) return rc;
     if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, gy, s))) return rc;
-    return launch_bwd_contract(Q, K, Qdec, Kdec, dtype, B, N, H, M, Dk, scale, S, AL, C, gy, dQ, dK, dQd, dKd, P1,
-                               P2, s);
+    return launch_bwd_contract(Q, K, Qdec, Kdec, dtype, B, N, H, M, Dk, scale, S, AL, C, gy, false, dQ, dK, dQd, dKd,
+                               P1, P2, s);
 }
 
 }  // namespace flare
