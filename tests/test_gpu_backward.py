@@ -207,6 +207,23 @@ def test_backward_fp16(M, D, N, sep):
     _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"fp16 M={M} D={D} N={N} sep={sep}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,D,Dv,N", [(48, 32, 96, 200), (64, 64, 256, 150), (32, 64, 32, 100),
+                                      (128, 64, 192, 130)])
+def test_backward_16bit_other_value_widths(dtype, M, D, Dv, N):
+    """16-bit inputs away from the square 64 / 128 heads: the chunk summary on its
+    scalar kernel (M or Dv outside the MFMA instances), GV on the MFMA at Dv = 32 and
+    96, and bwd_dv with eight 64-column value slabs (Dv > 128)."""
+    _case("bwd_16bit_widths", str(dtype), M, D, Dv, N)
+    Q, K, V, Qd, Kd, G = _inputs(23, 1, N, 2, M, D, Dv, dtype, False, False)
+    Q = (Q.float() / math.sqrt(D)).to(dtype)
+    scale = 1.0 / math.sqrt(D)
+    y, grads = _run(Q, K, V, Qd, Kd, G, scale)
+    assert y.dtype == dtype and all(g is None or g.dtype == dtype for g in grads)
+    tol = 3e-2 if max(D, Dv) >= 128 else 2e-2
+    _check(grads, O.ar_grads(Q, K, V, G, scale, Qd, Kd), tol, f"{dtype} M={M} D={D} Dv={Dv} N={N}")
+
+
 def test_backward_c_abi_rejects_bad_arguments():
     from causal_flare import _lib
     lib = _lib.lib()
