@@ -911,7 +911,9 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 //                  + sum_{t >= tau} e^{s_tau m - L_tm} alpha_tm GV[t][tau]
 //                  - e^{s_tau m - L_tau m} R_tau m,
 // R_tau = sum_{t >= tau} e^{L_tau - L_t} c_t = c_tau + e^{L_tau - L_tau+1} R_tau+1,
-// c_t = alpha_t gz_t = 2^(L_t - LA_t) gz_t (C holds gz), written over s.  Thread m.  The first and last terms are formed in one
+// c_t = alpha_t gz_t = 2^(L_t - LA_t) gz_t (C holds gz), written over s.  dsum (shared
+// weights, softmax encoder): da_tau m = alpha (gz - gy_tau) is added, so that the
+// contractions read ds + da from one array.  Thread m.  The first and last terms are formed in one
 // reverse pass over the chunk and kept in registers, with the chunk's scores; the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
 // runs per tau over 16-token blocks of t as in bwd_gz.  power > 0 (stablemax,
 // s2 = log2 s(a)): the gradient with respect to a is the one with respect to
@@ -921,7 +923,8 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     const T* __restrict__ V, const T* __restrict__ dY, int N, int H, int M, int Dv, float* __restrict__ S,
     float* __restrict__ L, const float* __restrict__ LA, const float* __restrict__ C,
-    const float* __restrict__ X, const float* __restrict__ Ysum, float power) {
+    const float* __restrict__ X, const float* __restrict__ Ysum, float power, const float* __restrict__ gy,
+    bool dsum) {
     __shared__ __attribute__((aligned(16))) float gvt[kBT * kGT];
     // dY and V slabs; afterwards (bf16) v_t . X_m of one 16-token half as [m][17]
     __shared__ __attribute__((aligned(16))) float gsv[2 * kBT * kGT];
@@ -1012,11 +1015,12 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
     for (int t = kBT - 1; t >= 0; --t) {
         if (t < nt) {
             const size_t o = (size_t)t * M;
-            const float l = lcol[o], s = sv[t];
-            R = ex2(l - la[t]) * ccol[o] + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
+            const float l = lcol[o], s = sv[t], al = ex2(l - la[t]), gzt = ccol[o];
+            R = al * gzt + (t + 1 < nt ? ex2(l - lnext) * R : 0.0f);
             lnext = l;
             float park = -ex2(s - l) * R;
             if (carry) park += ex2(s - lend) * (acc[t] - ysum);
+            if (dsum) park += al * (gzt - gy[(size_t)bh * N + t0 + t]);
             acc[t] = park;
         }
     }
@@ -1055,7 +1059,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
 // ---------------------------------------------------------------------------
 // bwd_dk: per token, dK_t = scale sum_m (ds_tm Q_m [+ da_tm Kd_m when Qd = K])
 // and dQd_t = scale sum_m da_tm Kd_m (separate Qd); da_tm = alpha_tm (gz_tm - gy_t)
-// (score_grad_da).
+// (score_grad_da).  dsum (shared weights only): DS already holds ds + da.
 // Thread (col, tg) owns tokens tg + 4 r (r < kDkTok / 4) and columns col + 64 k.
 // ---------------------------------------------------------------------------
 constexpr int kDkTok = 32;     // tokens per bwd_dk workgroup
@@ -1064,7 +1068,7 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
     const T* __restrict__ Q, const T* __restrict__ Kd, int N, int H, int M, int Dk, float scale, bool sep_q,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
-    const float* __restrict__ gy, bool cgz, T* __restrict__ dK, T* __restrict__ dQd) {
+    const float* __restrict__ gy, bool cgz, bool dsum, T* __restrict__ dK, T* __restrict__ dQd) {
     __shared__ __attribute__((aligned(16))) float dsl[kDkTok * 256];
     __shared__ __attribute__((aligned(16))) float dal[kDkTok * 256];
     const int bh = blockIdx.y, b = bh / H, h = bh % H, tid = threadIdx.x;
@@ -1074,7 +1078,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dk_kernel(
         const int i = e / M;
         const bool ok = i < nt;
         dsl[e] = ok ? DS[rbase + e] : 0.0f;
-        dal[e] = ok ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
+        dal[e] = ok && !dsum ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
     }
     __syncthreads();
     const int col = tid & 63, tg = tid >> 6;
@@ -1125,7 +1129,7 @@ template <typename T>
 __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
     const T* __restrict__ K, const T* __restrict__ Qd, int N, int H, int M, int Dk, bool sep_k,
     const float* __restrict__ DS, const float* __restrict__ AL, const float* __restrict__ C,
-    const float* __restrict__ gy, bool cgz, float* __restrict__ P1, float* __restrict__ P2) {
+    const float* __restrict__ gy, bool cgz, bool dsum, float* __restrict__ P1, float* __restrict__ P2) {
     __shared__ __attribute__((aligned(16))) float dsl[kBTok * 256];
     __shared__ __attribute__((aligned(16))) float dal[kBTok * 256];
     __shared__ __attribute__((aligned(16))) float kt[kBTok * kGT];
@@ -1148,7 +1152,7 @@ __global__ __launch_bounds__(kBNT) void bwd_dq_kernel(
             const int i = e / M;
             const bool ok = i < nt;
             dsl[e] = ok ? DS[rbase + e] : 0.0f;
-            dal[e] = ok ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
+            dal[e] = ok && !dsum ? score_grad_da(C[rbase + e], AL[rbase + e], gy[(size_t)bh * N + t0 + i], cgz) : 0.0f;
         }
         for (int e = tid; e < kBTok * 64; e += kBNT) {
             const int i = e >> 6, dd = e & 63, d = d0 + dd;
@@ -1202,26 +1206,26 @@ __global__ __launch_bounds__(256) void bwd_reduce_kernel(const float* __restrict
 template <typename T>
 static int launch_contract(const T* q, const T* k, const T* qd, const T* kd, bool sep_q, bool sep_k, int64_t B,
                            int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                           const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQd, void* dKd,
-                           float* P1, float* P2, hipStream_t st) {
+                           const float* C, const float* gy, bool cgz, bool dsum, void* dQ, void* dK, void* dQd,
+                           void* dKd, float* P1, float* P2, hipStream_t st) {
     const int64_t BH = B * H, NG = (N + kBGroup - 1) / kBGroup;
     int rc;
     constexpr bool kHalf = std::is_same<T, __half>::value;
     constexpr bool k16 = std::is_same<T, __hip_bfloat16>::value || kHalf;
     if (k16 && bwd_dk_mfma_supported(M, Dk)) {
-        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dK, dQd, kHalf, st)))
+        if ((rc = launch_dk_mfma(q, kd, sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dsum, dK, dQd, kHalf, st)))
             return rc;
     } else {
         hipLaunchKernelGGL(bwd_dk_kernel<T>, dim3((unsigned)((N + kDkTok - 1) / kDkTok), (unsigned)BH), dim3(kBNT),
                            0, st, q, kd, (int)N, (int)H, (int)M, (int)Dk, scale, sep_q, DS, AL, C, gy,
-                           cgz, static_cast<T*>(dK), static_cast<T*>(dQd));
+                           cgz, dsum, static_cast<T*>(dK), static_cast<T*>(dQd));
         if ((rc = check_launch("bwd_dk_kernel"))) return rc;
     }
     if (k16 && bwd_dq_mfma_supported(M, Dk)) {
-        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, cgz, P1, P2, kHalf, st))) return rc;
+        if ((rc = launch_dq_mfma(k, qd, sep_q, sep_k, B, N, H, M, Dk, DS, AL, C, gy, cgz, dsum, P1, P2, kHalf, st))) return rc;
     } else {
         hipLaunchKernelGGL(bwd_dq_kernel<T>, dim3((unsigned)NG, (unsigned)BH, (unsigned)((Dk + 63) / 64)),
-                           dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, cgz, P1, P2);
+                           dim3(kBNT), 0, st, k, qd, (int)N, (int)H, (int)M, (int)Dk, sep_k, DS, AL, C, gy, cgz, dsum, P1, P2);
         if ((rc = check_launch("bwd_dq_kernel"))) return rc;
     }
     const int64_t red = H * M * Dk;
@@ -1271,7 +1275,8 @@ int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const vo
     const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
 #define FLARE_CONTRACT(TY)                                                                                       \
     return launch_contract((const TY*)Q, (const TY*)K, (const TY*)(sep_q ? Qdec : K), (const TY*)(sep_k ? Kdec : Q), \
-                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dQ, dK, dQdec, dKdec, P1, P2, st)
+                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, false, dQ, dK, dQdec, dKdec, P1, \
+                           P2, st)
     if (dtype == FLARE_BF16) FLARE_CONTRACT(__hip_bfloat16);
     if (dtype == FLARE_F16) FLARE_CONTRACT(__half);
     FLARE_CONTRACT(float);
@@ -1408,11 +1413,14 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     auto* dv_kernel = Dv <= 2 * kBSlab ? bwd_dv_kernel<T, 2> : bwd_dv_kernel<T, kMaxVSlab>;
     hipLaunchKernelGGL(dv_kernel, gc, dim3(kBNT), 0, st, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
+    // shared weights with the softmax encoder: bwd_ds adds da to ds, and the contractions
+    // read that one array (not C, alpha and gy)
+    const bool dsum = !sep_q && !sep_k && power == 0.0f;
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
-                       C, pn, pd, power);
+                       C, pn, pd, power, gy, dsum);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
-    return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, true, dQ, dK, dQd, dKd,
-                           P1, P2, st);
+    return launch_contract(q, k, qd, kd, sep_q, sep_k, B, N, H, M, Dk, scale, S, AL, C, gy, true, dsum, dQ, dK, dQd,
+                           dKd, P1, P2, st);
 }
 
 bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv) {

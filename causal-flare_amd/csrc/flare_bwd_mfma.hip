@@ -1,7 +1,8 @@
 // flare_bwd_mfma.hip -- bf16 MFMA contractions of the FLARE backward on gfx950.
 //
 // dK (and dQ_dec) are contractions over the latent bank of the score gradients
-// ds and da = alpha (gz - gy) (fp32, [B*H, N, M]; C holds alpha gz or gz, see score_grad_da) with the bf16 latent tensors:
+// ds and da = alpha (gz - gy) (fp32, [B*H, N, M]; C holds alpha gz or gz, see score_grad_da;
+// dsum: DS already holds ds + da, for the shared-weight instances, which read no C or alpha) with the bf16 latent tensors:
 //     dK_t   = scale sum_m (ds_tm Q_m  [+ da_tm Kd_m when Qd = K])
 //     dQd_t  = scale sum_m  da_tm Kd_m                  (separate Qd)
 // (the per-token loop of bwd_dk in flare_ar_bwd.hip, which stays the fp32 /
@@ -31,7 +32,8 @@ template <int DK, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, const bf16* __restrict__ Kd, int N,
                                                    int H, int M, float scale, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
-                                                   const float* __restrict__ gy, bool cgz, __hip_bfloat16* __restrict__ dK,
+                                                   const float* __restrict__ gy, bool cgz, bool dsum,
+                                                   __hip_bfloat16* __restrict__ dK,
                                                    __hip_bfloat16* __restrict__ dQd) {
     constexpr int NJ = DK / 16;
     __shared__ __attribute__((aligned(16))) bf16 qt[DK * kDkLP];                 // Q^T[d][m]
@@ -81,14 +83,20 @@ __global__ __launch_bounds__(256) void bwd_dk_mfma(const bf16* __restrict__ Q, c
             if (t < N) {
                 const size_t o = ((size_t)bh * N + t) * M + m0 + 8 * g;
                 const f32x4 s0 = *reinterpret_cast<const f32x4*>(DS + o), s1 = *reinterpret_cast<const f32x4*>(DS + o + 4);
-                const f32x4 c0 = *reinterpret_cast<const f32x4*>(C + o), c1 = *reinterpret_cast<const f32x4*>(C + o + 4);
-                const f32x4 a0 = *reinterpret_cast<const f32x4*>(AL + o), a1 = *reinterpret_cast<const f32x4*>(AL + o + 4);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     ds[e] = s0[e];
                     ds[4 + e] = s1[e];
-                    da[e] = score_grad_da(c0[e], a0[e], gyt[ti], cgz);
-                    da[4 + e] = score_grad_da(c1[e], a1[e], gyt[ti], cgz);
+                    da[e] = da[4 + e] = 0.0f;
+                }
+                if (!(dsum && !TWO_B && !TWO_OUT)) {
+                    const f32x4 c0 = *reinterpret_cast<const f32x4*>(C + o), c1 = *reinterpret_cast<const f32x4*>(C + o + 4);
+                    const f32x4 a0 = *reinterpret_cast<const f32x4*>(AL + o), a1 = *reinterpret_cast<const f32x4*>(AL + o + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        da[e] = score_grad_da(c0[e], a0[e], gyt[ti], cgz);
+                        da[4 + e] = score_grad_da(c1[e], a1[e], gyt[ti], cgz);
+                    }
                 }
             } else {
 #pragma unroll
@@ -156,7 +164,8 @@ template <int MW, int DKS, bool TWO_A, bool TWO_B, bool TWO_OUT, bool F16>
 __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, const bf16* __restrict__ Qd, int N,
                                                    int H, int Dk, const float* __restrict__ DS,
                                                    const float* __restrict__ AL, const float* __restrict__ C,
-                                                   const float* __restrict__ gy, bool cgz, float* __restrict__ P1,
+                                                   const float* __restrict__ gy, bool cgz, bool dsum,
+                                                   float* __restrict__ P1,
                                                    float* __restrict__ P2) {
     constexpr int M = 64 * MW, NJ = DKS / 16;
     __shared__ __attribute__((aligned(16))) bf16 sh[M * kDqTP], sl[M * kDqTP];                    // ds^T hi, lo
@@ -190,7 +199,7 @@ __global__ __launch_bounds__(256) void bwd_dq_mfma(const bf16* __restrict__ K, c
                 if (t < tg1) {
                     const size_t o = ((size_t)bh * N + t) * M + m;
                     x[i] = DS[o];
-                    y[i] = score_grad_da(C[o], AL[o], gy[(size_t)bh * N + t], cgz);
+                    y[i] = (dsum && !TWO_A) ? 0.0f : score_grad_da(C[o], AL[o], gy[(size_t)bh * N + t], cgz);
                 } else {
                     x[i] = y[i] = 0.0f;
                 }
@@ -503,7 +512,7 @@ bool bwd_dq_mfma_supported(int64_t M, int64_t Dk) {
 // partial sums per group of 512 tokens into P1 (and P2 when sep_k), as bwd_dq_kernel
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
-                   bool cgz, float* P1, float* P2, bool f16in, hipStream_t st) {
+                   bool cgz, bool dsum, float* P1, float* P2, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dq_mfma_supported(M, Dk), "bwd_dq_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
@@ -513,7 +522,7 @@ int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_
     dim3 grid((unsigned)NG, (unsigned)(B * H), (unsigned)(Dk / dks));
 #define FLARE_DQ_T(MW, DKS, TA, TB, TO, F)                                                                     \
     hipLaunchKernelGGL((bwd_dq_mfma<MW, DKS, TA, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)K,         \
-                       (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, cgz, P1, P2)
+                       (const bf16*)Qd, (int)N, (int)H, (int)Dk, DS, AL, C, gy, cgz, dsum, P1, P2)
 #define FLARE_DQ(MW, DKS, TA, TB, TO)                          \
     do {                                                       \
         if (f16in) FLARE_DQ_T(MW, DKS, TA, TB, TO, true);      \
@@ -547,14 +556,14 @@ bool bwd_dk_mfma_supported(int64_t M, int64_t Dk) {
 // sep_q: dQd is its own output; sep_k: Kd is not Q (Q / Kd as in bwd_dk_kernel)
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
-                   const float* gy, bool cgz, void* dK, void* dQd, bool f16in, hipStream_t st) {
+                   const float* gy, bool cgz, bool dsum, void* dK, void* dQd, bool f16in, hipStream_t st) {
     using namespace mfma;
     FLARE_REQUIRE(bwd_dk_mfma_supported(M, Dk), "bwd_dk_mfma: unsupported M=%lld Dk=%lld", (long long)M,
                   (long long)Dk);
     dim3 grid((unsigned)((N + kDkMfmaTok - 1) / kDkMfmaTok), (unsigned)(B * H));
 #define FLARE_DK_T(DD, TB, TO, F)                                                                              \
     hipLaunchKernelGGL((bwd_dk_mfma<DD, TB, TO, F>), grid, dim3(256), 0, st, (const bf16*)Q, (const bf16*)Kd,  \
-                       (int)N, (int)H, (int)M, scale, DS, AL, C, gy, cgz, (__hip_bfloat16*)dK, (__hip_bfloat16*)dQd)
+                       (int)N, (int)H, (int)M, scale, DS, AL, C, gy, cgz, dsum, (__hip_bfloat16*)dK, (__hip_bfloat16*)dQd)
 #define FLARE_DK(DD, TB, TO)                          \
     do {                                              \
         if (f16in) FLARE_DK_T(DD, TB, TO, true);      \

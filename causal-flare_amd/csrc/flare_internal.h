@@ -121,7 +121,7 @@ constexpr int kBwdGroup = 512;
 bool bwd_dk_mfma_supported(int64_t M, int64_t Dk);
 int launch_dk_mfma(const void* Q, const void* Kd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, float scale, const float* DS, const float* AL, const float* C,
-                   const float* gy, bool cgz, void* dK, void* dQd, bool f16in, hipStream_t st);
+                   const float* gy, bool cgz, bool dsum, void* dK, void* dQd, bool f16in, hipStream_t st);
 bool bwd_summary_mfma_supported(int64_t M, int64_t Dv);
 int launch_summary_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t M, int64_t Dv, const float* L,
                         const float* LA, const float* C, float* a_out, float* b_out, bool f16in, hipStream_t st);
@@ -131,7 +131,7 @@ int launch_semi_dz_mfma(const void* dY, int64_t B, int64_t N, int64_t H, int64_t
 bool bwd_dq_mfma_supported(int64_t M, int64_t Dk);
 int launch_dq_mfma(const void* K, const void* Qd, bool sep_q, bool sep_k, int64_t B, int64_t N, int64_t H,
                    int64_t M, int64_t Dk, const float* DS, const float* AL, const float* C, const float* gy,
-                   bool cgz, float* P1, float* P2, bool f16in, hipStream_t st);
+                   bool cgz, bool dsum, float* P1, float* P2, bool f16in, hipStream_t st);
 int launch_prepare_public(const void* Q, const void* K, const void* V, int dtype, int64_t B,
                           int64_t N, int64_t H, int64_t M, int64_t Dk, int64_t Dv, float scale,
                           int64_t chunk, float* cmax, float* cden, float* cnum, hipStream_t stream,
