@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kBNT) void bwd_stats_kernel(
                 if (i < ni) {
                     const size_t o = ((size_t)bh * N + t0 + i0 + i) * M + m;
                     const float la = at[i * M + m] - lse[i];     // log alpha
-                    AL[o] = __expf(la);
+                    if (AL != nullptr) AL[o] = __expf(la);
                     LA[o] = lv[i] - la * kBLog2e;
                 }
             }
@@ -1381,16 +1381,21 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
             return rc;
     }
     const dim3 gc((unsigned)NC, (unsigned)BH);
+    // shared weights with the softmax encoder: bwd_ds adds da to ds, and the contractions
+    // read that one array (not C, alpha and gy); alpha is then read by no kernel and not
+    // written
+    const bool dsum = !sep_q && !sep_k && power == 0.0f;
+    float* const ALw = dsum ? nullptr : AL;
     bool stats_mfma = false;
     if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
         stats_mfma = M % 16 == 0 && Dk % 32 == 0;
         if (stats_mfma)
             hipLaunchKernelGGL((bwd_stats_kernel<T, true>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H,
-                               (int)M, (int)Dk, scale, shared, pm, pd, S, L, AL, LA, power);
+                               (int)M, (int)Dk, scale, shared, pm, pd, S, L, ALw, LA, power);
     }
     if (!stats_mfma)
         hipLaunchKernelGGL((bwd_stats_kernel<T, false>), gc, dim3(kBNT), 0, st, q, k, qd, kd, (int)N, (int)H, (int)M,
-                           (int)Dk, scale, shared, pm, pd, S, L, AL, LA, power);
+                           (int)Dk, scale, shared, pm, pd, S, L, ALw, LA, power);
     if ((rc = check_launch("bwd_stats_kernel"))) return rc;
     hipLaunchKernelGGL(bwd_gz_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, pm, pn, S,
                        L, C);
@@ -1413,9 +1418,6 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
     auto* dv_kernel = Dv <= 2 * kBSlab ? bwd_dv_kernel<T, 2> : bwd_dv_kernel<T, kMaxVSlab>;
     hipLaunchKernelGGL(dv_kernel, gc, dim3(kBNT), 0, st, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA, pn, static_cast<T*>(dV));
     if ((rc = check_launch("bwd_dv_kernel"))) return rc;
-    // shared weights with the softmax encoder: bwd_ds adds da to ds, and the contractions
-    // read that one array (not C, alpha and gy)
-    const bool dsum = !sep_q && !sep_k && power == 0.0f;
     hipLaunchKernelGGL(bwd_ds_kernel<T>, gc, dim3(kBNT), 0, st, v, dy, (int)N, (int)H, (int)M, (int)Dv, S, L, LA,
                        C, pn, pd, power, gy, dsum);
     if ((rc = check_launch("bwd_ds_kernel"))) return rc;
