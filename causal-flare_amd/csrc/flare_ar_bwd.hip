@@ -1270,12 +1270,12 @@ int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N
 
 int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
                         int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                        const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQdec, void* dKdec,
-                        float* P1, float* P2, hipStream_t st) {
+                        const float* C, const float* gy, bool cgz, bool dsum, void* dQ, void* dK, void* dQdec,
+                        void* dKdec, float* P1, float* P2, hipStream_t st) {
     const bool sep_q = Qdec != nullptr, sep_k = Kdec != nullptr;
 #define FLARE_CONTRACT(TY)                                                                                       \
     return launch_contract((const TY*)Q, (const TY*)K, (const TY*)(sep_q ? Qdec : K), (const TY*)(sep_k ? Kdec : Q), \
-                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, false, dQ, dK, dQdec, dKdec, P1, \
+                           sep_q, sep_k, B, N, H, M, Dk, scale, DS, AL, C, gy, cgz, dsum, dQ, dK, dQdec, dKdec, P1, \
                            P2, st)
     if (dtype == FLARE_BF16) FLARE_CONTRACT(__hip_bfloat16);
     if (dtype == FLARE_F16) FLARE_CONTRACT(__half);

@@ -148,8 +148,8 @@ int launch_bwd_gy(const void* dY, const void* Y, int dtype, int64_t B, int64_t N
                   hipStream_t stream);
 int launch_bwd_contract(const void* Q, const void* K, const void* Qdec, const void* Kdec, int dtype, int64_t B,
                         int64_t N, int64_t H, int64_t M, int64_t Dk, float scale, const float* DS, const float* AL,
-                        const float* C, const float* gy, bool cgz, void* dQ, void* dK, void* dQdec, void* dKdec,
-                        float* P1, float* P2, hipStream_t stream);
+                        const float* C, const float* gy, bool cgz, bool dsum, void* dQ, void* dK, void* dQdec,
+                        void* dKdec, float* P1, float* P2, hipStream_t stream);
 // The token-causal backward (shapes as ar_backward_supported).  power > 0: the
 // stablemax encoder weight s(a) in place of e^a (the decoder stays a softmax).
 bool ar_backward_supported(int64_t M, int64_t Dk, int64_t Dv);

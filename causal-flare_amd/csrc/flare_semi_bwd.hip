@@ -431,7 +431,9 @@ template <typename T, bool MF>
 __global__ __launch_bounds__(kSNT) void semi_bwd_ds_kernel(const T* __restrict__ V, int N, int H, int M, int Dv,
                                                            int blk, int NB, float* __restrict__ S, BlockStates st,
                                                            const float* __restrict__ X,
-                                                           const float* __restrict__ Yb) {
+                                                           const float* __restrict__ Yb, const float* __restrict__ AL,
+                                                           const float* __restrict__ C, const float* __restrict__ gy,
+                                                           bool dsum) {
     __shared__ __attribute__((aligned(16))) float vt[kSTok * 512];
     const int g = blockIdx.x, bh = blockIdx.y;
     const int b = bh / H, h = bh % H, tid = threadIdx.x, m = tid;
@@ -489,7 +491,8 @@ __global__ __launch_bounds__(kSNT) void semi_bwd_ds_kernel(const T* __restrict__
         for (int i = 0; i < kSTok; ++i) {
             if (i < ni) {
                 const size_t o = ((size_t)bh * N + tb0 + i0 + i) * M + m;
-                S[o] = sexp2(S[o] - lgm) * (vx[i] - ym);
+                const float da = dsum ? C[o] - AL[o] * gy[(size_t)bh * N + tb0 + i0 + i] : 0.0f;
+                S[o] = sexp2(S[o] - lgm) * (vx[i] - ym) + da;
             }
         }
     }
@@ -587,20 +590,23 @@ static int run_semi_backward(const void* Q, const void* K, const void* V, const 
         hipLaunchKernelGGL((semi_bwd_dv_kernel<T, false>), gdv, dim3(kSNT), 0, s, (int)N, (int)H, (int)M, (int)Dv,
                            (int)block, (int)NB, S, st, X, static_cast<T*>(dV));
     if ((rc = check_launch("semi_bwd_dv_kernel"))) return rc;
+    // shared weights: semi_bwd_ds adds da = c - alpha gy to ds, and the contractions read
+    // that one array (not C, alpha and gy)
+    const bool dsum = shared;
+    if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, gy, s))) return rc;
     bool ds_mfma = false;
     if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
         ds_mfma = M % 16 == 0 && Dv % 32 == 0;
         if (ds_mfma)
             hipLaunchKernelGGL((semi_bwd_ds_kernel<T, true>), gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N,
-                               (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
+                               (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb, AL, C, gy, dsum);
     }
     if (!ds_mfma)
         hipLaunchKernelGGL((semi_bwd_ds_kernel<T, false>), gb, dim3(kSNT), 0, s, static_cast<const T*>(V), (int)N,
-                           (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb);
+                           (int)H, (int)M, (int)Dv, (int)block, (int)NB, S, st, X, Yb, AL, C, gy, dsum);
     if ((rc = check_launch("semi_bwd_ds_kernel"))) return rc;
-    if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, gy, s))) return rc;
-    return launch_bwd_contract(Q, K, Qdec, Kdec, dtype, B, N, H, M, Dk, scale, S, AL, C, gy, false, dQ, dK, dQd, dKd,
-                               P1, P2, s);
+    return launch_bwd_contract(Q, K, Qdec, Kdec, dtype, B, N, H, M, Dk, scale, S, AL, C, gy, false, dsum, dQ, dK, dQd,
+                               dKd, P1, P2, s);
 }
 
 }  // namespace flare

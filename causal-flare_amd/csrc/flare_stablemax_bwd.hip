@@ -424,7 +424,7 @@ static int run_stablemax_backward(const void* Q, const void* K, const void* V, c
     if ((rc = check_launch("stablemax_bwd_tokens"))) return rc;
     if ((rc = launch_bwd_gy(dY, Y, dtype, B, N, H, Dv, F(lay.off_gy), st))) return rc;
     return launch_bwd_contract(Q, K, Qd, Kd, dtype, B, N, H, M, Dk, scale, F(lay.off_ds), F(lay.off_al),
-                               F(lay.off_c), F(lay.off_gy), false, dQ, dK, dQd, dKd, F(lay.off_p1), F(lay.off_p2), st);
+                               F(lay.off_c), F(lay.off_gy), false, false, dQ, dK, dQd, dKd, F(lay.off_p1), F(lay.off_p2), st);
 }
 
 }  // namespace flare
