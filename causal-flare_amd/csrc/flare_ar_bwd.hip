@@ -912,8 +912,8 @@ __global__ __launch_bounds__(kBNT) void bwd_dv_kernel(
 //                  - e^{s_tau m - L_tau m} R_tau m,
 // R_tau = sum_{t >= tau} e^{L_tau - L_t} c_t = c_tau + e^{L_tau - L_tau+1} R_tau+1,
 // c_t = alpha_t gz_t = 2^(L_t - LA_t) gz_t (C holds gz), written over s.  dsum (shared
-// weights, softmax encoder): da_tau m = alpha (gz - gy_tau) is added, so that the
-// contractions read ds + da from one array.  Thread m.  The first and last terms are formed in one
+// weights): da_tau m = alpha (gz - gy_tau) is added (after the stablemax factor, which
+// belongs to ds alone), so that the contractions read ds + da from one array.  Thread m.  The first and last terms are formed in one
 // reverse pass over the chunk and kept in registers, with the chunk's scores; the pair sum, exp2(s2_tau - LA_t) GV[t][tau],
 // runs per tau over 16-token blocks of t as in bwd_gz.  power > 0 (stablemax,
 // s2 = log2 s(a)): the gradient with respect to a is the one with respect to
@@ -1020,7 +1020,7 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
             lnext = l;
             float park = -ex2(s - l) * R;
             if (carry) park += ex2(s - lend) * (acc[t] - ysum);
-            if (dsum) park += al * (gzt - gy[(size_t)bh * N + t0 + t]);
+            if (dsum && power == 0.0f) park += al * (gzt - gy[(size_t)bh * N + t0 + t]);
             acc[t] = park;
         }
     }
@@ -1052,7 +1052,12 @@ __global__ __launch_bounds__(kBNT) void bwd_ds_kernel(
         }
         const size_t o = (size_t)tau * M;
         const float dlog = acc[tau] + sum;
-        scol[o] = power > 0.0f ? dlog * (power * ex2(-fabsf(s) / power)) : dlog;
+        float dsv = dlog;
+        if (power > 0.0f) {
+            dsv = dlog * (power * ex2(-fabsf(s) / power));
+            if (dsum) dsv += ex2(lcol[o] - la[tau]) * (ccol[o] - gy[(size_t)bh * N + t0 + tau]);
+        }
+        scol[o] = dsv;
     }
 }
 
@@ -1381,10 +1386,9 @@ static int run_backward(const void* Q, const void* K, const void* V, const void*
             return rc;
     }
     const dim3 gc((unsigned)NC, (unsigned)BH);
-    // shared weights with the softmax encoder: bwd_ds adds da to ds, and the contractions
-    // read that one array (not C, alpha and gy); alpha is then read by no kernel and not
-    // written
-    const bool dsum = !sep_q && !sep_k && power == 0.0f;
+    // shared weights: bwd_ds adds da to ds, and the contractions read that one array (not
+    // C, alpha and gy); alpha is then read by no kernel and not written
+    const bool dsum = !sep_q && !sep_k;
     float* const ALw = dsum ? nullptr : AL;
     bool stats_mfma = false;
     if constexpr (std::is_same<T, __hip_bfloat16>::value || std::is_same<T, __half>::value) {
